@@ -1,0 +1,370 @@
+#!/usr/bin/env python3
+"""Benchmark of SPECTRA's W4A16 linear hot path on one MI355X.
+
+Headline workload: the full SPECTRA linear at M=1 on
+Llama-3.2-3B shapes -- fused QKV (K=3072, N=5120) and down_proj (K=8192, N=3072),
+fp16 activations N(0,1) rotated by a blockwise FWHT-128, NF4 block-64 weights with
+fp16 absmax, 0.5% fp16 CSR outliers of magnitude |N(0,0.2)|, seeded CPU generators.
+
+One step = one QKV GEMV + one down_proj GEMV.  Weight copies rotate over a pool
+larger than the 256 MB Infinity Cache so every launch streams from HBM; the K timed
+steps are captured in one HIP graph (as the reference's engine captures its decode
+step, engine.py:1813-1830) and replayed between synchronizations.
+
+value = algorithmic bytes per step / time per step (GB/s); bytes are the stored
+operand bytes (packed + absmax + CSR) + x + y of both launches.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from spectra_amd import _lib as L  # noqa: E402
+from spectra_amd import compressor as C  # noqa: E402
+from spectra_amd import kernels as K  # noqa: E402
+
+METRIC = "W4A16 GEMV HBM GB/s (% of 8 TB/s peak) at M=1; decode tok/s, 3B-shape"
+PEAK_HBM_GBS = 8000.0
+PEAK_FP16_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
+HAD = 128
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# synthetic Format B weights (seeded on the CPU: identical on every box)
+# ---------------------------------------------------------------------------
+def synth_nf4(n: int, k: int, seed: int, ratio: float = 0.005, dev="cuda") -> C.NF4Weight:
+    gw = torch.Generator().manual_seed(seed + 1)
+    w = (torch.randn(n, k, generator=gw) * 0.02).half()
+    mask = None
+    if ratio > 0:
+        nnz = int(round(ratio * n * k))
+        pos = torch.randperm(n * k, generator=torch.Generator().manual_seed(seed + 2))[:nnz]
+        gv = torch.Generator().manual_seed(seed + 3)
+        mag = torch.randn(nnz, generator=gv).abs() * 0.2
+        sign = torch.where(torch.rand(nnz, generator=gv) < 0.5, -1.0, 1.0)
+        w.view(-1)[pos] = (mag * sign).half()
+        mask = torch.zeros(n * k, dtype=torch.bool)
+        mask[pos] = True
+        mask = mask.view(n, k).to(dev)
+    # the synthetic matrix is taken as already stored in the rotated basis
+    q = C.quantize_nf4(w.to(dev), 64, 0, mask, True)
+    q.hadamard_block = HAD
+    return q
+
+
+def synth_nf4_gpu(n: int, k: int, seed: int, ratio: float = 0.005) -> C.NF4Weight:
+    """Same distribution drawn with the GPU generator (for the 394M-weight lm_head)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+    mask = torch.rand(n, k, generator=g, device="cuda") < ratio
+    mag = (torch.randn(n, k, generator=g, device="cuda").abs() * 0.2).half()
+    w = torch.where(mask, torch.where(torch.rand(n, k, generator=g, device="cuda") < 0.5, -mag, mag), w)
+    q = C.quantize_nf4(w, 64, 0, mask, True)
+    q.hadamard_block = HAD
+    return q
+
+
+def clone_nf4(q: C.NF4Weight) -> C.NF4Weight:
+    return C.NF4Weight(q.packed.clone(), q.absmax.clone(), q.rowptr.clone(), q.col.clone(), q.val.clone(), q.k,
+                       q.blocksize, q.hadamard_block, q.marlin_layout)
+
+
+def operands(q: C.NF4Weight) -> K.QWeightOperands:
+    col, val = q.outliers()
+    return K.QWeightOperands(q.packed, q.absmax, None, q.k, codebook="nf4", group_size=q.blocksize,
+                             hadamard_block=q.hadamard_block, marlin_layout=q.marlin_layout, outlier_idx=col,
+                             outlier_w=val, outlier_rowptr=q.rowptr if col is not None else None)
+
+
+def gemv_bytes(q: C.NF4Weight, m: int = 1) -> int:
+    return q.nbytes() + m * q.k * 2 + m * q.n * 2
+
+
+class Launcher:
+    """Pre-bound linear call (descriptor, x, out[, workspace]) -> one ctypes call each.
+    m <= GEMV_MAX_M uses the GEMV family, larger m the MFMA GEMM."""
+
+    def __init__(self, lib, ops: K.QWeightOperands, x: torch.Tensor, out: torch.Tensor):
+        m = x.shape[0]
+        self.ops = ops
+        if m <= K.GEMV_MAX_M:
+            self.name, self.fn = "spectra_w4a16_gemv", lib.spectra_w4a16_gemv
+            self.args = (ctypes.byref(ops.desc), x.data_ptr(), x.stride(0), m, L.F16, out.data_ptr(), out.stride(0))
+        else:
+            ws = lib.spectra_w4a16_gemm_workspace(ctypes.byref(ops.desc), m, L.F16)
+            self.ws = torch.empty(int(ws), dtype=torch.uint8, device=x.device)
+            self.name, self.fn = "spectra_w4a16_gemm", lib.spectra_w4a16_gemm
+            self.args = (ctypes.byref(ops.desc), x.data_ptr(), x.stride(0), m, L.F16, out.data_ptr(), out.stride(0),
+                         self.ws.data_ptr(), self.ws.numel())
+
+    def __call__(self, stream: int) -> None:
+        st = self.fn(*self.args, stream)
+        if st != L.OK:
+            L.check(self.name, st)
+
+
+def graph_of(calls, reps: int = 1) -> torch.cuda.CUDAGraph:
+    for c in calls[: min(len(calls), 4)]:
+        c(torch.cuda.current_stream().cuda_stream)  # eager warm-up before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s = torch.cuda.current_stream().cuda_stream
+        for _ in range(reps):
+            for c in calls:
+                c(s)
+    return g
+
+
+def time_graph(g: torch.cuda.CUDAGraph, iters: int = 3) -> float:
+    """Median seconds of one replay, measured with events on the replay stream."""
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) / 1e3)
+    return float(np.median(ts))
+
+
+def pool_copies(bytes_per_copy: int, pool_bytes: float) -> int:
+    return max(2, int(math.ceil(pool_bytes / bytes_per_copy)))
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: the oracle (numpy restatement of the reference dequant + matmul)
+# ---------------------------------------------------------------------------
+def cpu_baseline(qs, xs, budget_s: float = 15.0):
+    import oracle as O
+    from threadpoolctl import threadpool_limits
+
+    hq = [(q.packed.cpu().numpy(), q.absmax.cpu().numpy(), q.rowptr.cpu().numpy(), q.col.cpu().numpy(),
+           q.val.cpu().numpy()) for q in qs]
+    hx = [x.cpu().numpy() for x in xs]
+    step_bytes = sum(gemv_bytes(q) for q in qs)
+    reps, t_total = 0, 0.0
+    with threadpool_limits(limits=1):
+        while t_total < budget_s and reps < 50:
+            t0 = time.perf_counter()
+            for (p, a, rp, c, v), x in zip(hq, hx):
+                w_eff = O.nf4_dequant(p, a, True, "float16", rp, c, v)          # per-call dequant
+                x_rot = O.rotate_blocks(x.astype(np.float32), HAD)              # FWHT-128
+                y = (x_rot @ w_eff.astype(np.float32).T).astype(np.float16)     # fp32 matmul -> fp16
+            t_total += time.perf_counter() - t0
+            reps += 1
+            del y
+    per_step = t_total / reps
+    return {"value": round(step_bytes / per_step / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} cfg2 steps (QKV + down_proj GEMV, per-call NF4 dequant + FWHT-128 + fp32 matmul), "
+                      f"{per_step * 1e3:.1f} ms/step, numpy single thread on {platform.processor() or 'host'} "
+                      f"({os.cpu_count()} logical CPUs visible)"}
+
+
+# ---------------------------------------------------------------------------
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--pool-gb", type=float, default=1.2, help="weight pool that defeats the 256 MB Infinity Cache")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-detail", action="store_true", help="skip the secondary configs")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only run the dominant kernel's timing loop (for rocprofv3 runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the multi-GPU sharding is design-only (DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU", file=sys.stderr)
+        sys.exit(1)
+    lib = L.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---- cfg2 operands
+    log("bench: building cfg2 weights (QKV 3072->5120, down 8192->3072, NF4 b64, 0.5% CSR)")
+    q_qkv = synth_nf4(5120, 3072, seed=0)
+    q_down = synth_nf4(3072, 8192, seed=10)
+    gx = torch.Generator().manual_seed(0)
+    x_qkv = torch.randn(1, 3072, generator=gx).half().to(dev)
+    x_down = torch.randn(1, 8192, generator=gx).half().to(dev)
+    y_qkv = torch.empty(1, 5120, dtype=torch.float16, device=dev)
+    y_down = torch.empty(1, 3072, dtype=torch.float16, device=dev)
+    b_qkv, b_down = gemv_bytes(q_qkv), gemv_bytes(q_down)
+    step_bytes = b_qkv + b_down
+    P = pool_copies(q_qkv.nbytes() + q_down.nbytes(), args.pool_gb * 1e9)
+    log(f"bench: pool of {P} weight copies ({P * (q_qkv.nbytes() + q_down.nbytes()) / 1e9:.2f} GB)")
+    pool = [(q_qkv, q_down)] + [(clone_nf4(q_qkv), clone_nf4(q_down)) for _ in range(P - 1)]
+    ops = [(operands(a), operands(b)) for a, b in pool]
+    qkv_calls = [Launcher(lib, oa, x_qkv, y_qkv) for oa, _ in ops]
+    down_calls = [Launcher(lib, ob, x_down, y_down) for _, ob in ops]
+
+    # ---- dominant kernel timing (down_proj GEMV, HIP events over a graph of launches)
+    nl = max(P, 100)
+    g_down = graph_of([down_calls[i % P] for i in range(nl)])
+    t_down = time_graph(g_down) / nl
+    if args.profile_kernel:
+        for _ in range(5):
+            g_down.replay()
+        torch.cuda.synchronize()
+        log(f"bench: down_proj GEMV {t_down * 1e6:.2f} us/launch")
+        return
+    g_qkv = graph_of([qkv_calls[i % P] for i in range(nl)])
+    t_qkv = time_graph(g_qkv) / nl
+
+    # ---- the timed run: K steps, one graph, between synchronizations
+    steps, warm = args.steps, args.warmup
+    for i in range(warm):
+        qkv_calls[i % P](torch.cuda.current_stream().cuda_stream)
+        down_calls[i % P](torch.cuda.current_stream().cuda_stream)
+    calls = []
+    for i in range(steps):
+        calls += [qkv_calls[i % P], down_calls[i % P]]
+    g = graph_of(calls)
+    g.replay()  # untimed replay
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / steps
+    value = step_bytes / (wall / steps) / 1e9
+
+    # correctness guard on the measured outputs (fp16 output of the last launched copy)
+    y_chk = torch.empty_like(y_down)
+    ref = K.fused_w4a16_gemv_hdsq(x_down, pool[(steps - 1) % P][1].packed, pool[(steps - 1) % P][1].absmax, None,
+                                  outlier_idx=q_down.col, outlier_w=q_down.val, marlin_layout=True, codebook="nf4",
+                                  hadamard_block=HAD, outlier_rowptr=q_down.rowptr, out=y_chk)
+    assert torch.equal(ref, y_down), "graph replay output differs from an eager launch"
+
+    achieved = b_down / t_down / 1e9
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic_gemv_cfg2_down.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    result = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (seeded CPU generators; random NF4 weights, N(0,1) activations)",
+        "config": {"workload": "cfg2: M=1 fused QKV (K=3072,N=5120) + down_proj (K=8192,N=3072) GEMV, NF4 block 64 "
+                               "+ fp16 absmax + FWHT-128 activations + 0.5% fp16 CSR outliers",
+                   "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)",
+                   "bytes_per_step": step_bytes, "weight_pool_copies": P, "timing": "one HIP graph of all steps"},
+        "roofline": {"bound": "hbm", "kernel": "gemv_kernel (down_proj K=8192 N=3072)", "achieved": round(achieved, 2),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": traffic, "algorithmic_bytes_per_launch": b_down,
+                     "avg_launch_us": round(t_down * 1e6, 3)},
+    }
+    detail = {"qkv_gemv_us": round(t_qkv * 1e6, 3), "qkv_gemv_GBps": round(b_qkv / t_qkv / 1e9, 1),
+              "down_gemv_us": round(t_down * 1e6, 3), "down_gemv_GBps": round(achieved, 1)}
+    if not args.no_detail:
+        detail.update(secondary(lib, dev, args.pool_gb))
+    result["detail"] = detail
+    if not args.no_cpu_baseline:
+        log("bench: timing the CPU oracle (bounded sample)")
+        result["cpu_baseline"] = cpu_baseline([q_qkv, q_down], [x_qkv, x_down])
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+def secondary(lib, dev, pool_gb: float) -> dict:
+    """cfg1 (plain NF4 GEMV), cfg3 (small-M), cfg4 (prefill GEMM) and the 28-layer
+    per-token linear chain of cfg5 -- reported as detail, not as the headline."""
+    out = {}
+    # cfg1: plain NF4, K=N=4096, no rotation, no outliers
+    q1 = synth_nf4(4096, 4096, seed=20, ratio=0.0)
+    q1.hadamard_block = 0
+    x1 = torch.randn(1, 4096, generator=torch.Generator().manual_seed(20)).half().to(dev)
+    y1 = torch.empty(1, 4096, dtype=torch.float16, device=dev)
+    P = pool_copies(q1.nbytes(), pool_gb * 1e9)
+    pool = [q1] + [clone_nf4(q1) for _ in range(P - 1)]
+    calls = [Launcher(lib, operands(q), x1, y1) for q in pool]
+    t = time_graph(graph_of([calls[i % P] for i in range(max(P, 100))])) / max(P, 100)
+    out["cfg1_gemv_us"] = round(t * 1e6, 3)
+    out["cfg1_gemv_GBps"] = round(gemv_bytes(q1) / t / 1e9, 1)
+    del pool, calls
+    # cfg3: M=4 gate_up on the GEMV family; M=8/16 on the MFMA GEMM (weight pool rotated)
+    q3 = synth_nf4(16384, 3072, seed=30)
+    P = pool_copies(q3.nbytes(), pool_gb * 1e9)
+    pool = [q3] + [clone_nf4(q3) for _ in range(P - 1)]
+    pool_ops = [operands(q) for q in pool]
+    for m in (4, 8, 16):
+        xm = torch.randn(m, 3072, generator=torch.Generator().manual_seed(30 + m)).half().to(dev)
+        ym = torch.empty(m, 16384, dtype=torch.float16, device=dev)
+        calls = [Launcher(lib, o, xm, ym) for o in pool_ops]
+        nl = max(P, 60)
+        t = time_graph(graph_of([calls[i % P] for i in range(nl)])) / nl
+        out[f"cfg3_gate_up_m{m}_us"] = round(t * 1e6, 2)
+        out[f"cfg3_gate_up_m{m}_GBps"] = round(gemv_bytes(q3, m) / t / 1e9, 1)
+    del q3, pool, pool_ops
+    # cfg4: prefill GEMM M=2048, (K,N) = (4096,14336) and (14336,4096), bf16
+    for (kk, nn) in ((4096, 14336), (14336, 4096)):
+        q4 = synth_nf4(nn, kk, seed=40 + kk)
+        a = torch.randn(2048, kk, generator=torch.Generator().manual_seed(kk)).bfloat16().to(dev)
+        t = _time_eager(lambda: K.batched_w4a16_gemm(a, q4.packed, q4.absmax, None, outlier_idx=q4.col,
+                                                     outlier_w=q4.val, marlin_layout=True, **q4.kernel_kwargs()),
+                        iters=10)
+        out[f"cfg4_gemm_k{kk}_n{nn}_us"] = round(t * 1e6, 1)
+        out[f"cfg4_gemm_k{kk}_n{nn}_TFLOPs"] = round(2 * 2048 * kk * nn / t / 1e12, 1)
+        out[f"cfg4_gemm_k{kk}_n{nn}_mfma_frac"] = round(2 * 2048 * kk * nn / t / 1e12 / PEAK_FP16_TFLOPS, 4)
+        del q4, a
+    # cfg5 linear chain: 28 x (QKV, o_proj, gate_up, down) + lm_head GEMVs, distinct weights
+    shapes = [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192)]
+    layer = [synth_nf4(n, k, seed=50 + i) for i, (n, k) in enumerate(shapes)]
+    head = synth_nf4_gpu(128256, 3072, seed=60)
+    xs = {k: torch.randn(1, k, generator=torch.Generator().manual_seed(k)).half().to(dev) for k in (3072, 8192)}
+    ys = {n: torch.empty(1, n, dtype=torch.float16, device=dev) for n in (5120, 3072, 16384, 128256)}
+    chain, keep = [], []
+    for li in range(28):
+        for q in (layer if li == 0 else [clone_nf4(q) for q in layer]):
+            keep.append(q)
+            chain.append(Launcher(lib, operands(q), xs[q.k], ys[q.n]))
+    chain.append(Launcher(lib, operands(head), xs[3072], ys[128256]))
+    t = time_graph(graph_of(chain))
+    chain_bytes = sum(gemv_bytes(q) for q in keep) + gemv_bytes(head)
+    out["cfg5_linear_chain_ms"] = round(t * 1e3, 4)
+    out["cfg5_linear_chain_GBps"] = round(chain_bytes / t / 1e9, 1)
+    out["cfg5_decode_tok_s_linears_only"] = round(1.0 / t, 1)
+    out["cfg5_note"] = "113 GEMVs of one decode token (28 layers + lm_head) in one graph; attention/norms excluded"
+    return out
+
+
+def _time_eager(fn, iters: int = 20) -> float:
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / iters
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,159 @@
+/*
+ * spectra_hip.h -- C ABI of the MI355X (gfx950) W4A16 quantized-linear library.
+ *
+ * Plain pointers, sizes and strides only: no torch types cross this boundary.
+ * Every device pointer is a HIP device address; every call is asynchronous on
+ * the given stream (0 = the null stream), performs no host synchronisation and
+ * no device allocation, so it can be captured into a HIP graph.
+ *
+ * Return value: SPECTRA_OK (0) on success, a negative spectra_status_t on
+ * failure; spectra_last_error() then returns a message (thread-local).
+ *
+ * Reference interfaces replaced (paths in the NeuraCryption/SPECTRA tree):
+ *   spectra_w4a16_gemv      <- spectra/kernels.py:132-184 fused_w4a16_gemv_hdsq
+ *   spectra_w4a16_gemm      <- spectra/kernels.py:333-389 batched_w4a16_gemm
+ *   spectra_w4a16_linear    <- spectra/engine.py:90-124  SpectraFusedLinear.forward
+ *   spectra_w4_dequant      <- tests/test_kernels.py:31-39, spectra/engine.py:185-210
+ *   spectra_quantize_group32<- spectra/compressor.py:71-156
+ *   spectra_quantize_nf4    <- Format B quantizer (no reference code; built on
+ *                              compressor.py:22-42 codebook and FWHT)
+ *   spectra_fwht_rows       <- spectra/compressor.py:29-42 fast_walsh_hadamard_transform
+ */
+#ifndef SPECTRA_HIP_H_
+#define SPECTRA_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* spectra_stream_t; /* == hipStream_t */
+
+typedef enum {
+  SPECTRA_OK = 0,
+  SPECTRA_ERR_INVALID = -1,     /* bad argument (shape, dtype, stride, alignment) */
+  SPECTRA_ERR_UNSUPPORTED = -2, /* valid but not served by this build */
+  SPECTRA_ERR_HIP = -3,         /* a HIP runtime call failed */
+  SPECTRA_ERR_WORKSPACE = -4    /* workspace missing or too small */
+} spectra_status_t;
+
+typedef enum { SPECTRA_F16 = 0, SPECTRA_BF16 = 1, SPECTRA_F32 = 2 } spectra_dtype_t;
+
+typedef enum {
+  SPECTRA_FMT_ASYM_G32 = 0, /* Format A: (q - z) * s, group 32, fp16 scale, uint8 zero */
+  SPECTRA_FMT_NF4 = 1       /* Format B: NF4 code * fp16 absmax, block = group_size */
+} spectra_format_t;
+
+typedef enum {
+  SPECTRA_OUTLIERS_NONE = 0,
+  SPECTRA_OUTLIERS_COLUMNS = 1, /* Format A: idx int64 [n_out] + dense w [N, n_out] */
+  SPECTRA_OUTLIERS_CSR = 2      /* Format B: row_ptr int32 [N+1], col int32, val fp16 */
+} spectra_outlier_kind_t;
+
+/*
+ * A quantized weight W[N, K] (out_features x in_features) and its side tensors.
+ * Strides are in elements of the pointed-to type; the inner stride of every
+ * 2-D operand is 1.
+ */
+typedef struct spectra_qweight {
+  int64_t n, k;
+  int32_t format;         /* spectra_format_t */
+  int32_t group_size;     /* 32 (Format A) or the NF4 block size (64) */
+  int32_t hadamard_block; /* 0, or a power of two in [8, 512] dividing k */
+  int32_t marlin_layout;  /* 1: byte j of a 32-run = q[j] | q[j+16]<<4; 0: q[2j] | q[2j+1]<<4 */
+  const uint8_t* packed;  int64_t packed_stride;  /* uint8 [N, K/2] */
+  const uint16_t* scales; int64_t scales_stride;  /* fp16 [N, K/group] (absmax for NF4) */
+  const uint8_t* zeros;   int64_t zeros_stride;   /* uint8 [N, K/32] (Format A only) */
+  int32_t outlier_kind;   /* spectra_outlier_kind_t */
+  int32_t num_outliers;   /* COLUMNS: n_out */
+  const int64_t* outlier_idx;                      /* COLUMNS: int64 [n_out], ascending */
+  const void* outlier_w; int64_t outlier_w_stride; /* COLUMNS: [N, n_out] */
+  int32_t outlier_w_dtype;                         /* COLUMNS: SPECTRA_F16 or SPECTRA_BF16 */
+  const int32_t* csr_rowptr;                       /* CSR: int32 [N+1] */
+  const int32_t* csr_col;                          /* CSR: int32 [nnz], ascending per row */
+  const uint16_t* csr_val;                         /* CSR: fp16 [nnz] */
+  int64_t csr_nnz;                                 /* CSR: number of stored outliers */
+  const void* bias; int32_t bias_dtype;            /* optional [N] */
+} spectra_qweight_t;
+
+/* Library identity and the last error message of the calling thread. */
+const char* spectra_version(void);
+const char* spectra_last_error(void);
+
+/*
+ * Decode GEMV family (M = 1..4 rows of activations):
+ *   out[m, :] = FWHT_hb(x[m, :]) . W_eff^T + bias,   fp32 accumulation, RNE store.
+ * x: act_dtype (F16/BF16) [m, K] row stride ldx; out: act_dtype [m, N] row stride ldo.
+ * Replaces kernels.py:132-184 (which serves one row; this serves up to 4).
+ */
+int spectra_w4a16_gemv(const spectra_qweight_t* w, const void* x, int64_t ldx, int32_t m,
+                       int32_t act_dtype, void* out, int64_t ldo, spectra_stream_t stream);
+
+/*
+ * Batched / prefill GEMM family (any M >= 1, MFMA):
+ *   out = FWHT_hb(a) . W_eff^T + bias,   fp16 MFMA operands, fp32 accumulation.
+ * a: act_dtype [m, K] row stride lda; out: act_dtype [m, N] row stride ldo.
+ * workspace: device scratch of at least spectra_w4a16_gemm_workspace() bytes
+ * (may be NULL when that size is 0).  Replaces kernels.py:333-389.
+ */
+size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64_t m, int32_t act_dtype);
+int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int64_t lda, int64_t m,
+                       int32_t act_dtype, void* out, int64_t ldo, void* workspace,
+                       size_t workspace_bytes, spectra_stream_t stream);
+
+/*
+ * Module dispatch (engine.py:90-124): m <= 4 -> GEMV family, else GEMM family.
+ * workspace as for spectra_w4a16_gemm (sized by spectra_w4a16_gemm_workspace).
+ */
+int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m,
+                         int32_t act_dtype, void* out, int64_t ldo, void* workspace,
+                         size_t workspace_bytes, spectra_stream_t stream);
+
+/*
+ * Materialise W_eff [N, K] in out_dtype (F16/BF16/F32), bit-exact:
+ *   Format A: round((q - z) * s in fp32), then outlier columns := round(outlier_w)
+ *   Format B: round(fp32(NF4[q]) * fp32(absmax)), then CSR positions := round(val)
+ * Bias is ignored.  (tests/test_kernels.py:31-39, engine.py:185-210)
+ */
+int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t ldo, int32_t out_dtype,
+                       spectra_stream_t stream);
+
+/*
+ * Format A quantizer (compressor.py:71-156): w [n, k] (F16/BF16/F32, row stride ldw);
+ * columns listed in outlier_idx (int64 [n_out], may be NULL) are zeroed first.
+ * Outputs: packed uint8 [n, k/2] (marlin layout), scales fp16 [n, k/32],
+ * packed_zeros uint8 [n, ceil(k/64)] (two zero points per byte).  group_size must be 32.
+ */
+int spectra_quantize_group32(const void* w, int64_t ldw, int32_t w_dtype, int64_t n, int64_t k,
+                             int32_t group_size, const int64_t* outlier_idx, int32_t n_out,
+                             uint8_t* packed, uint16_t* scales, uint8_t* packed_zeros,
+                             spectra_stream_t stream);
+
+/*
+ * Format B quantizer: w [n, k] (F16/BF16/F32, row stride ldw) -> optional blockwise
+ * FWHT of each row (hadamard_block) -> CSR positions (csr_rowptr/csr_col, may be
+ * NULL for none) are recorded into csr_val (fp16) and zeroed -> fp16 absmax per
+ * blocksize block -> nearest NF4 code (fp32 distances, lowest index on ties),
+ * packed per marlin_layout.  Outputs packed uint8 [n, k/2], absmax fp16 [n, k/blocksize].
+ */
+int spectra_quantize_nf4(const void* w, int64_t ldw, int32_t w_dtype, int64_t n, int64_t k,
+                         int32_t blocksize, int32_t hadamard_block, int32_t marlin_layout,
+                         const int32_t* csr_rowptr, const int32_t* csr_col, uint16_t* csr_val,
+                         uint8_t* packed, uint16_t* absmax, spectra_stream_t stream);
+
+/*
+ * Blockwise normalised FWHT of rows (compressor.py:29-42), fp32 arithmetic in the
+ * reference's butterfly order, division by fp32(sqrt(block)).
+ * x [rows, k] in_dtype (row stride ldx) -> out [rows, k] out_dtype (row stride ldo).
+ * block: power of two in [2, 1024] dividing k.
+ */
+int spectra_fwht_rows(const void* x, int64_t ldx, int32_t in_dtype, int64_t rows, int64_t k,
+                      int32_t block, void* out, int64_t ldo, int32_t out_dtype,
+                      spectra_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SPECTRA_HIP_H_ */

@@ -1,0 +1,355 @@
+"""numpy restatement of SPECTRA's W4A16 path (test infrastructure only).
+
+This module is the checker for the HIP product in ``spectra_amd``.  It is never
+imported by the product.  All arithmetic is stated explicitly in float32 (the
+reference's torch ops run in float32) with float64 used only for the matmul
+reference, and every function names the reference file:line it restates
+(paths relative to the reference checkout, ``spectra/`` or ``tests/``).
+
+Dtype conventions: float16 arrays are ``np.float16``; bfloat16 arrays are
+carried as their raw ``np.uint16`` bit patterns (numpy has no bfloat16), tagged
+by the ``dtype`` argument ``"bfloat16"``.
+
+Two packed-weight formats are covered:
+
+Format A (the reference, ``type: q4_g32_hdsq``, compressor.py:501-518)
+    asymmetric INT4, group 32, fp16 scale + 4-bit zero point per group,
+    "marlin" nibble interleave, dense outlier columns.
+
+Format B (the NF4 format this build serves; no reference implementation
+exists, so it is defined here from the reference's primitives)
+    NF4 code indices (codebook compressor.py:22-27), block 64, fp16 absmax per
+    block, optional blockwise Walsh-Hadamard rotation (compressor.py:29-42) of
+    the K axis, CSR element outliers (row_ptr int32, col int32, val fp16).
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, Optional, Tuple
+
+import numpy as np
+
+__all__ = [
+    "NF4_CODEBOOK", "f32_to_bf16_bits", "bf16_bits_to_f32", "to_f32", "round_to",
+    "fwht", "rotate_blocks",
+    "quantize_group32", "pack_nibbles", "unpack_nibbles", "pack_zeros", "unpack_zeros",
+    "dequant_group32", "apply_outlier_columns", "compute_group32_quant",
+    "nf4_quantize", "nf4_dequant", "nearest_code", "csr_from_mask", "linear_ref", "format_a_linear_ref",
+]
+
+# compressor.py:22-27 -- the 16 NF4 levels as float32 literals (index 7 is 0.0).
+NF4_CODEBOOK = np.array([
+    -1.0, -0.6961928009986877, -0.5250730514526367, -0.39491748809814453,
+    -0.28444138169288635, -0.18477343022823334, -0.09105003625154495, 0.0,
+    0.07958029955625534, 0.16093020141124725, 0.24611230194568634, 0.33791524171829224,
+    0.44070982933044434, 0.5626170039176941, 0.7229568362236023, 1.0,
+], dtype=np.float32)
+
+_F32_1E8 = np.float32(1e-8)  # torch compares/clamps against the scalar cast to float32
+
+
+# ----------------------------------------------------------------------------
+# dtype helpers
+# ----------------------------------------------------------------------------
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round float32 to bfloat16 with round-to-nearest-even; returns uint16 bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(x)
+    rounded = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    out = rounded.astype(np.uint16)
+    out[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)  # keep NaN quiet
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def to_f32(a: np.ndarray, dtype: str) -> np.ndarray:
+    """Widen an activation/weight array of the named dtype to float32 (exact)."""
+    if dtype == "bfloat16":
+        return bf16_bits_to_f32(a)
+    return np.asarray(a).astype(np.float32)
+
+
+def round_to(x32: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float32 values to ``dtype`` with round-to-nearest-even."""
+    if dtype == "float16":
+        return np.asarray(x32, dtype=np.float32).astype(np.float16)
+    if dtype == "bfloat16":
+        return f32_to_bf16_bits(x32)
+    if dtype == "float32":
+        return np.asarray(x32, dtype=np.float32)
+    raise ValueError(f"unsupported dtype {dtype}")
+
+
+# ----------------------------------------------------------------------------
+# Walsh-Hadamard transform -- compressor.py:29-42
+# ----------------------------------------------------------------------------
+def fwht(x: np.ndarray, normalize: bool = True) -> np.ndarray:
+    """Sylvester-order fast Walsh-Hadamard transform along the last axis, float32.
+
+    Restates compressor.py:29-42: stages h = 1, 2, 4, ... d/2; at each stage the
+    pair (i, i+h) inside every 2h-block becomes (u+v, u-v) (compressor.py:35-39);
+    normalisation divides by float32(sqrt(d)) (compressor.py:40-41; torch divides
+    a float32 tensor by the Python scalar rounded to float32).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    d = x.shape[-1]
+    if d & (d - 1):
+        raise ValueError(f"last dimension ({d}) must be a power of 2")  # compressor.py:32
+    res = x.reshape(-1, d).copy()
+    h = 1
+    while h < d:
+        v4 = res.reshape(-1, d // (2 * h), 2, h)
+        u, v = v4[:, :, 0, :].copy(), v4[:, :, 1, :].copy()
+        v4[:, :, 0, :] = u + v
+        v4[:, :, 1, :] = u - v
+        h *= 2
+    if normalize:
+        res = res / np.float32(math.sqrt(d))
+    return res.reshape(x.shape)
+
+
+def rotate_blocks(x: np.ndarray, block: int) -> np.ndarray:
+    """Blockwise FWHT of the last axis in independent ``block``-wide blocks (float32)."""
+    x = np.asarray(x, dtype=np.float32)
+    if block == 0:
+        return x.copy()
+    K = x.shape[-1]
+    if K % block:
+        raise ValueError(f"K={K} is not a multiple of the Hadamard block {block}")
+    return fwht(x.reshape(x.shape[:-1] + (K // block, block))).reshape(x.shape)
+
+
+# ----------------------------------------------------------------------------
+# Nibble layouts -- compressor.py:99-102 (pack), engine.py:185-202 (unpack)
+# ----------------------------------------------------------------------------
+def pack_nibbles(q: np.ndarray, marlin: bool) -> np.ndarray:
+    """Pack 4-bit codes [N, K] into bytes [N, K/2].
+
+    marlin=True: inside each 32-run, byte j holds q[j] (low) and q[j+16] (high)
+    (compressor.py:99-102).  marlin=False: byte j holds q[2j] (low) and q[2j+1]
+    (high) (the even-odd layout read at kernels.py:90-95 / engine.py:197-202).
+    """
+    q = np.asarray(q, dtype=np.uint8)
+    N, K = q.shape
+    if marlin:
+        if K % 32:
+            raise ValueError("marlin layout needs K % 32 == 0")
+        g = q.reshape(N, K // 32, 32)
+        return (g[:, :, :16] | (g[:, :, 16:] << 4)).astype(np.uint8).reshape(N, K // 2)
+    return (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_nibbles(packed: np.ndarray, marlin: bool) -> np.ndarray:
+    """Inverse of ``pack_nibbles``: bytes [N, K/2] -> codes [N, K] (engine.py:185-202)."""
+    p = np.asarray(packed, dtype=np.uint8)
+    N, KB = p.shape
+    lo, hi = p & 0x0F, p >> 4
+    if marlin:
+        lo_g = lo.reshape(N, KB // 16, 16)
+        hi_g = hi.reshape(N, KB // 16, 16)
+        return np.concatenate([lo_g, hi_g], axis=-1).reshape(N, 2 * KB)
+    return np.stack([lo, hi], axis=-1).reshape(N, 2 * KB)
+
+
+def pack_zeros(z: np.ndarray) -> np.ndarray:
+    """Two 4-bit zero points per byte, even group low (compressor.py:104-110)."""
+    z = np.asarray(z, dtype=np.uint8)
+    if z.shape[1] % 2:
+        z = np.pad(z, ((0, 0), (0, 1)))
+    return (z[:, 0::2] | (z[:, 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_zeros(pz: np.ndarray, groups: int) -> np.ndarray:
+    """engine.py:1007-1012 / tests/test_kernels.py:25-29: nibble-unpack then slice."""
+    pz = np.asarray(pz, dtype=np.uint8)
+    z = np.empty((pz.shape[0], pz.shape[1] * 2), dtype=np.uint8)
+    z[:, 0::2] = pz & 0x0F
+    z[:, 1::2] = pz >> 4
+    return np.ascontiguousarray(z[:, :groups])
+
+
+# ----------------------------------------------------------------------------
+# Format A: asymmetric INT4, group 32 -- compressor.py:71-156
+# ----------------------------------------------------------------------------
+def quantize_group32(w: np.ndarray, group_size: int = 32) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Restates ``_quantize_chunk_group32`` (compressor.py:71-112) in float32.
+
+    Returns (packed uint8 [N,K/2] marlin layout, scales float16 [N,K/32],
+    packed zero points uint8 [N, ceil(G/2)]).
+    """
+    if group_size != 32:
+        raise ValueError("group_size must be 32")  # compressor.py:53-54
+    w = np.asarray(w, dtype=np.float32)
+    N, K = w.shape
+    G = K // 32
+    wg = w.reshape(N, G, 32)
+    w_min = wg.min(axis=-1, keepdims=True)                         # :78
+    w_max = wg.max(axis=-1, keepdims=True)                         # :79
+    diff = (w_max - w_min).astype(np.float32)                      # :80
+    is_const = diff < _F32_1E8                                     # :81
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scales = np.where(is_const,
+                          np.where(w_min == 0, np.float32(1.0), np.abs(w_min)),
+                          diff / np.float32(15.0)).astype(np.float32)  # :83
+        scales = np.maximum(scales, _F32_1E8)                      # :84 clamp(min=1e-8)
+        z_norm = np.clip(np.rint(-w_min / scales), 0, 15).astype(np.uint8)   # :89
+        zeros = np.where(is_const, np.where(w_min < 0, 1, 0).astype(np.uint8), z_norm)  # :86-90
+        neg_zs = (-zeros.astype(np.float32)) * scales                # -z*s      :95
+        q_norm = np.clip(np.rint((wg - neg_zs) / scales), 0, 15).astype(np.uint8)      # :95
+    q_const = np.broadcast_to(np.where(w_min > 0, 1, 0).astype(np.uint8), wg.shape)   # :94
+    q = np.where(is_const, q_const, q_norm).astype(np.uint8)
+    packed = pack_nibbles(q.reshape(N, K), marlin=True)           # :99-102
+    return packed, scales[..., 0].astype(np.float16), pack_zeros(zeros[..., 0])      # :104-112
+
+
+def dequant_group32(packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray,
+                    marlin: bool = True, out_dtype: str = "float16") -> np.ndarray:
+    """``(q - z) * s`` in float32, rounded to ``out_dtype``.
+
+    Restates tests/test_kernels.py:31-36 (fp16) and engine.py:185-206 (model dtype):
+    nibbles unpacked per layout, zero points unpacked uint8 [N, G], float32
+    arithmetic, one rounding to the output dtype.
+    """
+    q = unpack_nibbles(packed, marlin).astype(np.float32)
+    N, K = q.shape
+    G = K // 32
+    s = np.asarray(scales, dtype=np.float16).astype(np.float32).reshape(N, G, 1)
+    z = np.asarray(zeros, dtype=np.uint8).astype(np.float32).reshape(N, G, 1)
+    w = ((q.reshape(N, G, 32) - z) * s).reshape(N, K)
+    return round_to(w.astype(np.float32), out_dtype)
+
+
+def apply_outlier_columns(w_deq: np.ndarray, idx: np.ndarray, ow: np.ndarray, dtype: str) -> np.ndarray:
+    """Substitute dense outlier columns (tests/test_kernels.py:38-39, engine.py:209-210).
+
+    ``ow`` is [N, n_out] in float16 (np.float16) or bfloat16 (uint16 bits); it is
+    cast to ``dtype`` like ``outlier_weight.to(target_dtype)``.
+    """
+    out = np.array(w_deq, copy=True)
+    ow_dtype = "bfloat16" if np.asarray(ow).dtype == np.uint16 else "float16"
+    out[:, np.asarray(idx, dtype=np.int64)] = round_to(to_f32(ow, ow_dtype), dtype)
+    return out
+
+
+def compute_group32_quant(w: np.ndarray, outlier_idx: Optional[np.ndarray] = None):
+    """``_compute_group32_quant`` (compressor.py:114-156): zero outlier columns, then
+    quantize.  The reference's 4096-row chunking is row-local and does not change
+    results, so the oracle quantizes in one pass."""
+    w = np.array(w, dtype=np.float32, copy=True)
+    if outlier_idx is not None:
+        w[:, np.asarray(outlier_idx, dtype=np.int64)] = 0.0        # :134-135 / :148-149
+    return quantize_group32(w)
+
+
+def format_a_linear_ref(x: np.ndarray, x_dtype: str, w_eff: np.ndarray, bias: Optional[np.ndarray] = None,
+                        bias_dtype: str = "float16") -> np.ndarray:
+    """fp64 reference of ``x @ w_deq.T (+ bias)`` (tests/test_kernels.py:46); returns float64."""
+    x64 = to_f32(x, x_dtype).astype(np.float64)
+    w64 = to_f32(w_eff, x_dtype).astype(np.float64)
+    y = x64 @ w64.T
+    if bias is not None:
+        y = y + to_f32(bias, bias_dtype).astype(np.float64)[None, :]
+    return y
+
+
+# ----------------------------------------------------------------------------
+# Format B: NF4, block 64, fp16 absmax, Hadamard rotation, CSR outliers
+# ----------------------------------------------------------------------------
+def csr_from_mask(mask: np.ndarray, values32: np.ndarray) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Row-major CSR (row_ptr int32 [N+1], col int32 [nnz], val float16 [nnz])."""
+    mask = np.asarray(mask, dtype=bool)
+    rows, cols = np.nonzero(mask)  # row-major order, columns ascending within a row
+    counts = np.bincount(rows, minlength=mask.shape[0])
+    rowptr = np.zeros(mask.shape[0] + 1, dtype=np.int64)
+    np.cumsum(counts, out=rowptr[1:])
+    val = np.asarray(values32, dtype=np.float32)[rows, cols].astype(np.float16)
+    return rowptr.astype(np.int32), cols.astype(np.int32), val
+
+
+def nearest_code(r: np.ndarray) -> np.ndarray:
+    """argmin_i |C_i - r| in float32, lowest index on ties (np.argmin semantics)."""
+    out = np.empty(r.shape, dtype=np.uint8)
+    flat, of = r.reshape(-1), out.reshape(-1)
+    step = 1 << 20
+    for s in range(0, flat.size, step):
+        d = np.abs(NF4_CODEBOOK[None, :] - flat[s:s + step, None])
+        of[s:s + step] = np.argmin(d, axis=1)
+    return out
+
+
+def nf4_quantize(w: np.ndarray, w_dtype: str = "float16", blocksize: int = 64, hadamard_block: int = 0,
+                 outlier_mask: Optional[np.ndarray] = None, marlin: bool = True) -> Dict[str, np.ndarray]:
+    """Format B quantizer (no reference code; built from compressor.py primitives).
+
+    1. w -> float32; if ``hadamard_block``: rotate each K-block (compressor.py:29-42),
+       so the stored matrix is W . blockdiag(H).
+    2. Outliers (``outlier_mask`` [N,K]): values kept as float16 in CSR, positions
+       zeroed before quantization (the zeroing convention of compressor.py:134-135).
+    3. absmax per ``blocksize`` block = float16(max |w|) (round-to-nearest-even).
+    4. r = w / float32(absmax) (0 where absmax == 0); q = nearest NF4 code index
+       with float32 distances, lowest index on ties; packed per ``marlin``.
+    """
+    w32 = to_f32(w, w_dtype).astype(np.float32)
+    N, K = w32.shape
+    if K % blocksize:
+        raise ValueError(f"K={K} not a multiple of blocksize {blocksize}")
+    if hadamard_block:
+        w32 = rotate_blocks(w32, hadamard_block)
+    else:
+        w32 = w32.copy()
+    if outlier_mask is not None:
+        rowptr, col, val = csr_from_mask(outlier_mask, w32)
+        w32[np.asarray(outlier_mask, dtype=bool)] = 0.0
+    else:
+        rowptr, col, val = np.zeros(N + 1, np.int32), np.zeros(0, np.int32), np.zeros(0, np.float16)
+    wb = w32.reshape(N, K // blocksize, blocksize)
+    amax32 = np.abs(wb).max(axis=-1)
+    absmax = amax32.astype(np.float16)
+    if not np.all(np.isfinite(absmax)):
+        raise ValueError("block absmax overflows float16")
+    a32 = absmax.astype(np.float32)[..., None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        r = np.where(a32 > 0, wb / np.where(a32 > 0, a32, np.float32(1)), np.float32(0)).astype(np.float32)
+    q = nearest_code(r).reshape(N, K)
+    return {"packed": pack_nibbles(q, marlin), "absmax": absmax, "rowptr": rowptr, "col": col, "val": val,
+            "codes": q}
+
+
+def nf4_dequant(packed: np.ndarray, absmax: np.ndarray, marlin: bool = True, out_dtype: str = "float16",
+                rowptr: Optional[np.ndarray] = None, col: Optional[np.ndarray] = None,
+                val: Optional[np.ndarray] = None, blocksize: int = 64) -> np.ndarray:
+    """W_eff = round_out(float32(C[q]) * float32(absmax)), then CSR positions := round_out(val).
+
+    The float32 product is rounded once to float32 and once to the output dtype
+    (the torch expression ``(code.float() * absmax.float()).to(dtype)``).
+    """
+    q = unpack_nibbles(packed, marlin)
+    N, K = q.shape
+    codes = NF4_CODEBOOK[q].reshape(N, K // blocksize, blocksize)
+    a32 = np.asarray(absmax, dtype=np.float16).astype(np.float32)[..., None]
+    w = round_to((codes * a32).astype(np.float32).reshape(N, K), out_dtype)
+    if rowptr is not None and col is not None and len(col):
+        rows = np.repeat(np.arange(N), np.diff(np.asarray(rowptr, dtype=np.int64)))
+        w[rows, np.asarray(col, dtype=np.int64)] = round_to(np.asarray(val, np.float16).astype(np.float32), out_dtype)
+    return w
+
+
+def linear_ref(x: np.ndarray, x_dtype: str, w_eff: np.ndarray, w_dtype: str, hadamard_block: int = 0,
+               bias: Optional[np.ndarray] = None, bias_dtype: str = "float16",
+               round_x_to: Optional[str] = None) -> np.ndarray:
+    """y = float32(FWHT_hb(x)) @ float32(W_eff)^T (+ bias), accumulated in float64.
+
+    ``round_x_to`` optionally rounds the rotated activations to a 16-bit dtype
+    first (what a 16-bit MFMA operand sees).  Returns float64 (unrounded).
+    """
+    x32 = rotate_blocks(to_f32(x, x_dtype), hadamard_block)
+    if round_x_to is not None:
+        x32 = to_f32(round_to(x32, round_x_to), round_x_to)
+    y = x32.astype(np.float64) @ to_f32(w_eff, w_dtype).astype(np.float64).T
+    if bias is not None:
+        y = y + to_f32(bias, bias_dtype).astype(np.float64)[None, :]
+    return y

@@ -1,0 +1,94 @@
+// C-ABI glue: error state, weight-descriptor validation, module dispatch.
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "common.h"
+
+namespace spectra {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int fail(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+
+int validate_qweight(const spectra_qweight_t* w) {
+  SPECTRA_REQUIRE(w != nullptr, "weight descriptor is NULL");
+  SPECTRA_REQUIRE(w->n > 0 && w->k > 0, "N and K must be positive");
+  SPECTRA_REQUIRE(w->n < (1LL << 31) && w->k < (1LL << 30), "N or K too large");
+  SPECTRA_REQUIRE(w->packed != nullptr && w->scales != nullptr, "packed/scales pointer is NULL");
+  SPECTRA_REQUIRE(w->format == SPECTRA_FMT_ASYM_G32 || w->format == SPECTRA_FMT_NF4, "unknown format");
+  if (w->format == SPECTRA_FMT_ASYM_G32) {
+    SPECTRA_REQUIRE(w->group_size == 32, "Format A (asymmetric INT4) requires group_size 32");
+    SPECTRA_REQUIRE(w->zeros != nullptr, "Format A needs unpacked zero points");
+    SPECTRA_REQUIRE(w->zeros_stride >= w->k / 32, "zeros row stride too small");
+  } else {
+    SPECTRA_REQUIRE(w->group_size >= 16 && is_pow2(w->group_size), "NF4 block size must be a power of two >= 16");
+  }
+  SPECTRA_REQUIRE(w->k % 32 == 0, "K must be a multiple of 32");
+  SPECTRA_REQUIRE(w->k % w->group_size == 0, "K must be a multiple of the group/block size");
+  SPECTRA_REQUIRE(w->hadamard_block == 0 || (is_pow2(w->hadamard_block) && w->hadamard_block >= 2 &&
+                                             w->hadamard_block <= 1024 && w->k % w->hadamard_block == 0),
+                  "hadamard_block must be 0 or a power of two in [2, 1024] dividing K");
+  SPECTRA_REQUIRE(w->packed_stride >= w->k / 2, "packed row stride too small");
+  SPECTRA_REQUIRE(w->scales_stride >= w->k / w->group_size, "scales row stride too small");
+  SPECTRA_REQUIRE(w->outlier_kind >= SPECTRA_OUTLIERS_NONE && w->outlier_kind <= SPECTRA_OUTLIERS_CSR,
+                  "unknown outlier kind");
+  if (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS) {
+    SPECTRA_REQUIRE(w->num_outliers > 0 && w->outlier_idx && w->outlier_w, "outlier columns need idx and w");
+    SPECTRA_REQUIRE(w->outlier_w_dtype == SPECTRA_F16 || w->outlier_w_dtype == SPECTRA_BF16,
+                    "outlier weights must be fp16 or bf16");
+    SPECTRA_REQUIRE(w->outlier_w_stride >= w->num_outliers, "outlier_w row stride too small");
+  }
+  if (w->outlier_kind == SPECTRA_OUTLIERS_CSR) {
+    SPECTRA_REQUIRE(w->csr_rowptr != nullptr, "CSR outliers need rowptr");
+    SPECTRA_REQUIRE(w->csr_nnz >= 0 && w->csr_nnz < (1LL << 31), "bad CSR nnz");
+    SPECTRA_REQUIRE(w->csr_nnz == 0 || (w->csr_col && w->csr_val), "CSR outliers need col/val");
+  }
+  if (w->bias)
+    SPECTRA_REQUIRE(w->bias_dtype == SPECTRA_F16 || w->bias_dtype == SPECTRA_BF16 || w->bias_dtype == SPECTRA_F32,
+                    "bias dtype must be fp16, bf16 or fp32");
+  return SPECTRA_OK;
+}
+
+int ensure_lds_limit(const void* kernel) {
+  static std::mutex mu;
+  static std::vector<std::pair<const void*, int>> done;
+  int dev = 0;
+  SPECTRA_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lk(mu);
+  for (const auto& d : done)
+    if (d.first == kernel && d.second == dev) return SPECTRA_OK;
+  int max_lds = 0;
+  SPECTRA_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
+  SPECTRA_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds));
+  done.emplace_back(kernel, dev);
+  return SPECTRA_OK;
+}
+
+}  // namespace spectra
+
+// gemv.hip / gemm.hip
+namespace spectra {
+int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, int act_dtype, void* out,
+                int64_t ldo, hipStream_t stream);
+}
+
+extern "C" const char* spectra_version(void) { return "spectra_hip 0.1.0 gfx950"; }
+
+extern "C" const char* spectra_last_error(void) { return spectra::g_last_error.c_str(); }
+
+extern "C" int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m,
+                                    int32_t act_dtype, void* out, int64_t ldo, void* workspace,
+                                    size_t workspace_bytes, spectra_stream_t stream) {
+  // engine.py:94-124: single-token rows go to the GEMV family, everything else to the GEMM family
+  if (m >= 1 && m <= 4)
+    return spectra_w4a16_gemv(w, x, ldx, (int32_t)m, act_dtype, out, ldo, stream);
+  return spectra_w4a16_gemm(w, x, ldx, m, act_dtype, out, ldo, workspace, workspace_bytes, stream);
+}

@@ -1,0 +1,114 @@
+// Shared device/host helpers for the gfx950 W4A16 library.
+// Compiled with -ffp-contract=off: every float operation below rounds exactly
+// where it is written, which the bit-exact quantizer/dequant kernels rely on.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "spectra_hip.h"
+
+namespace spectra {
+
+// ---------------------------------------------------------------------------
+// error reporting (host)
+// ---------------------------------------------------------------------------
+void set_error(const std::string& msg);
+int fail(int status, const std::string& msg);
+#define SPECTRA_REQUIRE(cond, msg)                                   \
+  do {                                                               \
+    if (!(cond)) return ::spectra::fail(SPECTRA_ERR_INVALID, (msg)); \
+  } while (0)
+#define SPECTRA_HIP_CHECK(expr)                                                        \
+  do {                                                                                 \
+    hipError_t e_ = (expr);                                                            \
+    if (e_ != hipSuccess)                                                              \
+      return ::spectra::fail(SPECTRA_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+  } while (0)
+
+// Validates a spectra_qweight_t (shapes, pointers, alignment); returns status.
+int validate_qweight(const spectra_qweight_t* w);
+// Raises a kernel's dynamic-LDS limit to the device maximum once per (kernel, device).
+int ensure_lds_limit(const void* kernel);
+inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// ---------------------------------------------------------------------------
+// NF4 codebook (compressor.py:22-27): fp32 literals and their fp16 roundings
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float nf4_code_f32(int i) {
+  // select chain over literal constants: no memory access, any lane index
+  float r = -1.0f;
+  r = (i == 1) ? -0.6961928009986877f : r;
+  r = (i == 2) ? -0.5250730514526367f : r;
+  r = (i == 3) ? -0.39491748809814453f : r;
+  r = (i == 4) ? -0.28444138169288635f : r;
+  r = (i == 5) ? -0.18477343022823334f : r;
+  r = (i == 6) ? -0.09105003625154495f : r;
+  r = (i == 7) ? 0.0f : r;
+  r = (i == 8) ? 0.07958029955625534f : r;
+  r = (i == 9) ? 0.16093020141124725f : r;
+  r = (i == 10) ? 0.24611230194568634f : r;
+  r = (i == 11) ? 0.33791524171829224f : r;
+  r = (i == 12) ? 0.44070982933044434f : r;
+  r = (i == 13) ? 0.5626170039176941f : r;
+  r = (i == 14) ? 0.7229568362236023f : r;
+  r = (i == 15) ? 1.0f : r;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit float conversions (round-to-nearest-even)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, RNE
+}
+__device__ __forceinline__ float bf2f(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+// dtype-tagged load/store of one element
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
+  if (dtype == SPECTRA_F16) return h2f(((const uint16_t*)p)[i]);
+  if (dtype == SPECTRA_BF16) return bf2f(((const uint16_t*)p)[i]);
+  return ((const float*)p)[i];
+}
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dtype, float v) {
+  if (dtype == SPECTRA_F16) ((uint16_t*)p)[i] = f2h(v);
+  else if (dtype == SPECTRA_BF16) ((uint16_t*)p)[i] = f2bf(v);
+  else ((float*)p)[i] = v;
+}
+__device__ __forceinline__ float to_f32_16(uint16_t v, int dtype) {
+  return dtype == SPECTRA_BF16 ? bf2f(v) : h2f(v);
+}
+__device__ __forceinline__ uint16_t from_f32_16(float v, int dtype) {
+  return dtype == SPECTRA_BF16 ? f2bf(v) : f2h(v);
+}
+
+// k index of nibble `half` (0 = low, 1 = high) of packed byte j in a row
+__host__ __device__ __forceinline__ int64_t nibble_k(int64_t j, int half, int marlin) {
+  return marlin ? ((j >> 4) << 5) + (j & 15) + (half << 4) : 2 * j + half;
+}
+// inverse: (byte j, half) holding element k
+__host__ __device__ __forceinline__ void k_to_nibble(int64_t k, int marlin, int64_t* j, int* half) {
+  if (marlin) {
+    *j = ((k >> 5) << 4) + (k & 15);
+    *half = (int)((k >> 4) & 1);
+  } else {
+    *j = k >> 1;
+    *half = (int)(k & 1);
+  }
+}
+
+inline int elem_size(int dtype) { return dtype == SPECTRA_F32 ? 4 : 2; }
+
+}  // namespace spectra

@@ -1,0 +1,80 @@
+// W_eff materialisation, bit-exact against the reference's torch dequant:
+//   Format A: round_out((q - z) * s) in fp32 (tests/test_kernels.py:31-36,
+//             engine.py:185-206), then outlier columns := round_out(outlier_w)
+//             (tests/test_kernels.py:38-39, engine.py:209-210)
+//   Format B: round_out(fp32(NF4[q]) * fp32(absmax)), then CSR positions := round_out(val)
+#include "common.h"
+
+namespace spectra {
+
+constexpr int kDqThreads = 256;
+
+__global__ void __launch_bounds__(kDqThreads) dequant_kernel(spectra_qweight_t w, void* __restrict__ out,
+                                                              int64_t ldo, int out_dt) {
+  const int64_t kb = w.k / 2;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= w.n * kb) return;
+  const int64_t row = t / kb, j = t % kb;
+  const uint8_t byte = w.packed[row * w.packed_stride + j];
+  for (int half = 0; half < 2; ++half) {
+    const int q = half ? (byte >> 4) : (byte & 15);
+    const int64_t kk = nibble_k(j, half, w.marlin_layout);
+    float v;
+    if (w.format == SPECTRA_FMT_ASYM_G32) {
+      const int64_t g = kk / 32;
+      const float s = h2f(w.scales[row * w.scales_stride + g]);
+      const float z = (float)w.zeros[row * w.zeros_stride + g];
+      v = ((float)q - z) * s;
+    } else {
+      const int64_t blk = kk / w.group_size;
+      v = nf4_code_f32(q) * h2f(w.scales[row * w.scales_stride + blk]);
+    }
+    store_elem(out, row * ldo + kk, out_dt, v);
+  }
+}
+
+__global__ void __launch_bounds__(kDqThreads) scatter_columns_kernel(spectra_qweight_t w, void* __restrict__ out,
+                                                                      int64_t ldo, int out_dt) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= w.n * w.num_outliers) return;
+  const int64_t row = t / w.num_outliers, j = t % w.num_outliers;
+  const float v = load_elem(w.outlier_w, row * w.outlier_w_stride + j, w.outlier_w_dtype);
+  store_elem(out, row * ldo + w.outlier_idx[j], out_dt, v);
+}
+
+__global__ void __launch_bounds__(kDqThreads) scatter_csr_kernel(spectra_qweight_t w, void* __restrict__ out,
+                                                                  int64_t ldo, int out_dt) {
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= w.n) return;
+  for (int e = w.csr_rowptr[row]; e < w.csr_rowptr[row + 1]; ++e)
+    store_elem(out, row * ldo + w.csr_col[e], out_dt, h2f(w.csr_val[e]));
+}
+
+}  // namespace spectra
+
+using namespace spectra;
+
+extern "C" int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t ldo, int32_t out_dtype,
+                                  spectra_stream_t stream) {
+  int st = validate_qweight(w);
+  if (st != SPECTRA_OK) return st;
+  SPECTRA_REQUIRE(out != nullptr, "out is NULL");
+  SPECTRA_REQUIRE(ldo >= w->k, "out row stride smaller than K");
+  SPECTRA_REQUIRE(out_dtype >= SPECTRA_F16 && out_dtype <= SPECTRA_F32, "bad out dtype");
+  const hipStream_t s = (hipStream_t)stream;
+  const int64_t work = w->n * (w->k / 2);
+  hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((work + kDqThreads - 1) / kDqThreads)), dim3(kDqThreads), 0, s,
+                     *w, out, ldo, (int)out_dtype);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  if (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS) {
+    const int64_t cw = w->n * w->num_outliers;
+    hipLaunchKernelGGL(scatter_columns_kernel, dim3((unsigned)((cw + kDqThreads - 1) / kDqThreads)),
+                       dim3(kDqThreads), 0, s, *w, out, ldo, (int)out_dtype);
+    SPECTRA_HIP_CHECK(hipGetLastError());
+  } else if (w->outlier_kind == SPECTRA_OUTLIERS_CSR) {
+    hipLaunchKernelGGL(scatter_csr_kernel, dim3((unsigned)((w->n + kDqThreads - 1) / kDqThreads)),
+                       dim3(kDqThreads), 0, s, *w, out, ldo, (int)out_dtype);
+    SPECTRA_HIP_CHECK(hipGetLastError());
+  }
+  return SPECTRA_OK;
+}

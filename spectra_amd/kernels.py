@@ -1,0 +1,266 @@
+"""Drop-in replacements for the reference's ``spectra/kernels.py`` entry points.
+
+``fused_w4a16_gemv_hdsq`` and ``batched_w4a16_gemm`` keep the reference's
+positional signatures (kernels.py:132-142, :333-341) and argument meaning; the
+Format B (NF4 + Hadamard + CSR) operands are reached through keyword-only
+arguments whose defaults leave Format A calls unchanged:
+
+    codebook="asym" | "nf4"     Format A (q - z) * s   |  Format B NF4 * absmax
+    group_size=None             32 for Format A, NF4 block size (default 64)
+    hadamard_block=0            blockwise FWHT of the activations (0 = none)
+    outlier_rowptr=None         when given, outlier_idx / outlier_w are the CSR
+                                col (int32 [nnz]) / val (fp16 [nnz]) arrays
+    bias=None                   (batched only) fused bias, as engine.py:122-123
+
+All work runs in libspectra_hip.so on the current HIP stream; nothing here
+computes on the host and there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Tuple
+
+import torch
+
+from . import _lib as L
+
+__all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_dequant", "fwht_rows",
+           "QWeightOperands", "GEMV_MAX_M"]
+
+GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
+
+_DT = {torch.float16: L.F16, torch.bfloat16: L.BF16, torch.float32: L.F32}
+_TORCH_DT = {v: k for k, v in _DT.items()}
+
+
+def _dtype_code(t: torch.Tensor, allowed, what: str) -> int:
+    if t.dtype not in allowed:
+        raise ValueError(f"{what} must be one of {[str(a) for a in allowed]}, got {t.dtype}")
+    return _DT[t.dtype]
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _rows(t: torch.Tensor, name: str, align: int = 1) -> Tuple[torch.Tensor, int]:
+    """2-D operand with unit inner stride (and optional base/row alignment in bytes)."""
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+        t = t.contiguous()
+    es = t.element_size()
+    if align > 1 and (t.data_ptr() % align or (t.stride(0) * es) % align):
+        t = t.contiguous().clone() if t.is_contiguous() else t.contiguous()
+        if t.data_ptr() % align or (t.stride(0) * es) % align:
+            raise ValueError(f"{name}: cannot satisfy {align}-byte row alignment for shape {tuple(t.shape)}")
+    return t, t.stride(0)
+
+
+class QWeightOperands:
+    """Validated device operands of one quantized weight + its C descriptor.
+
+    Keeps every tensor it hands to the library alive for as long as the
+    descriptor is used.
+    """
+
+    def __init__(self, packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor], k: int, *,
+                 codebook: str = "asym", group_size: Optional[int] = None, hadamard_block: int = 0,
+                 marlin_layout: bool = False, outlier_idx: Optional[torch.Tensor] = None,
+                 outlier_w: Optional[torch.Tensor] = None, outlier_rowptr: Optional[torch.Tensor] = None,
+                 bias: Optional[torch.Tensor] = None, packed_align: int = 16):
+        if not packed.is_cuda:
+            raise ValueError("packed weights must be on the GPU")
+        dev = packed.device
+        if packed.dtype != torch.uint8:
+            raise ValueError(f"packed weights must be uint8, got {packed.dtype}")
+        n = packed.shape[0]
+        if codebook not in ("asym", "nf4"):
+            raise ValueError(f"codebook must be 'asym' or 'nf4', got {codebook!r}")
+        fmt = L.FMT_ASYM_G32 if codebook == "asym" else L.FMT_NF4
+        gs = group_size if group_size is not None else (32 if fmt == L.FMT_ASYM_G32 else 64)
+        if k <= 0 or k % 2 or packed.shape[1] != k // 2:
+            raise ValueError(f"packed weights {tuple(packed.shape)} do not match K={k} (need [N, K/2])")
+        if k % gs:
+            raise ValueError(f"K={k} is not a multiple of group_size {gs}")
+        keep: List[torch.Tensor] = []
+        packed, ldp = _rows(packed, "packed_w", packed_align)
+        keep.append(packed)
+        if scales.dtype != torch.float16:
+            raise ValueError(f"scales must be float16, got {scales.dtype}")
+        if scales.shape[0] != n or scales.shape[1] < k // gs:
+            raise ValueError(f"scales {tuple(scales.shape)} do not match [N={n}, K/group={k // gs}]")
+        scales, lds = _rows(scales, "scales")
+        keep.append(scales)
+        w = L.QWeight()
+        w.n, w.k, w.format, w.group_size = n, k, fmt, gs
+        w.hadamard_block, w.marlin_layout = int(hadamard_block), int(bool(marlin_layout))
+        w.packed, w.packed_stride = packed.data_ptr(), ldp
+        w.scales, w.scales_stride = scales.data_ptr(), lds
+        if fmt == L.FMT_ASYM_G32:
+            if zeros is None:
+                raise ValueError("Format A needs zero points")
+            if zeros.dtype != torch.uint8 or zeros.shape[0] != n or zeros.shape[1] < k // 32:
+                raise ValueError(f"zeros must be uint8 [N, K/32] (unpacked), got {zeros.dtype} {tuple(zeros.shape)}")
+            zeros, ldz = _rows(zeros, "zeros")
+            keep.append(zeros)
+            w.zeros, w.zeros_stride = zeros.data_ptr(), ldz
+        w.outlier_kind = L.OUTLIERS_NONE
+        if outlier_rowptr is not None:
+            if outlier_idx is None or outlier_w is None:
+                raise ValueError("CSR outliers need outlier_rowptr, outlier_idx (col) and outlier_w (val)")
+            rp = outlier_rowptr.to(device=dev, dtype=torch.int32).contiguous()
+            col = outlier_idx.to(device=dev, dtype=torch.int32).contiguous()
+            if outlier_w.dtype != torch.float16:
+                raise ValueError(f"CSR outlier values must be float16, got {outlier_w.dtype}")
+            val = outlier_w.to(device=dev).contiguous()
+            if rp.numel() != n + 1 or col.numel() != val.numel():
+                raise ValueError("CSR shapes: rowptr [N+1], col and val [nnz]")
+            keep += [rp, col, val]
+            w.outlier_kind = L.OUTLIERS_CSR
+            w.csr_rowptr, w.csr_col, w.csr_val, w.csr_nnz = rp.data_ptr(), col.data_ptr(), val.data_ptr(), col.numel()
+        elif outlier_idx is not None and outlier_w is not None:
+            idx = outlier_idx.to(device=dev, dtype=torch.int64).contiguous()
+            ow = outlier_w
+            if ow.dim() != 2 or ow.shape[0] != n or ow.shape[1] != idx.numel():
+                raise ValueError(f"outlier_w must be [N, n_out], got {tuple(ow.shape)}")
+            odt = _dtype_code(ow, (torch.float16, torch.bfloat16), "outlier_w")
+            ow, ldow = _rows(ow, "outlier_w")
+            keep += [idx, ow]
+            w.outlier_kind = L.OUTLIERS_COLUMNS
+            w.num_outliers = idx.numel()
+            w.outlier_idx, w.outlier_w, w.outlier_w_stride, w.outlier_w_dtype = idx.data_ptr(), ow.data_ptr(), ldow, odt
+        if bias is not None:
+            if bias.numel() != n:
+                raise ValueError(f"bias must have N={n} elements")
+            b = bias.detach().reshape(n).contiguous()
+            w.bias, w.bias_dtype = b.data_ptr(), _dtype_code(b, _DT.keys(), "bias")
+            keep.append(b)
+        self.desc = w
+        self.keep = keep
+        self.n, self.k, self.device = n, k, dev
+
+    def ptr(self):
+        return ctypes.byref(self.desc)
+
+
+def _run_linear(ops: QWeightOperands, x2: torch.Tensor, out2: torch.Tensor, family: str) -> None:
+    lib = L.load()
+    m, k = x2.shape
+    adt = _DT[x2.dtype]
+    stream = _stream(x2.device)
+    if family == "gemv":
+        L.check("spectra_w4a16_gemv", lib.spectra_w4a16_gemv(ops.ptr(), x2.data_ptr(), x2.stride(0), m, adt,
+                                                              out2.data_ptr(), out2.stride(0), stream))
+        return
+    ws_bytes = lib.spectra_w4a16_gemm_workspace(ops.ptr(), m, adt)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=x2.device)
+    fn = lib.spectra_w4a16_gemm if family == "gemm" else lib.spectra_w4a16_linear
+    L.check(fn.__name__, fn(ops.ptr(), x2.data_ptr(), x2.stride(0), m, adt, out2.data_ptr(), out2.stride(0),
+                            ws.data_ptr(), ws.numel(), stream))
+
+
+def _activations(x: torch.Tensor, k: int) -> Tuple[torch.Tensor, torch.dtype]:
+    """[M, K] fp16/bf16 view with a 16-byte aligned base and row stride; fp32 inputs are
+    computed in fp16 like the reference's compute dtype (kernels.py:347-348)."""
+    if not x.is_cuda:
+        raise ValueError("activations must be on the GPU")
+    if x.shape[-1] != k:
+        raise ValueError(f"activation inner dim {x.shape[-1]} != K={k}")
+    in_dtype = x.dtype
+    x2 = x.reshape(-1, k)
+    if x2.dtype not in (torch.float16, torch.bfloat16):
+        x2 = x2.to(torch.float16)
+    x2, _ = _rows(x2, "x", 16)
+    return x2, in_dtype
+
+
+def fused_w4a16_gemv_hdsq(x: torch.Tensor, packed_w: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
+                          bias: Optional[torch.Tensor] = None, outlier_idx: Optional[torch.Tensor] = None,
+                          outlier_w: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                          marlin_layout: bool = False, *, codebook: str = "asym", group_size: Optional[int] = None,
+                          hadamard_block: int = 0, outlier_rowptr: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode GEMV (kernels.py:132-184): ``out[b] = x[b] . W_eff^T + bias``.
+
+    x is [K] or [B, K].  Rows up to GEMV_MAX_M run on the GEMV family; the reference
+    kernel reads only row 0 (kernels.py:42-98), here every row is computed (larger B
+    goes to the MFMA GEMM family).
+    """
+    orig_1d = x.dim() == 1
+    if orig_1d:
+        x = x.unsqueeze(0)
+    if x.dim() != 2:
+        raise ValueError(f"x must be [K] or [B, K], got {tuple(x.shape)}")
+    B, K = x.shape
+    ops = QWeightOperands(packed_w, scales, zeros, K, codebook=codebook, group_size=group_size,
+                          hadamard_block=hadamard_block, marlin_layout=marlin_layout, outlier_idx=outlier_idx,
+                          outlier_w=outlier_w, outlier_rowptr=outlier_rowptr, bias=bias)
+    x2, in_dtype = _activations(x, K)
+    N = ops.n
+    if out is None:
+        out = torch.empty((B, N), device=x.device, dtype=in_dtype)
+    if out.shape != (B, N):
+        raise ValueError(f"out must be [B={B}, N={N}], got {tuple(out.shape)}")
+    target = out if (out.dtype == x2.dtype and out.stride(1) == 1) else torch.empty((B, N), device=x.device,
+                                                                                      dtype=x2.dtype)
+    _run_linear(ops, x2, target, "gemv" if B <= GEMV_MAX_M else "gemm")
+    if target is not out:
+        out.copy_(target)
+    return out.squeeze(0) if orig_1d else out
+
+
+def batched_w4a16_gemm(a: torch.Tensor, packed_b: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
+                       outlier_idx: Optional[torch.Tensor] = None, outlier_w: Optional[torch.Tensor] = None,
+                       marlin_layout: bool = False, *, codebook: str = "asym", group_size: Optional[int] = None,
+                       hadamard_block: int = 0, outlier_rowptr: Optional[torch.Tensor] = None,
+                       bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Batched / prefill GEMM (kernels.py:333-389): ``c = a . W_eff^T`` over all leading dims,
+    returned in ``a.dtype`` with shape ``a.shape[:-1] + (N,)``."""
+    K = a.shape[-1]
+    ops = QWeightOperands(packed_b, scales, zeros, K, codebook=codebook, group_size=group_size,
+                          hadamard_block=hadamard_block, marlin_layout=marlin_layout, outlier_idx=outlier_idx,
+                          outlier_w=outlier_w, outlier_rowptr=outlier_rowptr, bias=bias)
+    x2, in_dtype = _activations(a, K)
+    c = torch.empty((x2.shape[0], ops.n), device=a.device, dtype=x2.dtype)
+    _run_linear(ops, x2, c, "gemm")
+    return c.reshape(a.shape[:-1] + (ops.n,)).to(in_dtype)
+
+
+def w4a16_linear(ops: QWeightOperands, x: torch.Tensor) -> torch.Tensor:
+    """Module dispatch through the C ABI (engine.py:90-124): GEMV family for up to
+    GEMV_MAX_M rows, MFMA GEMM otherwise.  Returns ``x.shape[:-1] + (N,)`` in x.dtype."""
+    x2, in_dtype = _activations(x, ops.k)
+    out = torch.empty((x2.shape[0], ops.n), device=x.device, dtype=x2.dtype)
+    _run_linear(ops, x2, out, "linear")
+    return out.reshape(x.shape[:-1] + (ops.n,)).to(in_dtype)
+
+
+def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor], *, k: Optional[int] = None,
+               out_dtype: torch.dtype = torch.float16, codebook: str = "asym", group_size: Optional[int] = None,
+               marlin_layout: bool = False, outlier_idx: Optional[torch.Tensor] = None,
+               outlier_w: Optional[torch.Tensor] = None, outlier_rowptr: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Materialise W_eff [N, K] bit-exactly (tests/test_kernels.py:31-39, engine.py:185-210)."""
+    k = k if k is not None else packed.shape[1] * 2
+    ops = QWeightOperands(packed, scales, zeros, k, codebook=codebook, group_size=group_size,
+                          marlin_layout=marlin_layout, outlier_idx=outlier_idx, outlier_w=outlier_w,
+                          outlier_rowptr=outlier_rowptr, packed_align=1)
+    out = torch.empty((ops.n, k), device=packed.device, dtype=out_dtype)
+    lib = L.load()
+    L.check("spectra_w4_dequant", lib.spectra_w4_dequant(ops.ptr(), out.data_ptr(), out.stride(0),
+                                                          _dtype_code(out, _DT.keys(), "out_dtype"),
+                                                          _stream(out.device)))
+    return out
+
+
+def fwht_rows(x: torch.Tensor, block: int, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Blockwise normalised FWHT of the last dim (compressor.py:29-42), fp32 arithmetic."""
+    if not x.is_cuda:
+        raise ValueError("x must be on the GPU")
+    k = x.shape[-1]
+    x2, ldx = _rows(x.reshape(-1, k), "x")
+    out = torch.empty(x2.shape, device=x.device, dtype=out_dtype or x.dtype)
+    lib = L.load()
+    L.check("spectra_fwht_rows", lib.spectra_fwht_rows(x2.data_ptr(), ldx, _dtype_code(x2, _DT.keys(), "x"),
+                                                        x2.shape[0], k, int(block), out.data_ptr(), out.stride(0),
+                                                        _dtype_code(out, _DT.keys(), "out"), _stream(x.device)))
+    return out.reshape(x.shape)

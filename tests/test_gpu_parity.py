@@ -1,0 +1,429 @@
+"""GPU parity of the HIP path against the CPU oracle (run on an MI355X).
+
+Bars:
+  * quantizers, FWHT and W_eff dequant: bit-exact;
+  * GEMV / GEMM outputs, fp16: max-abs <= 1e-2 and L2-relative <= 1e-3 against
+    y_ref = fp32(FWHT(x)) @ fp32(W_eff)^T accumulated in float64;
+  * bf16 outputs: bf16 rounding alone is ~2^-9 relative, so the bar is max error
+    <= 1 bf16 ulp of |y_ref| (+1e-2 absolute) and L2-relative <= 5e-3.
+Every case prints its parameters first so a failure names it.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from spectra_amd import compressor as C
+from spectra_amd import kernels as K
+from spectra_amd.engine import SpectraFusedLinear
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+TDT = {"float16": torch.float16, "bfloat16": torch.bfloat16, "float32": torch.float32}
+
+
+def case(**kw):
+    print("case:", ", ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+def cuda(a, dtype=None):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16 and dtype == torch.bfloat16:
+        return torch.from_numpy(a.view(np.int16)).view(torch.bfloat16).cuda()
+    t = torch.from_numpy(a).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def host(t, dtype="float16"):
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def check_y(y, y_ref, dtype):
+    yv = y.detach().float().cpu().double().numpy().reshape(y_ref.shape)
+    err = np.abs(yv - y_ref)
+    rel = np.linalg.norm(yv - y_ref) / max(np.linalg.norm(y_ref), 1e-30)
+    if dtype == torch.float16:
+        assert err.max() <= 1e-2, f"max-abs {err.max()}"
+        assert rel <= 1e-3, f"rel-L2 {rel}"
+    else:
+        ulp = np.abs(O.bf16_bits_to_f32(O.f32_to_bf16_bits(y_ref.astype(np.float32)))).astype(np.float64) * 2.0 ** -7
+        assert np.all(err <= ulp + 1e-2), f"max excess {np.max(err - ulp)}"
+        assert rel <= 5e-3, f"rel-L2 {rel}"
+    return err.max(), rel
+
+
+def rand_np(rng, shape, scale=1.0, dtype=np.float16):
+    return (rng.standard_normal(shape) * scale).astype(dtype)
+
+
+# ---------------------------------------------------------------------------
+# quantizers / FWHT / dequant: bit-exact
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("wdt", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("n,k,n_out", [(128, 256, 0), (64, 1024, 9), (3, 96, 2)])
+def test_quantize_group32_bitexact(hip, wdt, n, k, n_out):
+    case(wdt=wdt, n=n, k=k, n_out=n_out)
+    rng = np.random.default_rng(n * k + n_out)
+    w32 = rand_np(rng, (n, k), 0.05, np.float32)
+    w32[0, :32] = 2.5       # KAT groups (tests/test_quantizer.py:19-55)
+    w32[1, :32] = -4.25
+    w32[2, :32] = 0.0
+    wt = cuda(w32, TDT[wdt])
+    w_exact = wt.float().cpu().numpy()  # the values the GPU sees
+    idx = np.sort(rng.permutation(k)[:n_out]).astype(np.int64) if n_out else None
+    packed, scales, pz = C.compute_group32_quant(wt, outlier_idx=cuda(idx) if idx is not None else None)
+    rp, rs, rz = O.compute_group32_quant(w_exact, idx)
+    assert np.array_equal(host(packed), rp)
+    assert np.array_equal(host(scales), rs)
+    assert np.array_equal(host(pz), rz)
+
+
+@pytest.mark.parametrize("had", [0, 128, 64])
+@pytest.mark.parametrize("marlin", [True, False])
+@pytest.mark.parametrize("outliers", [False, True])
+def test_quantize_nf4_bitexact(hip, had, marlin, outliers):
+    case(had=had, marlin=marlin, outliers=outliers)
+    rng = np.random.default_rng(100 + had + marlin * 7 + outliers)
+    n, k = 48, 1024
+    w = rand_np(rng, (n, k), 0.02)
+    w[3, 64:128] = 0  # zero block
+    mask = rng.random((n, k)) < 0.005 if outliers else None
+    q = C.quantize_nf4(cuda(w), blocksize=64, hadamard_block=had, outlier_mask=cuda(mask) if outliers else None,
+                       marlin_layout=marlin)
+    r = O.nf4_quantize(w, "float16", blocksize=64, hadamard_block=had, outlier_mask=mask, marlin=marlin)
+    assert np.array_equal(host(q.packed), r["packed"])
+    assert np.array_equal(host(q.absmax), r["absmax"])
+    assert np.array_equal(host(q.rowptr), r["rowptr"])
+    assert np.array_equal(host(q.col), r["col"])
+    assert np.array_equal(host(q.val), r["val"])
+
+
+def test_golden_format_b_quantizer(hip):
+    g = np.load(os.path.join(HERE, "golden", "format_b_small.npz"))
+    q = C.quantize_nf4(cuda(g["w"]), 64, 0, cuda(g["mask"]), True)
+    assert np.array_equal(host(q.packed), g["packed"]) and np.array_equal(host(q.absmax), g["absmax"])
+    assert np.array_equal(host(q.val), g["val"])
+    qr = C.quantize_nf4(cuda(g["w_plain"]), 64, int(g["had"]), None, False)
+    assert np.array_equal(host(qr.packed), g["packed_rot"]) and np.array_equal(host(qr.absmax), g["absmax_rot"])
+
+
+@pytest.mark.parametrize("block", [2, 8, 128, 512, 1024])
+@pytest.mark.parametrize("in_dt", ["float32", "float16", "bfloat16"])
+def test_fwht_bitexact(hip, block, in_dt):
+    case(block=block, in_dt=in_dt)
+    rng = np.random.default_rng(block)
+    x = rand_np(rng, (7, 2048), 1.0, np.float32)
+    xt = cuda(x, TDT[in_dt])
+    y = K.fwht_rows(xt, block, out_dtype=torch.float32)
+    ref = O.rotate_blocks(xt.float().cpu().numpy(), block)
+    assert np.array_equal(host(y), ref)
+
+
+@pytest.mark.parametrize("out_dt", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("marlin", [True, False])
+def test_dequant_format_a_bitexact(hip, out_dt, marlin):
+    case(out_dt=out_dt, marlin=marlin)
+    g = np.load(os.path.join(HERE, "golden", "format_a_small.npz"))
+    z = cuda(g["zeros"])
+    w = K.w4_dequant(cuda(g["packed"]), cuda(g["scales"]), z, out_dtype=TDT[out_dt], codebook="asym",
+                     marlin_layout=marlin, outlier_idx=cuda(g["idx"]), outlier_w=cuda(g["ow"]))
+    ref = O.apply_outlier_columns(O.dequant_group32(g["packed"], g["scales"], g["zeros"], marlin, out_dt),
+                                  g["idx"], g["ow"], out_dt)
+    assert np.array_equal(host(w), ref)
+    if out_dt == "float16" and marlin:
+        assert np.array_equal(host(w), g["w_deq"])  # golden fixture
+
+
+@pytest.mark.parametrize("out_dt", ["float16", "bfloat16", "float32"])
+def test_dequant_format_b_bitexact(hip, out_dt):
+    case(out_dt=out_dt)
+    g = np.load(os.path.join(HERE, "golden", "format_b_small.npz"))
+    w = K.w4_dequant(cuda(g["packed"]), cuda(g["absmax"]), None, out_dtype=TDT[out_dt], codebook="nf4",
+                     group_size=64, marlin_layout=True, outlier_idx=cuda(g["col"]), outlier_w=cuda(g["val"]),
+                     outlier_rowptr=cuda(g["rowptr"]))
+    ref = O.nf4_dequant(g["packed"], g["absmax"], True, out_dt, g["rowptr"], g["col"], g["val"])
+    assert np.array_equal(host(w), ref)
+    if out_dt == "float16":
+        assert np.array_equal(host(w), g["w_eff16"])
+    if out_dt == "bfloat16":
+        assert np.array_equal(host(w), g["w_effbf"])
+
+
+# ---------------------------------------------------------------------------
+# Format A GEMV / GEMM (the reference's own test cases, tests/test_kernels.py:43-70)
+# ---------------------------------------------------------------------------
+def _format_a(seed, n, k, n_out, act="float16"):
+    rng = np.random.default_rng(seed)
+    w = rand_np(rng, (n, k), 1.0)
+    idx = np.sort(rng.permutation(k)[:n_out]).astype(np.int64) if n_out else None
+    packed, scales, pz = O.compute_group32_quant(w.astype(np.float32), idx)
+    z = O.unpack_zeros(pz, k // 32)
+    w_deq = O.dequant_group32(packed, scales, z, True, act)
+    ow = None
+    if n_out:
+        ow = w[:, idx] if act == "float16" else O.round_to(w[:, idx].astype(np.float32), act)
+        w_deq = O.apply_outlier_columns(w_deq, idx, ow, act)
+    return packed, scales, z, idx, ow, w_deq
+
+
+@pytest.mark.parametrize("act", ["float16", "bfloat16"])
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+@pytest.mark.parametrize("n_out", [0, 16])
+def test_format_a_reference_cases(hip, act, m, n_out):
+    case(act=act, m=m, n_out=n_out)
+    packed, scales, z, idx, ow, w_deq = _format_a(42, 128, 256, n_out, act)
+    rng = np.random.default_rng(m)
+    x = rand_np(rng, (m, 256), 1.0, np.float32)
+    x = O.round_to(x, act)
+    xt = cuda(x, TDT[act])
+    y_ref = O.format_a_linear_ref(x, act, w_deq)
+    kw = dict(outlier_idx=cuda(idx) if n_out else None, outlier_w=cuda(ow, TDT[act]) if n_out else None,
+              marlin_layout=True)
+    if m == 1:
+        y = K.fused_w4a16_gemv_hdsq(xt, cuda(packed), cuda(scales), cuda(z), **kw)
+    else:
+        y = K.batched_w4a16_gemm(xt, cuda(packed), cuda(scales), cuda(z), **kw)
+    assert y.dtype == TDT[act] and y.shape == (m, 128)
+    # the reference's own bar (tests/test_kernels.py:48-49) ...
+    assert np.abs(y.float().cpu().double().numpy() - y_ref).max() <= 0.05
+    # ... and this build's
+    check_y(y, y_ref, TDT[act])
+
+
+@pytest.mark.parametrize("m", [1, 3, 4, 5, 16, 33])
+@pytest.mark.parametrize("marlin", [True, False])
+def test_format_a_gemv_gemm_with_bias(hip, m, marlin):
+    case(m=m, marlin=marlin)
+    rng = np.random.default_rng(m + 10 * marlin)
+    n, k = 200, 1536
+    w = rand_np(rng, (n, k), 0.05)
+    idx = np.sort(rng.permutation(k)[:20]).astype(np.int64)
+    packed, scales, pz = O.compute_group32_quant(w.astype(np.float32), idx)
+    if not marlin:  # same codes, even-odd nibble order
+        packed = O.pack_nibbles(O.unpack_nibbles(packed, True), False)
+    z = O.unpack_zeros(pz, k // 32)
+    ow = w[:, idx]
+    w_deq = O.apply_outlier_columns(O.dequant_group32(packed, scales, z, marlin, "float16"), idx, ow, "float16")
+    b = rand_np(rng, (n,), 0.5)
+    x = rand_np(rng, (m, k), 1.0)
+    y_ref = O.format_a_linear_ref(x, "float16", w_deq, bias=b)
+    lin = SpectraFusedLinear(k, n, 32, has_bias=True, marlin_layout=marlin).cuda()
+    lin.set_weights(cuda(packed), cuda(scales), cuda(z), bias=cuda(b), outlier_idx=cuda(idx), outlier_weight=cuda(ow),
+                    marlin_layout=marlin)
+    y = lin(cuda(x))
+    check_y(y, y_ref, torch.float16)
+
+
+# ---------------------------------------------------------------------------
+# Format B (NF4 + Hadamard + CSR)
+# ---------------------------------------------------------------------------
+def _format_b(seed, n, k, had, ratio=0.005, marlin=True, scale=0.02):
+    rng = np.random.default_rng(seed)
+    w = rand_np(rng, (n, k), scale)
+    mask = rng.random((n, k)) < ratio
+    w[mask] = (np.abs(rng.standard_normal(mask.sum())) * 0.2 * np.sign(rng.standard_normal(mask.sum()))).astype(
+        np.float16)
+    q = O.nf4_quantize(w, "float16", 64, 0, mask if ratio > 0 else None, marlin)
+    return q, rng
+
+
+@pytest.mark.parametrize("act", ["float16", "bfloat16"])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("had", [0, 128])
+@pytest.mark.parametrize("marlin", [True, False])
+def test_format_b_gemv(hip, act, m, had, marlin):
+    case(act=act, m=m, had=had, marlin=marlin)
+    q, rng = _format_b(m * 3 + had + marlin, 257, 3072, had, marlin=marlin)
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], marlin, act, q["rowptr"], q["col"], q["val"])
+    x = O.round_to(rand_np(rng, (m, 3072), 1.0, np.float32), act)
+    b = rand_np(rng, (257,), 0.1)
+    y_ref = O.linear_ref(x, act, w_eff, act, hadamard_block=had, bias=b)
+    y = K.fused_w4a16_gemv_hdsq(cuda(x, TDT[act]), cuda(q["packed"]), cuda(q["absmax"]), None, bias=cuda(b),
+                                outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]), marlin_layout=marlin,
+                                codebook="nf4", group_size=64, hadamard_block=had, outlier_rowptr=cuda(q["rowptr"]))
+    check_y(y, y_ref, TDT[act])
+
+
+def test_golden_format_b_gemv(hip):
+    g = np.load(os.path.join(HERE, "golden", "format_b_small.npz"))
+    y = K.fused_w4a16_gemv_hdsq(cuda(g["x"]), cuda(g["packed"]), cuda(g["absmax"]), None, outlier_idx=cuda(g["col"]),
+                                outlier_w=cuda(g["val"]), marlin_layout=True, codebook="nf4", group_size=64,
+                                hadamard_block=int(g["had"]), outlier_rowptr=cuda(g["rowptr"]))
+    check_y(y, g["y_ref"], torch.float16)
+
+
+@pytest.mark.parametrize("n,k", [(1, 1024), (33, 256), (100, 1536), (513, 4096), (64, 8192), (40, 14336)])
+def test_format_b_gemv_shapes(hip, n, k):
+    case(n=n, k=k)
+    q, rng = _format_b(n + k, n, k, 128)
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, "float16", q["rowptr"], q["col"], q["val"])
+    x = rand_np(rng, (1, k), 1.0)
+    y_ref = O.linear_ref(x, "float16", w_eff, "float16", hadamard_block=128)
+    y = K.fused_w4a16_gemv_hdsq(cuda(x[0]), cuda(q["packed"]), cuda(q["absmax"]), None, outlier_idx=cuda(q["col"]),
+                                outlier_w=cuda(q["val"]), marlin_layout=True, codebook="nf4", hadamard_block=128,
+                                outlier_rowptr=cuda(q["rowptr"]))
+    assert y.shape == (n,)
+    check_y(y.unsqueeze(0), y_ref, torch.float16)
+
+
+@pytest.mark.parametrize("act", ["float16", "bfloat16"])
+@pytest.mark.parametrize("m", [5, 16, 64, 130])
+def test_format_b_gemm(hip, act, m):
+    case(act=act, m=m)
+    n, k = 320, 2048
+    q, rng = _format_b(m, n, k, 128, ratio=0.01)
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, act, q["rowptr"], q["col"], q["val"])
+    x = O.round_to(rand_np(rng, (m, k), 1.0, np.float32), act)
+    y_ref = O.linear_ref(x, act, w_eff, act, hadamard_block=128)
+    y = K.batched_w4a16_gemm(cuda(x, TDT[act]), cuda(q["packed"]), cuda(q["absmax"]), None,
+                             outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]), marlin_layout=True, codebook="nf4",
+                             hadamard_block=128, outlier_rowptr=cuda(q["rowptr"]))
+    check_y(y, y_ref, TDT[act])
+
+
+def test_dense_outlier_rows(hip):
+    """A row with many outliers in one 64-wide tile exercises the GEMM's slow path and
+    the GEMV's beyond-register entries."""
+    n, k = 130, 1024
+    q, rng = _format_b(5, n, k, 0, ratio=0.0)
+    mask = np.zeros((n, k), bool)
+    mask[7, 64:128] = True          # 64 outliers in one tile
+    mask[100, :] = True             # a fully dense row
+    mask[129, ::3] = True
+    w = rand_np(rng, (n, k), 0.02)
+    qq = O.nf4_quantize(w, "float16", 64, 0, mask, True)
+    w_eff = O.nf4_dequant(qq["packed"], qq["absmax"], True, "float16", qq["rowptr"], qq["col"], qq["val"])
+    for m in (1, 4, 20):
+        case(m=m)
+        x = rand_np(rng, (m, k), 1.0)
+        y_ref = O.linear_ref(x, "float16", w_eff, "float16")
+        fn = K.fused_w4a16_gemv_hdsq if m <= 4 else K.batched_w4a16_gemm
+        y = fn(cuda(x), cuda(qq["packed"]), cuda(qq["absmax"]), None, outlier_idx=cuda(qq["col"]),
+               outlier_w=cuda(qq["val"]), marlin_layout=True, codebook="nf4", outlier_rowptr=cuda(qq["rowptr"]))
+        check_y(y, y_ref, torch.float16)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE shapes (configs 1-3) at full size, M=1..16, against the oracle
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("name,n,k,had,ratio,ms", [
+    ("cfg1", 4096, 4096, 0, 0.0, (1,)),
+    ("cfg2_qkv", 5120, 3072, 128, 0.005, (1,)),
+    ("cfg2_down", 3072, 8192, 128, 0.005, (1, 4, 16)),
+    ("cfg3_gate_up", 16384, 3072, 128, 0.005, (4, 8)),
+])
+def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(n, k, generator=g) * 0.02).half()
+    mask = None
+    if ratio:
+        nnz = int(round(ratio * n * k))
+        pos = torch.randperm(n * k, generator=g)[:nnz]
+        vals = (torch.randn(nnz, generator=g).abs() * 0.2 * torch.sign(torch.randn(nnz, generator=g))).half()
+        w.view(-1)[pos] = vals
+        mask = torch.zeros(n * k, dtype=torch.bool)
+        mask[pos] = True
+        mask = mask.view(n, k)
+    q = C.quantize_nf4(w.cuda(), 64, 0, mask.cuda() if mask is not None else None, True)
+    # the full-size quantizer and dequant agree bit for bit with the oracle on sampled rows
+    rows = np.array([0, 1, n // 2, n - 1])
+    sub = O.nf4_quantize(w.numpy()[rows], "float16", 64, 0, mask.numpy()[rows] if mask is not None else None, True)
+    assert np.array_equal(host(q.packed)[rows], sub["packed"]) and np.array_equal(host(q.absmax)[rows], sub["absmax"])
+    w_eff_t = K.w4_dequant(q.packed, q.absmax, None, codebook="nf4", marlin_layout=True,
+                           outlier_idx=q.col if q.col.numel() else None, outlier_w=q.val if q.col.numel() else None,
+                           outlier_rowptr=q.rowptr if q.col.numel() else None)
+    w_eff = O.nf4_dequant(host(q.packed), host(q.absmax), True, "float16", host(q.rowptr), host(q.col), host(q.val))
+    assert np.array_equal(host(w_eff_t), w_eff)
+    for m in ms:
+        case(name=name, m=m)
+        x = (torch.randn(m, k, generator=g)).half()
+        y_ref = O.linear_ref(x.numpy(), "float16", w_eff, "float16", hadamard_block=had)
+        kw = q.kernel_kwargs()
+        col, val = q.outliers()
+        fn = K.fused_w4a16_gemv_hdsq if m <= 4 else K.batched_w4a16_gemm
+        y = fn(x.cuda(), q.packed, q.absmax, None, outlier_idx=col, outlier_w=val, marlin_layout=True, **kw)
+        err, rel = check_y(y, y_ref, torch.float16)
+        print(f"{name} m={m}: max-abs {err:.3e} rel-L2 {rel:.3e}", flush=True)
+
+
+def test_prefill_gemm_against_torch_fp32(hip):
+    """cfg4 shape class (K=4096 -> N=14336, M=512 here): fp32 torch reference on the
+    GPU built from the bit-exact dequant and FWHT kernels, plus oracle rows."""
+    g = torch.Generator().manual_seed(4)
+    m, k, n = 512, 4096, 14336
+    w = (torch.randn(n, k, generator=g) * 0.02).half()
+    nnz = int(round(0.005 * n * k))
+    pos = torch.randperm(n * k, generator=g)[:nnz]
+    mask = torch.zeros(n * k, dtype=torch.bool)
+    mask[pos] = True
+    w.view(-1)[pos] = (torch.randn(nnz, generator=g) * 0.2).half()
+    q = C.quantize_nf4(w.cuda(), 64, 0, mask.view(n, k).cuda(), True)
+    x = torch.randn(m, k, generator=g).bfloat16().cuda()
+    y = K.batched_w4a16_gemm(x, q.packed, q.absmax, None, outlier_idx=q.col, outlier_w=q.val, marlin_layout=True,
+                             **q.kernel_kwargs() | dict(hadamard_block=128))
+    w_eff = K.w4_dequant(q.packed, q.absmax, None, out_dtype=torch.bfloat16, codebook="nf4", marlin_layout=True,
+                         outlier_idx=q.col, outlier_w=q.val, outlier_rowptr=q.rowptr)
+    x_rot = K.fwht_rows(x, 128, out_dtype=torch.float32)
+    y_t = (x_rot @ w_eff.float().T).double().cpu().numpy()
+    check_y(y, y_t, torch.bfloat16)
+
+
+# ---------------------------------------------------------------------------
+# engineering properties
+# ---------------------------------------------------------------------------
+def test_determinism_and_graph_replay(hip):
+    q, rng = _format_b(3, 1024, 4096, 128)
+    args = (cuda(q["packed"]), cuda(q["absmax"]), None)
+    kw = dict(outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]), marlin_layout=True, codebook="nf4",
+              hadamard_block=128, outlier_rowptr=cuda(q["rowptr"]))
+    lin = SpectraFusedLinear(4096, 1024, 64, codebook="nf4", hadamard_block=128).cuda()
+    lin.set_weights(*args, outlier_idx=kw["outlier_idx"], outlier_weight=kw["outlier_w"], marlin_layout=True,
+                    outlier_rowptr=kw["outlier_rowptr"])
+    x1 = cuda(rand_np(rng, (1, 4096), 1.0))
+    x8 = cuda(rand_np(rng, (8, 4096), 1.0))
+    e1, e8 = lin(x1), lin(x8)
+    assert torch.equal(lin(x1), e1) and torch.equal(lin(x8), e8)  # bitwise deterministic
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            lin(x1), lin(x8)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        g1 = lin(x1)
+        g8 = lin(x8)
+    for _ in range(3):
+        g1.zero_()
+        g8.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(g1, e1) and torch.equal(g8, e8)
+        _ = lin(x1)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_module_edge_cases(hip):
+    q, rng = _format_b(9, 64, 256, 0, ratio=0.0)
+    lin = SpectraFusedLinear(256, 64, 64, codebook="nf4").cuda()
+    lin.set_weights(cuda(q["packed"]), cuda(q["absmax"]), None, marlin_layout=True)
+    assert lin(torch.empty(0, 256, dtype=torch.float16, device="cuda")).shape == (0, 64)
+    x = cuda(rand_np(rng, (2, 3, 256), 1.0))
+    y = lin(x)
+    assert y.shape == (2, 3, 64)
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, "float16")
+    check_y(y.reshape(6, 64), O.linear_ref(host(x).reshape(6, 256), "float16", w_eff, "float16"), torch.float16)
+    with pytest.raises(ValueError):
+        K.fused_w4a16_gemv_hdsq(x.reshape(6, 256)[:, :128], cuda(q["packed"]), cuda(q["absmax"]), None,
+                                codebook="nf4")
+    with pytest.raises(ValueError):
+        C.SpectraCompressor(group_size=64)
+    with pytest.raises(NotImplementedError):
+        C.SpectraCompressor(hadamard_incoherence=True)

@@ -1,0 +1,301 @@
+"""CPU checks that pin the numpy oracle (oracle/spectra_oracle.py).
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped term,
+a wrong sign or index, a transposed operand, a swapped nibble order, a wrong
+butterfly pairing, float64 leaking into float32 arithmetic) fails it:
+  * the reference's own known-answer tests (tests/test_quantizer.py:19-55),
+  * closed forms and invariants (reconstruction bound, exact code points,
+    involution of the normalised Hadamard matrix, dense Sylvester matrix),
+  * brute force (nearest NF4 code in float64),
+  * library routines (scipy's Hadamard matrix, torch's float32/bfloat16
+    arithmetic and casts) for the floating-point semantics.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import scipy.linalg
+import torch
+
+import oracle as O
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+# ---------------------------------------------------------------------------
+# Format A quantizer -- reference KATs (tests/test_quantizer.py:19-55)
+# ---------------------------------------------------------------------------
+def _kats():
+    with open(os.path.join(HERE, "golden", "kat_group32.json")) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _kats(), ids=lambda c: c["name"])
+def test_group32_kat(case):
+    w = np.full((1, 32), case["value"], dtype=np.float32)
+    packed, scales, pz = O.quantize_group32(w)
+    z = O.unpack_zeros(pz, 1)
+    q = O.unpack_nibbles(packed, marlin=True)
+    assert float(scales[0, 0]) == case["scale"]
+    assert int(z[0, 0]) == case["zero"]
+    assert np.all(q == case["q"])
+    deq = O.dequant_group32(packed, scales, z, marlin=True, out_dtype="float32")
+    # the reference asserts equality to 4 places; the closed form gives it exactly
+    assert np.all(deq == np.float32(case["dequant"]))
+
+
+def test_group32_size_enforced():
+    # compressor.py:53-54 / tests/test_quantizer.py:6-13
+    with pytest.raises(ValueError):
+        O.quantize_group32(np.zeros((1, 64), np.float32), group_size=64)
+
+
+def test_group32_reconstruction_bound():
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((64, 512)) * 0.05).astype(np.float16).astype(np.float32)
+    packed, scales, pz = O.quantize_group32(w)
+    z = O.unpack_zeros(pz, 512 // 32)
+    deq = O.dequant_group32(packed, scales, z, out_dtype="float32")
+    g = w.reshape(64, 16, 32)
+    contains0 = (g.min(-1) <= 0) & (g.max(-1) >= 0)
+    s = scales.astype(np.float32)
+    s32 = (g.max(-1) - g.min(-1)) / np.float32(15)
+    # |deq - w| <= s/2 (rounding) + 15*|s16 - s32| (fp16 scale) + float slack
+    bound = 0.5 * s32 + 15.0 * np.abs(s - s32) + 1e-6
+    err = np.abs(deq.reshape(64, 16, 32) - g).max(-1)
+    assert np.all(err[contains0] <= bound[contains0])
+    # zero points stay in range and codes use the full 0..15 span of the group
+    assert z.max() <= 15
+
+
+def test_group32_matches_torch_float32_semantics():
+    """Float32 semantics pin: torch evaluating the same op sequence (divide by
+    the scalar rounded to float32, round-half-even, where/clamp) gives the
+    identical bits.  Catches float64 promotion or reciprocal-multiply slips."""
+    g = torch.Generator().manual_seed(3)
+    w = (torch.randn(32, 256, generator=g) * 0.1).half().float()
+    w[0, :32] = 1.5   # constant group
+    w[1, :32] = 0.0   # zero group
+    w[2, :32] = -3.0  # constant negative group
+    wg = w.reshape(32, 8, 32)
+    wmin = wg.amin(-1, keepdim=True)
+    wmax = wg.amax(-1, keepdim=True)
+    diff = wmax - wmin
+    const = diff < 1e-8
+    s = torch.where(const, torch.where(wmin == 0, torch.ones_like(wmin), wmin.abs()), diff / 15.0).clamp(min=1e-8)
+    z = torch.where(const, torch.where(wmin < 0, 1, 0).to(torch.uint8),
+                    torch.clamp(torch.round(-wmin / s), 0, 15).to(torch.uint8))
+    q = torch.where(const, torch.where(wmin > 0, 1, 0).to(torch.uint8).expand_as(wg),
+                    torch.clamp(torch.round((wg - (-z.float() * s)) / s), 0, 15).to(torch.uint8))
+    packed, scales, pz = O.quantize_group32(w.numpy())
+    assert np.array_equal(O.unpack_nibbles(packed, True), q.reshape(32, 256).numpy())
+    assert np.array_equal(scales, s[..., 0].half().numpy())
+    assert np.array_equal(O.unpack_zeros(pz, 8), z[..., 0].numpy())
+
+
+def test_outlier_columns_dequant_to_zero():
+    """compressor.py:134-135: zeroed outlier columns dequantize to exactly 0,
+    so adding the outlier product equals substituting the column."""
+    rng = np.random.default_rng(2)
+    w = (rng.standard_normal((48, 256)) * 0.02).astype(np.float16).astype(np.float32)
+    w[5, :] = np.abs(w[5, :]) + 0.01   # all-positive row
+    w[6, :] = -np.abs(w[6, :]) - 0.01  # all-negative row
+    idx = np.array([3, 40, 77, 200], dtype=np.int64)
+    packed, scales, pz = O.compute_group32_quant(w, idx)
+    z = O.unpack_zeros(pz, 8)
+    deq = O.dequant_group32(packed, scales, z, out_dtype="float32")
+    assert np.all(deq[:, idx] == 0)
+    ow = w[:, idx].astype(np.float16)
+    sub = O.apply_outlier_columns(O.dequant_group32(packed, scales, z, out_dtype="float16"), idx, ow, "float16")
+    assert np.array_equal(sub[:, idx], ow)
+
+
+# ---------------------------------------------------------------------------
+# nibble layouts and zero-point packing
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("marlin", [True, False])
+def test_pack_roundtrip_all_bytes(marlin):
+    rng = np.random.default_rng(4)
+    q = rng.integers(0, 16, size=(8, 256), dtype=np.uint8)
+    assert np.array_equal(O.unpack_nibbles(O.pack_nibbles(q, marlin), marlin), q)
+    every = np.arange(256, dtype=np.uint8).reshape(2, 128)
+    assert np.array_equal(O.pack_nibbles(O.unpack_nibbles(every, marlin), marlin), every)
+
+
+def test_marlin_byte_contents():
+    # compressor.py:99-102: byte j of a 32-run = q[j] | q[j+16] << 4
+    q = np.arange(64, dtype=np.uint8).reshape(1, 64) % 16
+    q[0, 16:32] = 15 - q[0, 16:32]
+    p = O.pack_nibbles(q, True)
+    for j in range(16):
+        assert p[0, j] == (q[0, j] | (q[0, j + 16] << 4))
+    e = O.pack_nibbles(q, False)
+    for j in range(32):
+        assert e[0, j] == (q[0, 2 * j] | (q[0, 2 * j + 1] << 4))
+
+
+def test_zero_point_packing_odd_groups():
+    z = np.array([[1, 2, 3], [15, 0, 7]], dtype=np.uint8)
+    pz = O.pack_zeros(z)
+    assert pz.shape == (2, 2) and pz[0, 0] == 0x21 and pz[0, 1] == 0x03 and pz[1, 0] == 0x0F
+    assert np.array_equal(O.unpack_zeros(pz, 3), z)
+
+
+# ---------------------------------------------------------------------------
+# Walsh-Hadamard transform (compressor.py:29-42)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("d", [2, 4, 8, 16, 32, 64, 128])
+def test_fwht_matches_dense_sylvester(d):
+    rng = np.random.default_rng(d)
+    x = rng.standard_normal((5, d)).astype(np.float32)
+    H = scipy.linalg.hadamard(d).astype(np.float64)
+    ref = x.astype(np.float64) @ H.T / math.sqrt(d)
+    got = O.fwht(x)
+    assert np.max(np.abs(got - ref)) < 1e-5 * math.sqrt(d)
+
+
+@pytest.mark.parametrize("d", [8, 128])
+def test_fwht_exact_on_integers(d):
+    """Integer inputs: every butterfly is exact, so the unnormalised result is
+    exactly H.x and the normalised one is float32(H.x) / float32(sqrt(d))."""
+    rng = np.random.default_rng(7)
+    x = rng.integers(-50, 50, size=(9, d)).astype(np.float32)
+    H = scipy.linalg.hadamard(d).astype(np.int64)
+    hx = (x.astype(np.int64) @ H.T).astype(np.float32)
+    assert np.array_equal(O.fwht(x, normalize=False), hx)
+    assert np.array_equal(O.fwht(x), hx / np.float32(math.sqrt(d)))
+
+
+def test_fwht_involution_and_blocks():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((3, 512)).astype(np.float32)
+    y = O.rotate_blocks(x, 128)
+    assert np.max(np.abs(O.rotate_blocks(y, 128) - x)) < 1e-5
+    # blocks are independent: perturbing block 2 changes only block 2
+    x2 = x.copy()
+    x2[:, 256:384] += 1.0
+    d = np.abs(O.rotate_blocks(x2, 128) - y)
+    assert d[:, :256].max() == 0 and d[:, 384:].max() == 0 and d[:, 256:384].max() > 0
+    with pytest.raises(ValueError):
+        O.fwht(np.zeros((1, 12), np.float32))
+
+
+def test_fwht_matches_torch_division_semantics():
+    """compressor.py:40-41 divides by the Python float sqrt(d); torch rounds
+    that scalar to float32 and divides -- not a reciprocal multiply."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(64, 128, generator=g)
+    res = x.clone().reshape(-1, 128)
+    h = 1
+    while h < 128:
+        r = res.reshape(-1, 128 // (2 * h), 2, h)
+        res = torch.stack([r[:, :, 0, :] + r[:, :, 1, :], r[:, :, 0, :] - r[:, :, 1, :]], dim=2).reshape(-1, 128)
+        h *= 2
+    res = res / math.sqrt(128)
+    assert np.array_equal(O.fwht(x.numpy()), res.numpy())
+
+
+# ---------------------------------------------------------------------------
+# Format B: NF4 quantizer / dequant
+# ---------------------------------------------------------------------------
+def test_nf4_codebook_shape():
+    c = O.NF4_CODEBOOK
+    assert c.dtype == np.float32 and c.shape == (16,)
+    assert c[0] == -1.0 and c[7] == 0.0 and c[15] == 1.0
+    assert np.all(np.diff(c) > 0)
+
+
+def test_nf4_nearest_code_brute_force():
+    rng = np.random.default_rng(11)
+    r = np.concatenate([rng.uniform(-1.2, 1.2, 200000), O.NF4_CODEBOOK,
+                        (O.NF4_CODEBOOK[1:] + O.NF4_CODEBOOK[:-1]) / 2]).astype(np.float32)
+    q = O.nearest_code(r)
+    d64 = np.abs(O.NF4_CODEBOOK.astype(np.float64)[None, :] - r.astype(np.float64)[:, None])
+    best = d64.min(1)
+    # the chosen code is a nearest code (float32 distance rounding can only
+    # matter when two codes are equidistant within a few ulp)
+    assert np.all(d64[np.arange(r.size), q] <= best + 1e-7)
+    clear = np.sort(d64, 1)[:, 1] - best > 1e-6
+    assert np.array_equal(q[clear], d64.argmin(1)[clear])
+    # monotone in r
+    order = np.argsort(r, kind="stable")
+    assert np.all(np.diff(q[order].astype(int)) >= 0)
+
+
+def test_nf4_code_points_exact():
+    """w = C_i * a reproduces code i, and dequant returns round(C_i * a)."""
+    for a in (np.float16(0.02), np.float16(1.0), np.float16(3.5)):
+        w = (O.NF4_CODEBOOK * np.float32(a)).astype(np.float32)
+        w = np.tile(w, 4).reshape(1, 64)  # one block containing +-1*a -> absmax = a
+        out = O.nf4_quantize(w, w_dtype="float32")
+        assert out["absmax"][0, 0] == a
+        assert np.array_equal(out["codes"][0], np.tile(np.arange(16), 4))
+        deq = O.nf4_dequant(out["packed"], out["absmax"], out_dtype="float32")
+        assert np.array_equal(deq[0], w[0])
+
+
+def test_nf4_zero_block_and_outliers():
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((4, 256)) * 0.02).astype(np.float16)
+    w[1, 64:128] = 0
+    mask = np.zeros((4, 256), bool)
+    mask[0, [3, 100]] = True
+    mask[3, 255] = True
+    w[0, 3] = np.float16(0.7)
+    out = O.nf4_quantize(w, "float16", outlier_mask=mask)
+    assert np.all(out["codes"][1, 64:128] == 7) and out["absmax"][1, 1] == 0
+    assert np.all(out["codes"][mask] == 7)
+    assert out["rowptr"].tolist() == [0, 2, 2, 2, 3]
+    assert out["col"].tolist() == [3, 100, 255]
+    assert out["val"][0] == np.float16(0.7)
+    deq = O.nf4_dequant(out["packed"], out["absmax"], out_dtype="float16",
+                        rowptr=out["rowptr"], col=out["col"], val=out["val"])
+    assert np.array_equal(deq[mask], w[mask])
+    plain = O.nf4_dequant(out["packed"], out["absmax"], out_dtype="float16")
+    assert np.all(plain[mask] == 0)
+
+
+@pytest.mark.parametrize("out_dtype", ["float16", "bfloat16"])
+def test_nf4_dequant_matches_torch_casts(out_dtype):
+    """Library pin for float32 product + RNE cast (torch .to(dtype)), including
+    the oracle's own bfloat16 rounding routine."""
+    rng = np.random.default_rng(13)
+    w = (rng.standard_normal((16, 512)) * 0.05).astype(np.float16)
+    out = O.nf4_quantize(w, "float16", marlin=False)
+    deq = O.nf4_dequant(out["packed"], out["absmax"], marlin=False, out_dtype=out_dtype)
+    codes = torch.from_numpy(O.NF4_CODEBOOK)[torch.from_numpy(out["codes"].astype(np.int64))]
+    a = torch.from_numpy(out["absmax"]).float().repeat_interleave(64, dim=1)
+    t = (codes * a).to(torch.float16 if out_dtype == "float16" else torch.bfloat16)
+    ref = t.numpy() if out_dtype == "float16" else t.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(deq, ref)
+
+
+def test_bf16_rounding_matches_torch():
+    g = torch.Generator().manual_seed(14)
+    x = torch.cat([torch.randn(100000, generator=g) * 10 ** torch.randint(-30, 30, (100000,), generator=g).float(),
+                   torch.tensor([0.0, -0.0, float("inf"), -float("inf"), 3.3895314e38])])
+    ref = x.bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.f32_to_bf16_bits(x.numpy()), ref)
+
+
+def test_nf4_rotation_preserves_product():
+    """Stored weights are W.blockdiag(H); with x rotated the same way the
+    product x.W^T is preserved (H symmetric and involutory)."""
+    rng = np.random.default_rng(15)
+    w = (rng.standard_normal((32, 256)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    wr = O.rotate_blocks(w, 128)
+    y = O.linear_ref(x, "float32", wr, "float32", hadamard_block=128)
+    assert np.max(np.abs(y - x.astype(np.float64) @ w.T.astype(np.float64))) < 1e-5
+
+
+def test_linear_ref_matches_torch():
+    rng = np.random.default_rng(16)
+    x = rng.standard_normal((3, 384)).astype(np.float16)
+    w = (rng.standard_normal((40, 384)) * 0.02).astype(np.float16)
+    b = rng.standard_normal(40).astype(np.float16)
+    y = O.linear_ref(x, "float16", w, "float16", bias=b)
+    t = torch.from_numpy(x).float() @ torch.from_numpy(w).float().T + torch.from_numpy(b).float()
+    assert np.max(np.abs(y - t.double().numpy())) < 1e-4
