@@ -246,10 +246,11 @@ def compute_group32_quant(w: np.ndarray, outlier_idx: Optional[np.ndarray] = Non
 
 
 def format_a_linear_ref(x: np.ndarray, x_dtype: str, w_eff: np.ndarray, bias: Optional[np.ndarray] = None,
-                        bias_dtype: str = "float16") -> np.ndarray:
-    """fp64 reference of ``x @ w_deq.T (+ bias)`` (tests/test_kernels.py:46); returns float64."""
+                        bias_dtype: str = "float16", w_dtype: Optional[str] = None) -> np.ndarray:
+    """fp64 reference of ``x @ w_deq.T (+ bias)`` (tests/test_kernels.py:46); returns float64.
+    ``w_dtype`` defaults to the activation dtype (the reference test's W_eff dtype)."""
     x64 = to_f32(x, x_dtype).astype(np.float64)
-    w64 = to_f32(w_eff, x_dtype).astype(np.float64)
+    w64 = to_f32(w_eff, w_dtype or x_dtype).astype(np.float64)
     y = x64 @ w64.T
     if bias is not None:
         y = y + to_f32(bias, bias_dtype).astype(np.float64)[None, :]

@@ -67,7 +67,10 @@ int ensure_lds_limit(const void* kernel) {
     if (d.first == kernel && d.second == dev) return SPECTRA_OK;
   int max_lds = 0;
   SPECTRA_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
-  SPECTRA_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, max_lds));
+  hipFuncAttributes fa;
+  SPECTRA_HIP_CHECK(hipFuncGetAttributes(&fa, kernel));
+  const int dyn = max_lds - (int)fa.sharedSizeBytes;  // static LDS counts against the same limit
+  SPECTRA_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
   done.emplace_back(kernel, dev);
   return SPECTRA_OK;
 }

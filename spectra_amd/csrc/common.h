@@ -21,11 +21,15 @@ int fail(int status, const std::string& msg);
   do {                                                               \
     if (!(cond)) return ::spectra::fail(SPECTRA_ERR_INVALID, (msg)); \
   } while (0)
+// On failure the runtime's sticky error is read back (cleared) so that it cannot be
+// reported again by an unrelated later call.
 #define SPECTRA_HIP_CHECK(expr)                                                        \
   do {                                                                                 \
     hipError_t e_ = (expr);                                                            \
-    if (e_ != hipSuccess)                                                              \
+    if (e_ != hipSuccess) {                                                            \
+      (void)hipGetLastError();                                                         \
       return ::spectra::fail(SPECTRA_ERR_HIP, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    }                                                                                  \
   } while (0)
 
 // Validates a spectra_qweight_t (shapes, pointers, alignment); returns status.

@@ -3,9 +3,15 @@
 Bars:
   * quantizers, FWHT and W_eff dequant: bit-exact;
   * GEMV / GEMM outputs, fp16: max-abs <= 1e-2 and L2-relative <= 1e-3 against
-    y_ref = fp32(FWHT(x)) @ fp32(W_eff)^T accumulated in float64;
+    y_ref = fp32(FWHT(x)) @ fp32(W_eff)^T accumulated in float64.  Where |y_ref|
+    >= 16 one fp16 output ulp exceeds 1e-2, so the per-element bar is
+    max(1e-2, 1 ulp); the L2-relative bar applies to outputs of >= 64 elements
+    (on a single element it only measures that element's cancellation);
   * bf16 outputs: bf16 rounding alone is ~2^-9 relative, so the bar is max error
-    <= 1 bf16 ulp of |y_ref| (+1e-2 absolute) and L2-relative <= 5e-3.
+    <= 1 bf16 ulp of |y_ref| (+1e-2 absolute) and L2-relative <= 5e-3.  For bf16
+    the reference is the float32 dequant (W_eff in float32), the arithmetic of the
+    reference GEMV itself (kernels.py:73-74): W_eff rounded to bf16 would add a
+    2^-9 weight error that the kernels do not make (they keep >= fp16 precision).
 Every case prints its parameters first so a failure names it.
 """
 import os
@@ -49,13 +55,15 @@ def check_y(y, y_ref, dtype):
     yv = y.detach().float().cpu().double().numpy().reshape(y_ref.shape)
     err = np.abs(yv - y_ref)
     rel = np.linalg.norm(yv - y_ref) / max(np.linalg.norm(y_ref), 1e-30)
+    big = y_ref.size >= 64
     if dtype == torch.float16:
-        assert err.max() <= 1e-2, f"max-abs {err.max()}"
-        assert rel <= 1e-3, f"rel-L2 {rel}"
+        ulp = np.spacing(np.abs(y_ref).astype(np.float16)).astype(np.float64)
+        assert np.all(err <= np.maximum(1e-2, ulp)), f"max-abs {err.max()} (excess over bar {np.max(err - np.maximum(1e-2, ulp))})"
+        assert not big or rel <= 1e-3, f"rel-L2 {rel}"
     else:
         ulp = np.abs(O.bf16_bits_to_f32(O.f32_to_bf16_bits(y_ref.astype(np.float32)))).astype(np.float64) * 2.0 ** -7
         assert np.all(err <= ulp + 1e-2), f"max excess {np.max(err - ulp)}"
-        assert rel <= 5e-3, f"rel-L2 {rel}"
+        assert not big or rel <= 5e-3, f"rel-L2 {rel}"
     return err.max(), rel
 
 
@@ -159,17 +167,18 @@ def test_dequant_format_b_bitexact(hip, out_dt):
 # ---------------------------------------------------------------------------
 # Format A GEMV / GEMM (the reference's own test cases, tests/test_kernels.py:43-70)
 # ---------------------------------------------------------------------------
-def _format_a(seed, n, k, n_out, act="float16"):
+def _format_a(seed, n, k, n_out, act="float16", ref_dtype=None):
     rng = np.random.default_rng(seed)
     w = rand_np(rng, (n, k), 1.0)
     idx = np.sort(rng.permutation(k)[:n_out]).astype(np.int64) if n_out else None
     packed, scales, pz = O.compute_group32_quant(w.astype(np.float32), idx)
     z = O.unpack_zeros(pz, k // 32)
-    w_deq = O.dequant_group32(packed, scales, z, True, act)
+    rd = ref_dtype or act
+    w_deq = O.dequant_group32(packed, scales, z, True, rd)
     ow = None
     if n_out:
         ow = w[:, idx] if act == "float16" else O.round_to(w[:, idx].astype(np.float32), act)
-        w_deq = O.apply_outlier_columns(w_deq, idx, ow, act)
+        w_deq = O.apply_outlier_columns(w_deq, idx, ow, rd)
     return packed, scales, z, idx, ow, w_deq
 
 
@@ -179,11 +188,12 @@ def _format_a(seed, n, k, n_out, act="float16"):
 def test_format_a_reference_cases(hip, act, m, n_out):
     case(act=act, m=m, n_out=n_out)
     packed, scales, z, idx, ow, w_deq = _format_a(42, 128, 256, n_out, act)
+    w_ref = w_deq if act == "float16" else _format_a(42, 128, 256, n_out, act, ref_dtype="float32")[-1]
     rng = np.random.default_rng(m)
     x = rand_np(rng, (m, 256), 1.0, np.float32)
     x = O.round_to(x, act)
     xt = cuda(x, TDT[act])
-    y_ref = O.format_a_linear_ref(x, act, w_deq)
+    y_ref = O.format_a_linear_ref(x, act, w_ref, w_dtype="float16" if act == "float16" else "float32")
     kw = dict(outlier_idx=cuda(idx) if n_out else None, outlier_w=cuda(ow, TDT[act]) if n_out else None,
               marlin_layout=True)
     if m == 1:
@@ -191,8 +201,9 @@ def test_format_a_reference_cases(hip, act, m, n_out):
     else:
         y = K.batched_w4a16_gemm(xt, cuda(packed), cuda(scales), cuda(z), **kw)
     assert y.dtype == TDT[act] and y.shape == (m, 128)
-    # the reference's own bar (tests/test_kernels.py:48-49) ...
-    assert np.abs(y.float().cpu().double().numpy() - y_ref).max() <= 0.05
+    # the reference's own bar (tests/test_kernels.py:48-49; it tests fp16 only) ...
+    if act == "float16":
+        assert np.abs(y.float().cpu().double().numpy() - y_ref).max() <= 0.05
     # ... and this build's
     check_y(y, y_ref, TDT[act])
 
@@ -241,10 +252,11 @@ def _format_b(seed, n, k, had, ratio=0.005, marlin=True, scale=0.02):
 def test_format_b_gemv(hip, act, m, had, marlin):
     case(act=act, m=m, had=had, marlin=marlin)
     q, rng = _format_b(m * 3 + had + marlin, 257, 3072, had, marlin=marlin)
-    w_eff = O.nf4_dequant(q["packed"], q["absmax"], marlin, act, q["rowptr"], q["col"], q["val"])
+    rd = act if act == "float16" else "float32"
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], marlin, rd, q["rowptr"], q["col"], q["val"])
     x = O.round_to(rand_np(rng, (m, 3072), 1.0, np.float32), act)
     b = rand_np(rng, (257,), 0.1)
-    y_ref = O.linear_ref(x, act, w_eff, act, hadamard_block=had, bias=b)
+    y_ref = O.linear_ref(x, act, w_eff, rd, hadamard_block=had, bias=b)
     y = K.fused_w4a16_gemv_hdsq(cuda(x, TDT[act]), cuda(q["packed"]), cuda(q["absmax"]), None, bias=cuda(b),
                                 outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]), marlin_layout=marlin,
                                 codebook="nf4", group_size=64, hadamard_block=had, outlier_rowptr=cuda(q["rowptr"]))
@@ -279,9 +291,10 @@ def test_format_b_gemm(hip, act, m):
     case(act=act, m=m)
     n, k = 320, 2048
     q, rng = _format_b(m, n, k, 128, ratio=0.01)
-    w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, act, q["rowptr"], q["col"], q["val"])
+    rd = act if act == "float16" else "float32"
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, rd, q["rowptr"], q["col"], q["val"])
     x = O.round_to(rand_np(rng, (m, k), 1.0, np.float32), act)
-    y_ref = O.linear_ref(x, act, w_eff, act, hadamard_block=128)
+    y_ref = O.linear_ref(x, act, w_eff, rd, hadamard_block=128)
     y = K.batched_w4a16_gemm(cuda(x, TDT[act]), cuda(q["packed"]), cuda(q["absmax"]), None,
                              outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]), marlin_layout=True, codebook="nf4",
                              hadamard_block=128, outlier_rowptr=cuda(q["rowptr"]))
@@ -345,6 +358,7 @@ def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
         case(name=name, m=m)
         x = (torch.randn(m, k, generator=g)).half()
         y_ref = O.linear_ref(x.numpy(), "float16", w_eff, "float16", hadamard_block=had)
+        q.hadamard_block = had  # the synthetic matrix is the stored (rotated-basis) weight
         kw = q.kernel_kwargs()
         col, val = q.outliers()
         fn = K.fused_w4a16_gemv_hdsq if m <= 4 else K.batched_w4a16_gemm
@@ -368,7 +382,7 @@ def test_prefill_gemm_against_torch_fp32(hip):
     x = torch.randn(m, k, generator=g).bfloat16().cuda()
     y = K.batched_w4a16_gemm(x, q.packed, q.absmax, None, outlier_idx=q.col, outlier_w=q.val, marlin_layout=True,
                              **q.kernel_kwargs() | dict(hadamard_block=128))
-    w_eff = K.w4_dequant(q.packed, q.absmax, None, out_dtype=torch.bfloat16, codebook="nf4", marlin_layout=True,
+    w_eff = K.w4_dequant(q.packed, q.absmax, None, out_dtype=torch.float32, codebook="nf4", marlin_layout=True,
                          outlier_idx=q.col, outlier_w=q.val, outlier_rowptr=q.rowptr)
     x_rot = K.fwht_rows(x, 128, out_dtype=torch.float32)
     y_t = (x_rot @ w_eff.float().T).double().cpu().numpy()
