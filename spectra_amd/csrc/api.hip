@@ -57,7 +57,7 @@ int validate_qweight(const spectra_qweight_t* w) {
   return SPECTRA_OK;
 }
 
-int ensure_lds_limit(const void* kernel) {
+int ensure_lds_limit(const void* kernel, bool dyn_at_zero) {
   static std::mutex mu;
   static std::vector<std::pair<const void*, int>> done;
   int dev = 0;
@@ -69,6 +69,8 @@ int ensure_lds_limit(const void* kernel) {
   SPECTRA_HIP_CHECK(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev));
   hipFuncAttributes fa;
   SPECTRA_HIP_CHECK(hipFuncGetAttributes(&fa, kernel));
+  if (dyn_at_zero && fa.sharedSizeBytes != 0)  // the kernel addresses its dynamic LDS from 0
+    return fail(SPECTRA_ERR_UNSUPPORTED, "kernel was built with static LDS; its LDS layout needs none");
   const int dyn = max_lds - (int)fa.sharedSizeBytes;  // static LDS counts against the same limit
   SPECTRA_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, dyn));
   done.emplace_back(kernel, dev);

@@ -35,7 +35,8 @@ int fail(int status, const std::string& msg);
 // Validates a spectra_qweight_t (shapes, pointers, alignment); returns status.
 int validate_qweight(const spectra_qweight_t* w);
 // Raises a kernel's dynamic-LDS limit to the device maximum once per (kernel, device).
-int ensure_lds_limit(const void* kernel);
+// dyn_at_zero: the kernel addresses dynamic LDS from address 0 (fails if it has static LDS).
+int ensure_lds_limit(const void* kernel, bool dyn_at_zero = false);
 inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,687 @@
+// Decode GEMV family for gfx950: out[m, :] = FWHT(x[m, :]) . W_eff^T + bias, m <= 4.
+//
+// Replaces the reference's single-row Triton GEMV (kernels.py:16-184).  Design:
+//  * Workgroup = S x G waves (at most 8).  S = ceil(K / 2048) K-slices; G row groups.  A wave
+//    owns one slice (each lane 32 k = 16 packed bytes, one dwordx4) of RPW rows.  All weight
+//    loads of a wave are issued up front, after the activation loads, so waiting for x
+//    never waits for the weight stream (vmcnt counts in issue order).
+//  * VALU is the scarce resource while the stream is in flight, so every setup step is
+//    sized per element, never per wave:
+//    - activations: each thread owns half of a 32-element run of x (16 values), so every
+//      wave shares the work: butterfly stages on register bits in registers, the stages
+//      across lanes as one v_fmac_f32 with a DPP-permuted source per value (lanes of a
+//      Hadamard block are numbered in a reflected order so that the quad permutes and
+//      the half-row / row mirrors pair exactly the lanes each stage needs; the high side
+//      of a cross-lane butterfly keeps the negated difference and the lane's sign is
+//      applied with the run scale); the run is scaled by its own power of two
+//      (max |x| -> [2^14, 2^15)), rounded to fp16 and stored in LDS in "pair order" (the
+//      two k's of packed byte j side by side) with the run's inverse scale beside it; the
+//      1/sqrt(block) normalisation is applied once per output.
+//    - nibble decode: a 256-entry LUT in LDS maps a packed byte to the fp16 pair
+//      (code[lo], code[hi]) -- NF4 levels for Format B, the integers 0..15 for Format A.
+//      It is replicated per lane (64 KB) so that lane l always reads bank l: the LDS
+//      address is (byte << 8) | (lane << 2), built by one v_perm_b32.  Each wave fills
+//      its share from a 16-entry table it wrote itself (no barrier, no select chains).
+//  * Math per packed byte: v_perm + ds_read_b32 + v_dot2_f32_f16.  Scales are applied once
+//    per 32 k: Format B acc * absmax * run_scale; Format A (acc - z * sum(x)) * s * run_scale.
+//  * Lane partials of all rows are reduced across the wave with a transposed halving
+//    reduction; per-row totals (slices, outliers, bias) are reduced by one wave per row in
+//    a fixed order: the result is deterministic run to run.
+#pragma once
+
+#include "common.h"
+
+namespace spectra {
+
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kRpwMax = 12;  // rows per wave held in registers
+constexpr int kLutBytes = 65536;
+constexpr int kMaxWaves = 8;
+
+struct GemvParams {
+  const uint8_t* packed;
+  int64_t ldp;
+  const uint16_t* scales;
+  int64_t lds;
+  const uint8_t* zeros;
+  int64_t ldz;
+  const int64_t* oidx;
+  const void* ow;
+  int64_t ldow;
+  const int32_t* rowptr;
+  const int32_t* ccol;
+  const uint16_t* cval;
+  const void* bias;
+  const void* x;
+  int64_t ldx;
+  void* out;
+  int64_t ldo;
+  int n, k, m;
+  int gshift;  // log2(group / block size)
+  int had, log_had, marlin;
+  int okind, n_out, ow_dt, bias_dt, act_dt;
+  int csr_nnz;
+  int R, S, G, ocap;
+  uint32_t off_xp, off_xsc, off_part, off_codes, off_rp, off_bias, off_oprod;
+  float out_scale;  // 1/sqrt(hadamard_block) (1 without rotation)
+  float inv_n_out;  // 1/n_out (dense outlier columns)
+};
+
+__device__ __forceinline__ uint16_t nf4_f16_bits(int i) {
+  // fp16 roundings of the NF4 levels (compressor.py:22-27)
+  uint16_t r = 0xbc00;
+  r = (i == 1) ? 0xb992 : r;
+  r = (i == 2) ? 0xb833 : r;
+  r = (i == 3) ? 0xb652 : r;
+  r = (i == 4) ? 0xb48d : r;
+  r = (i == 5) ? 0xb1ea : r;
+  r = (i == 6) ? 0xadd4 : r;
+  r = (i == 7) ? 0x0000 : r;
+  r = (i == 8) ? 0x2d18 : r;
+  r = (i == 9) ? 0x3126 : r;
+  r = (i == 10) ? 0x33e0 : r;
+  r = (i == 11) ? 0x3568 : r;
+  r = (i == 12) ? 0x370d : r;
+  r = (i == 13) ? 0x3880 : r;
+  r = (i == 14) ? 0x39c9 : r;
+  r = (i == 15) ? 0x3c00 : r;
+  return r;
+}
+
+__device__ __forceinline__ float pow2f(int e) {  // e in [-126, 127]
+  return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
+}
+
+// fp16 position of element k inside one activation row of xp: run q = k / 32 holds 16
+// (lo, hi) pairs (pair j = (k_j, k_j + 16) for the marlin nibble order, (2j, 2j+1)
+// otherwise) in 4 16-byte chunks stored at [slice q / 64][chunk][lane q % 64]
+__device__ __forceinline__ int xp_pos(int k, int marlin) {
+  const int q = k >> 5, e = k & 31;
+  const int j = marlin ? (e & 15) : (e >> 1), half = marlin ? (e >> 4) : (e & 1);
+  return ((((q >> 6) * 4 + (j >> 2)) * 64 + (q & 63)) * 4 + (j & 3)) * 2 + half;
+}
+
+// value of lane (lane ^ MASK): DPP quad permutes for 1 and 2, ds_swizzle (xor mode, no
+// address register) for 4..16, a cross-lane permute for 32
+template <int MASK>
+__device__ __forceinline__ float lane_xor_c(float v) {
+  const int iv = __builtin_bit_cast(int, v);
+  if constexpr (MASK == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+  else if constexpr (MASK == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+  else if constexpr (MASK < 32) return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, (MASK << 10) | 0x1F));
+  else return __shfl_xor(v, MASK, 64);
+}
+
+// Transposed halving reduction of N values per lane across the 64 lanes: at the step
+// with offset OFF the lanes with bit OFF set keep the upper half of their values and add
+// their partner's upper half (the others the lower half), so N values cost N-1 exchanges
+// instead of 6N.  Offsets go 1, 2, 4, ... so the steps that move the most values use the
+// cheap DPP permutes.  At the end every lane holds the total number idx(lane).
+template <int N, int OFF>
+__device__ __forceinline__ void transposed_reduce(float* vals, int lane, int& idx) {
+  if constexpr (OFF <= 32) {
+    if constexpr (N > 1) {
+      constexpr int H = N / 2;
+      const bool upper = (lane & OFF) != 0;
+#pragma unroll
+      for (int q = 0; q < H; ++q) {
+        const float send = upper ? vals[q] : vals[q + H];
+        const float keep = upper ? vals[q + H] : vals[q];
+        vals[q] = keep + lane_xor_c<OFF>(send);
+      }
+      if (upper) idx += H;
+      transposed_reduce<H, OFF * 2>(vals, lane, idx);
+    } else {
+      vals[0] += lane_xor_c<OFF>(vals[0]);
+      transposed_reduce<1, OFF * 2>(vals, lane, idx);
+    }
+  }
+}
+
+// Lane j of a Hadamard block of 2^b lanes holds logical chunk reflect_chunk(j, b):
+// identity inside a quad, and for a top bit t >= 2 the chunk of the mirrored lane
+// (2^(t+1) - 1 - j) with bit t set.  With this numbering lane-logical bit 0/1 pairs the
+// lanes of DPP quad_perm [1,0,3,2] / [2,3,0,1], bit 2 the lanes of row_half_mirror, bit 3
+// those of row_mirror and bit 4 those of a 32-lane mirror (j <-> 31 - j).
+__device__ __forceinline__ int reflect_chunk(int j, int b) {
+  int out = 0;
+#pragma unroll
+  for (int t = 4; t >= 2; --t) {
+    if (t < b && ((j >> t) & 1)) {
+      out |= 1 << t;
+      j ^= (1 << t) - 1;
+    }
+    j &= (1 << t) - 1;
+  }
+  return out | j;
+}
+
+// Butterfly on register bit RB of the 16 values of a thread (stage pairs (u, v) ->
+// (u + v, u - v), compressor.py:34-39).
+template <int RB>
+__device__ __forceinline__ void fly_in(float (&v)[16]) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    if ((r & (1 << RB)) == 0) {
+      const float a = v[r], b = v[r | (1 << RB)];
+      v[r] = a + b;
+      v[r | (1 << RB)] = a - b;
+    }
+  }
+}
+
+#define SPECTRA_XFLY(CTRL)                                                                      \
+  asm volatile("s_nop 1\n"                                                                      \
+               "v_fmac_f32_dpp %0, %0, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %1, %1, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %2, %2, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %3, %3, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %4, %4, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %5, %5, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %6, %6, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %7, %7, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %8, %8, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %9, %9, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"              \
+               "v_fmac_f32_dpp %10, %10, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"            \
+               "v_fmac_f32_dpp %11, %11, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"            \
+               "v_fmac_f32_dpp %12, %12, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"            \
+               "v_fmac_f32_dpp %13, %13, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"            \
+               "v_fmac_f32_dpp %14, %14, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"            \
+               "v_fmac_f32_dpp %15, %15, %16 " CTRL " row_mask:0xf bank_mask:0xf\n"            \
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),        \
+                 "+v"(v[6]), "+v"(v[7]), "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]),      \
+                 "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15])                             \
+               : "v"(c))
+
+// Butterfly across the lanes on lane-logical bit KB: v += c * v(partner) with c = +1 on
+// the low side and -1 on the high side, which leaves u + v on the low side and
+// -(u - v) on the high side (the product by +-1 is exact and the fma rounds once, as
+// the reference's add/subtract does).  Partners carry equal signs before every stage
+// (they differ only in bit KB), so the lane's sign after all stages is
+// (-1)^popcount(chunk bits).  The DPP source needs two wait states after the VALU write
+// that produced it: the s_nop 1 at the head of the block provides them.
+template <int KB>
+__device__ __forceinline__ void fly_x(float (&v)[16], float c) {
+  if constexpr (KB == 0) SPECTRA_XFLY("quad_perm:[1,0,3,2]");
+  else if constexpr (KB == 1) SPECTRA_XFLY("quad_perm:[2,3,0,1]");
+  else if constexpr (KB == 2) SPECTRA_XFLY("row_half_mirror");
+  else if constexpr (KB == 3) SPECTRA_XFLY("row_mirror");
+  else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {  // lane j <-> 31 - j: ds_swizzle xor 0x1F
+      const float o = __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v[r]), 0x7C1F));
+      v[r] = __builtin_fmaf(o, c, v[r]);
+    }
+  }
+}
+
+// fwht_half for a block size known at compile time: straight-line, no stage branches
+template <int LOG, bool MAR>
+__device__ __forceinline__ void fwht_half_t(float (&v)[16], int cl) {
+  const auto sgn = [&](int kb) { return ((cl >> kb) & 1) ? -1.0f : 1.0f; };
+  if constexpr (LOG > 0) fly_in<0>(v);
+  if constexpr (LOG > 1) fly_in<1>(v);
+  if constexpr (LOG > 2) fly_in<2>(v);
+  if constexpr (MAR) {
+    if constexpr (LOG > 3) fly_x<0>(v, sgn(0));
+    if constexpr (LOG > 4) fly_in<3>(v);
+  } else {
+    if constexpr (LOG > 3) fly_in<3>(v);
+    if constexpr (LOG > 4) fly_x<0>(v, sgn(0));
+  }
+  if constexpr (LOG > 5) fly_x<1>(v, sgn(1));
+  if constexpr (LOG > 6) fly_x<2>(v, sgn(2));
+  if constexpr (LOG > 7) fly_x<3>(v, sgn(3));
+  if constexpr (LOG > 8) fly_x<4>(v, sgn(4));
+}
+
+// Blockwise FWHT (block 2^log_had) of the 16 values of a half-run, in the reference's
+// stage order h = 1, 2, 4, ... (compressor.py:34-39).  Element e of the 32-run sits in
+// register r of half `hf`: plain order e = 16 hf + r (stages h = 1..8 on register bits,
+// h = 16 across the half pair); marlin order e = (r & 7) + 8 hf + 16 (r >> 3) (h = 1..4
+// and 16 on register bits, h = 8 across the half pair).  h >= 32 runs across the lanes
+// of the block.  `cl` is the lane's logical chunk inside its block (bit 0 = hf).
+__device__ __forceinline__ void fwht_half(float (&v)[16], int log_had, bool marlin, int cl) {
+  const auto sgn = [&](int kb) { return ((cl >> kb) & 1) ? -1.0f : 1.0f; };
+  if (log_had > 0) fly_in<0>(v);
+  if (log_had > 1) fly_in<1>(v);
+  if (log_had > 2) fly_in<2>(v);
+  if (marlin) {
+    if (log_had > 3) fly_x<0>(v, sgn(0));
+    if (log_had > 4) fly_in<3>(v);
+  } else {
+    if (log_had > 3) fly_in<3>(v);
+    if (log_had > 4) fly_x<0>(v, sgn(0));
+  }
+  if (log_had > 5) fly_x<1>(v, sgn(1));
+  if (log_had > 6) fly_x<2>(v, sgn(2));
+  if (log_had > 7) fly_x<3>(v, sgn(3));
+  if (log_had > 8) fly_x<4>(v, sgn(4));
+}
+
+// Sum over the 64 lanes with DPP only (no LDS): quad permutes, half-row and row mirrors,
+// then row broadcasts; the total ends in lane 63 and is read back as a scalar.
+__device__ __forceinline__ float wave_sum(float v) {
+  int t;
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  v += __builtin_bit_cast(float, t);
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  v += __builtin_bit_cast(float, t);
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false);  // row_half_mirror
+  v += __builtin_bit_cast(float, t);
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false);  // row_mirror
+  v += __builtin_bit_cast(float, t);
+  t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_bit_cast(float, t);
+  t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false);  // row_bcast:31
+  v += __builtin_bit_cast(float, t);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+template <int FMT, int MT, int RPW, bool BF>
+__global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int XH = 2 * MT;  // 16-element half-runs of activations per thread (at most)
+  const int tid = threadIdx.x;
+  const int BD = 64 * p.S * p.G;  // == blockDim.x (the launch uses S x G waves), without the implicit-argument load
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nwaves = BD >> 6;
+  const int s = wave % p.S, g = wave / p.S;
+  const int r0 = blockIdx.x * p.R;
+  const int Rw = min(p.R, p.n - r0);
+  const int K = p.k;
+  const int qpr = K >> 5;  // 32-element runs per activation row
+  // every argument the prologue needs, fetched in one round trip before the first load
+  asm volatile("" ::"s"(p.x), "s"(p.ldx), "s"(p.packed), "s"(p.ldp), "s"(p.scales), "s"(p.lds), "s"(p.m),
+               "s"(p.gshift), "s"(p.log_had), "s"(p.marlin), "s"(p.zeros), "s"(p.ldz), "s"(p.rowptr), "s"(p.okind), "s"(p.bias), "s"(p.bias_dt));
+
+  // ---------------- (1) activation runs and CSR row pointers: raw bits, issued first ----------------
+  // half-run hr = tid + i * BD of the MT x (K / 16) half-runs; inside a Hadamard block of
+  // 2^bL lanes the lane holds logical chunk reflect_chunk (bit 0 = which half of its run)
+  const int hpr = K >> 4;  // half-runs per activation row
+  const int bL = p.log_had >= 5 ? p.log_had - 4 : (p.marlin && p.log_had == 4 ? 1 : 0);
+  uint4 xr[XH][2];
+  int xm[XH], xq[XH], xcl[XH], xhf[XH];
+#pragma unroll
+  for (int i = 0; i < XH; ++i) {
+    const int hd = tid + i * BD;
+    int m = 0;
+#pragma unroll
+    for (int mm = 1; mm < MT; ++mm) m += hd >= mm * hpr ? 1 : 0;
+    const int hrr = hd - m * hpr;
+    const int bm = (1 << bL) - 1;
+    const int cl = (hrr & ~bm) | reflect_chunk(hrr & bm, bL);
+    xm[i] = m;
+    xq[i] = cl >> 1;
+    xcl[i] = cl & bm;  // the bits of the cross-lane stages (their signs)
+    const int hf = cl & 1;
+    xhf[i] = hf;
+    // padded rows (m >= p.m) and slots past the last half-run read row 0: finite values
+    // whose results are never stored
+    const bool ok = hd < MT * hpr && m < p.m;
+    const uint16_t* src = (const uint16_t*)p.x + (ok ? (int64_t)m * p.ldx + (int64_t)(cl >> 1) * 32 : 0);
+    // waves with no half-run in this slot skip its loads (a wave-uniform branch; the
+    // loads come before every other load, so later wait counts are unaffected)
+    if (i == 0 || wave * 64 + i * BD < MT * hpr) {
+      xr[i][0] = *(const uint4*)(src + (p.marlin ? 8 * hf : 16 * hf));
+      xr[i][1] = *(const uint4*)(src + (p.marlin ? 16 + 8 * hf : 16 * hf + 8));
+    } else {
+      xr[i][0] = xr[i][1] = make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // CSR row pointers, issued before the weights: the outlier loads need e0 before the
+  // stream has arrived (the wait counts are in issue order)
+  int rp_v = 0, e0 = 0, e1 = 0;
+  if (p.okind == SPECTRA_OUTLIERS_CSR) {
+    rp_v = p.rowptr[r0 + min(tid, Rw)];
+    e0 = p.rowptr[r0];
+    e1 = p.rowptr[r0 + Rw];
+  }
+
+  // ---------------- (2) the weight stream: every row of this wave, up front ----------------
+  const int kb = s * 2048 + lane * 32;  // first k of this lane (one 32-run)
+  const bool kvalid = kb < K;
+  uint4 wq[RPW];
+  uint16_t sc[RPW];
+  uint8_t zq[RPW];
+  bool wok[RPW];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int rl = g + i * p.G;
+    // the row is wave-uniform (its address is scalar arithmetic); only k is per lane
+    const bool rok = rl < Rw;
+    wok[i] = rok && kvalid;
+    const int64_t row = r0 + (rok ? rl : 0);
+    const int kk = kvalid ? kb : 0;
+    wq[i] = *(const uint4*)(p.packed + row * p.ldp + (kk >> 1));
+    sc[i] = p.scales[row * p.lds + (kk >> p.gshift)];
+    if (FMT == SPECTRA_FMT_ASYM_G32) zq[i] = p.zeros[row * p.ldz + (kk >> 5)];
+  }
+
+  // ---------------- (2b) bias: consumed after the stream ----------------
+  uint32_t bias_raw = 0;
+  if (p.bias != nullptr) {
+    const int64_t bi = r0 + (tid < Rw ? tid : 0);
+    if (p.bias_dt == SPECTRA_F32) bias_raw = ((const uint32_t*)p.bias)[bi];
+    else bias_raw = ((const uint16_t*)p.bias)[bi];
+  }
+
+  // ---------------- (3) nibble-pair LUT from a wave-private 16-entry code table ----------------
+  {
+    uint16_t* codes = (uint16_t*)(smem + p.off_codes) + wave * 16;
+    if (lane < 16) codes[lane] = FMT == SPECTRA_FMT_NF4 ? nf4_f16_bits(lane) : f2h((float)lane);
+    // 64 wave-instructions of 1 KB fill the 64 KB: instruction i writes rows
+    // v = 16 (i >> 2) + 4 (i & 3) + (lane >> 4), lane & 15 picking the 16-byte chunk (4
+    // consecutive rows, conflict-free).  All code reads of a batch are issued before the
+    // first store, so the batch waits for LDS once.
+    uint4* lut = (uint4*)smem;
+    for (int i0 = wave; i0 < 64; i0 += 8 * nwaves) {
+      uint32_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j * nwaves < 64 ? i0 + j * nwaves : 0;
+        e[j] = (uint32_t)codes[4 * (i & 3) + (lane >> 4)] | ((uint32_t)codes[i >> 2] << 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j * nwaves;
+        if (i < 64) lut[(16 * (i >> 2) + 4 * (i & 3) + (lane >> 4)) * 16 + (lane & 15)] = make_uint4(e[j], e[j], e[j], e[j]);
+      }
+    }
+  }
+
+  // ---------------- (4) activation half-runs: FWHT, run scale, fp16 pairs -> LDS ----------------
+  uint16_t* xp = (uint16_t*)(smem + p.off_xp);
+  const int XS = ((K + 2047) >> 11) << 11;  // xp row stride: whole 2048-element slices
+  float* xsc = (float*)(smem + p.off_xsc);
+#pragma unroll
+  for (int i = 0; i < XH; ++i) {
+    // wave-uniform guard: the cross-lane stages need every lane of the wave
+    if (wave * 64 + i * BD >= MT * hpr) break;
+    float v[16];
+    const uint32_t u[8] = {xr[i][0].x, xr[i][0].y, xr[i][0].z, xr[i][0].w,
+                           xr[i][1].x, xr[i][1].y, xr[i][1].z, xr[i][1].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (BF) {
+        v[2 * e] = __builtin_bit_cast(float, u[e] << 16);
+        v[2 * e + 1] = __builtin_bit_cast(float, u[e] & 0xffff0000u);
+      } else {
+        v[2 * e] = h2f((uint16_t)u[e]);
+        v[2 * e + 1] = h2f((uint16_t)(u[e] >> 16));
+      }
+    }
+    const bool mar = p.marlin != 0;
+    // straight-line code for the common blocks (none, 128), stage branches otherwise
+    if (p.log_had == 7) {
+      if (mar) fwht_half_t<7, true>(v, xcl[i]);
+      else fwht_half_t<7, false>(v, xcl[i]);
+    } else if (p.log_had != 0) {
+      fwht_half(v, p.log_had, mar, xcl[i]);
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fabsf(v[r]));
+    mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, mx), 0xB1, 0xF, 0xF,
+                                                                       false)));  // the other half of the run
+    const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
+    const int eb = (int)(bits >> 23);
+    const int E = eb == 0 ? -126 : eb - 127;   // floor(log2(mx)) for normal mx
+    int F = bits == 0 ? 0 : 14 - E;            // mx * 2^F in [2^14, 2^15)
+    F = F < -126 ? -126 : (F > 126 ? 126 : F);
+    // the lane's butterfly sign rides on the (exact) power-of-two scale
+    const float f = (__builtin_popcount(xcl[i]) & 1) ? -pow2f(F) : pow2f(F);
+    uint32_t d[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {  // pair j of this half: plain (2j, 2j+1), marlin (j, j+8)
+      const float lo = mar ? v[j] : v[2 * j], hi = mar ? v[j + 8] : v[2 * j + 1];
+      d[j] = (uint32_t)f2h(lo * f) | ((uint32_t)f2h(hi * f) << 16);
+    }
+    if (tid + i * BD < MT * hpr) {
+      // run q is consumed by lane q % 64 of slice q / 64: 4 16-byte chunks at
+      // [m][slice][chunk][lane] (each ds_read_b128 of the stream reads 1 KB contiguous);
+      // half hf of the run owns chunks 2 hf and 2 hf + 1
+      const int q = xq[i], hf = xhf[i];
+      uint4* dst = (uint4*)(xp + xm[i] * XS) + ((q >> 6) * 4 + 2 * hf) * 64 + (q & 63);
+      dst[0] = make_uint4(d[0], d[1], d[2], d[3]);
+      dst[64] = make_uint4(d[4], d[5], d[6], d[7]);
+      if (hf == 0) xsc[xm[i] * qpr + q] = pow2f(-F);
+    }
+  }
+
+  // ---------------- (5) outlier entries of this workgroup (consumed after the stream) ----------------
+  // entries el < olim have their products staged in LDS; the rest (beyond the LDS share,
+  // or in a partial last CSR group of 4) are read from the side tensors per row
+  const int olim = p.okind == SPECTRA_OUTLIERS_CSR ? min(p.ocap, (p.csr_nnz & ~3) - e0) : p.ocap;
+  // raw bits, one load pair per thread, branch-free (the wait counts never branch).
+  // CSR: four consecutive entries per thread from the 4-aligned entry below e0 (one
+  // dwordx4 of columns, one dwordx2 of fp16 values; entry e covers el = e - e0).
+  // Dense columns: entry el = tid, row el / n_out, column el % n_out.
+  int ocol[4];
+  uint32_t oraw[4];
+  int obase;  // el of this thread's first entry
+  {
+    const bool has_o = p.okind != SPECTRA_OUTLIERS_NONE;
+    const bool csr = p.okind == SPECTRA_OUTLIERS_CSR;
+    const int n_out = p.n_out > 0 ? p.n_out : 1;
+    // (row, column) of a dense-column entry: float reciprocal, exact after one correction
+    const int ei = tid < Rw * n_out ? tid : 0;
+    int r = (int)((float)ei * p.inv_n_out);
+    int jj = ei - r * n_out;
+    r = jj < 0 ? r - 1 : (jj >= n_out ? r + 1 : r);
+    jj = ei - r * n_out;
+    const int b4 = e0 & ~3;
+    const int g4 = b4 + 4 * tid;
+    // CSR groups that would run past the array end re-read group 0 (entries of a partial
+    // last group are read in the per-row phase); without outliers the loads read the
+    // first bytes of the packed tensor
+    const int gc = g4 + 4 <= p.csr_nnz ? g4 : 0;
+    const int4* cptr = !has_o ? (const int4*)p.packed
+                              : (csr ? (const int4*)(p.ccol + gc) : (const int4*)(p.oidx + jj));
+    const uint2* vptr = !has_o ? (const uint2*)p.packed
+                               : (csr ? (const uint2*)(p.cval + gc)
+                                      : (const uint2*)((const uint16_t*)p.ow + (int64_t)(r0 + r) * p.ldow + jj));
+    if (csr || !has_o) {
+      const int4 c = *cptr;
+      const uint2 v = *vptr;
+      ocol[0] = c.x; ocol[1] = c.y; ocol[2] = c.z; ocol[3] = c.w;
+      oraw[0] = v.x & 0xffffu; oraw[1] = v.x >> 16; oraw[2] = v.y & 0xffffu; oraw[3] = v.y >> 16;
+      obase = g4 - e0;
+    } else {  // dense: the same two loads, one entry (the low dword of idx, the 16-bit weight)
+      const int c = *(const int*)cptr;
+      const uint32_t v = *(const uint16_t*)vptr;
+      ocol[0] = c; ocol[1] = ocol[2] = ocol[3] = 0;
+      oraw[0] = v; oraw[1] = oraw[2] = oraw[3] = 0;
+      obase = tid;
+    }
+  }
+
+  __syncthreads();  // --- barrier 1: LUT, activation pairs and run scales
+
+  // ---------------- (6) this lane's activation pairs and run scales ----------------
+  uint32_t xpair[MT][16];
+  float xs[MT], xsum[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    const int kk = kvalid ? kb : 0;
+    const int q = kk >> 5;  // this lane's run: lane (q & 63) of slice s
+    const uint4* src = (const uint4*)(xp + m * XS) + ((q >> 6) * 4) * 64 + (q & 63);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 a = src[64 * c];
+      xpair[m][4 * c] = a.x; xpair[m][4 * c + 1] = a.y; xpair[m][4 * c + 2] = a.z; xpair[m][4 * c + 3] = a.w;
+    }
+    xs[m] = xsc[m * qpr + (kk >> 5)];
+    xsum[m] = 0.0f;
+    if (FMT == SPECTRA_FMT_ASYM_G32) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        xsum[m] += h2f((uint16_t)xpair[m][q]) + h2f((uint16_t)(xpair[m][q] >> 16));
+    }
+  }
+
+  // ---------------- (7) the stream: LUT decode + dot2 per packed byte ----------------
+  constexpr int V = RPW * MT;
+  constexpr int VP = V <= 1 ? 1 : V <= 2 ? 2 : V <= 4 ? 4 : V <= 8 ? 8 : V <= 16 ? 16 : V <= 32 ? 32 : 64;
+  float vals[VP];
+#pragma unroll
+  for (int q = 0; q < VP; ++q) vals[q] = 0.0f;
+  const uint32_t lanebits = (uint32_t)lane << 2;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+    const uint32_t wd[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+#pragma unroll
+    for (int b = 0; b < 16; ++b) {
+      const uint32_t addr = __builtin_amdgcn_perm(wd[b >> 2], lanebits, 0x0c0c0000u | ((4u + (b & 3)) << 8));
+      // the LUT starts at LDS address 0 (the kernel has no static LDS; the host checks)
+      const uint32_t code2 = *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr;
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+        acc[m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, code2),
+                                        __builtin_bit_cast(f16x2_t, xpair[m][b]), acc[m], false);
+    }
+    const float sf = h2f(sc[i]);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      float v;
+      if (FMT == SPECTRA_FMT_ASYM_G32) v = (acc[m] - (float)zq[i] * xsum[m]) * (sf * xs[m]);
+      else v = acc[m] * (sf * xs[m]);
+      vals[i * MT + m] = wok[i] ? v : 0.0f;
+    }
+  }
+
+  // ---------------- (8) transposed halving reduction across the wave ----------------
+  int idx = 0;
+  transposed_reduce<VP, 1>(vals, lane, idx);
+  // every lane now holds the total number idx (set by its low log2(VP) bits); lanes
+  // 0..VP-1 write them
+  float* part = (float*)(smem + p.off_part);
+  if (lane < VP && idx < V) {
+    const int i = idx / MT, m = idx - i * MT;
+    const int rl = g + i * p.G;
+    if (rl < Rw) part[(rl * p.S + s) * MT + m] = vals[0];
+  }
+
+  // ---------------- (9) outlier products, in the same scaled fp16 activation basis ----------------
+  float* oprod = (float*)(smem + p.off_oprod);
+  {
+    const bool csr = p.okind == SPECTRA_OUTLIERS_CSR;
+    const int cnt = p.okind == SPECTRA_OUTLIERS_NONE ? 0 : (csr ? e1 - e0 : Rw * p.n_out);
+    const int odt = csr ? SPECTRA_F16 : p.ow_dt;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int el = obase + u;  // workgroup-local entry index
+      if ((csr || u == 0) && el >= 0 && el < cnt && el < olim) {
+        const int col = ocol[u];
+        const int pos = xp_pos(col, p.marlin);
+        const float ov = to_f32_16((uint16_t)oraw[u], odt);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          oprod[el * MT + m] = ov * (h2f(xp[m * XS + pos]) * xsc[m * qpr + (col >> 5)]);
+      }
+    }
+  }
+  int32_t* rps = (int32_t*)(smem + p.off_rp);
+  if (p.okind == SPECTRA_OUTLIERS_CSR && tid <= Rw) rps[tid] = rp_v;
+  float* bl = (float*)(smem + p.off_bias);
+  if (p.bias != nullptr && tid < Rw)
+    bl[tid] = p.bias_dt == SPECTRA_F32 ? __builtin_bit_cast(float, bias_raw) : to_f32_16((uint16_t)bias_raw, p.bias_dt);
+
+  __syncthreads();  // --- barrier 2: slice partials and outlier products
+
+  // ---------------- (10) per-row totals: one wave per row, fixed order ----------------
+  for (int r = wave; r < Rw; r += nwaves) {
+    int lo = 0, hi = 0;
+    if (p.okind == SPECTRA_OUTLIERS_CSR) {
+      lo = rps[r] - e0;
+      hi = rps[r + 1] - e0;
+    } else if (p.okind == SPECTRA_OUTLIERS_COLUMNS) {
+      lo = r * p.n_out;
+      hi = lo + p.n_out;
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      if (m >= p.m) break;
+      float v = lane < p.S ? part[(r * p.S + lane) * MT + m] : 0.0f;
+      for (int el = lo + lane; el < hi; el += 64) {
+        if (el < olim) {
+          v += oprod[el * MT + m];
+        } else {  // beyond the register-staged entries: read the side tensor directly
+          int col;
+          float val;
+          if (p.okind == SPECTRA_OUTLIERS_CSR) {
+            col = p.ccol[e0 + el];
+            val = h2f(p.cval[e0 + el]);
+          } else {
+            const int rr = el / p.n_out, jj = el - rr * p.n_out;
+            col = (int)p.oidx[jj];
+            val = load_elem(p.ow, (int64_t)(r0 + rr) * p.ldow + jj, p.ow_dt);
+          }
+          v += val * (h2f(xp[m * XS + xp_pos(col, p.marlin)]) * xsc[m * qpr + (col >> 5)]);
+        }
+      }
+      v = wave_sum(v);
+      if (lane == 0) {
+        float y = v * p.out_scale;
+        if (p.bias != nullptr) y += bl[r];
+        ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + r] = from_f32_16(y, BF ? SPECTRA_BF16 : SPECTRA_F16);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// kernel selection (instantiated per activation dtype in gemv_f16.hip / gemv_bf16.hip)
+// ---------------------------------------------------------------------------
+typedef void (*gemv_fn)(const GemvParams);
+
+gemv_fn gemv_pick_f16(int fmt, int mt, int rpw);
+gemv_fn gemv_pick_bf16(int fmt, int mt, int rpw);
+
+
+template <int FMT, int MT, bool BF>
+gemv_fn pick_rpw(int rpw) {
+  switch (rpw) {
+    case 1: return gemv_kernel<FMT, MT, 1, BF>;
+    case 2: return gemv_kernel<FMT, MT, 2, BF>;
+    case 3: return gemv_kernel<FMT, MT, 3, BF>;
+    case 4: return gemv_kernel<FMT, MT, 4, BF>;
+    case 5: return gemv_kernel<FMT, MT, 5, BF>;
+    case 6: return gemv_kernel<FMT, MT, 6, BF>;
+    case 7: return gemv_kernel<FMT, MT, 7, BF>;
+    case 8: return gemv_kernel<FMT, MT, 8, BF>;
+    case 9: return gemv_kernel<FMT, MT, 9, BF>;
+    case 10: return gemv_kernel<FMT, MT, 10, BF>;
+    case 11: return gemv_kernel<FMT, MT, 11, BF>;
+    default: return gemv_kernel<FMT, MT, 12, BF>;
+  }
+}
+
+template <int FMT, bool BF>
+gemv_fn pick_rpw4(int rpw) {
+  switch (rpw) {
+    case 1: return gemv_kernel<FMT, 4, 1, BF>;
+    case 2: return gemv_kernel<FMT, 4, 2, BF>;
+    case 3: return gemv_kernel<FMT, 4, 3, BF>;
+    case 4: return gemv_kernel<FMT, 4, 4, BF>;
+    case 5: return gemv_kernel<FMT, 4, 5, BF>;
+    case 6: return gemv_kernel<FMT, 4, 6, BF>;
+    case 7: return gemv_kernel<FMT, 4, 7, BF>;
+    default: return gemv_kernel<FMT, 4, 8, BF>;
+  }
+}
+
+template <int FMT, bool BF>
+gemv_fn pick_kernel(int mt, int rpw) {
+  if (mt == 1) return pick_rpw<FMT, 1, BF>(rpw);
+  if (mt == 2) return pick_rpw<FMT, 2, BF>(rpw);
+  return pick_rpw4<FMT, BF>(rpw);
+}
+
+}  // namespace spectra
