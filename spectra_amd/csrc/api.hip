@@ -92,8 +92,11 @@ extern "C" const char* spectra_last_error(void) { return spectra::g_last_error.c
 extern "C" int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m,
                                     int32_t act_dtype, void* out, int64_t ldo, void* workspace,
                                     size_t workspace_bytes, spectra_stream_t stream) {
-  // engine.py:94-124: single-token rows go to the GEMV family, everything else to the GEMM family
-  if (m >= 1 && m <= 4)
-    return spectra_w4a16_gemv(w, x, ldx, (int32_t)m, act_dtype, out, ldo, stream);
+  // engine.py:94-124: single-token rows go to the GEMV family, everything else (and any
+  // operand combination the GEMV family does not serve) to the GEMM family
+  if (m >= 1 && m <= 4) {
+    const int st = spectra_w4a16_gemv(w, x, ldx, (int32_t)m, act_dtype, out, ldo, stream);
+    if (st != SPECTRA_ERR_UNSUPPORTED) return st;
+  }
   return spectra_w4a16_gemm(w, x, ldx, m, act_dtype, out, ldo, workspace, workspace_bytes, stream);
 }

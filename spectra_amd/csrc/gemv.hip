@@ -79,8 +79,12 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
   if (csr)
     SPECTRA_REQUIRE(ptr_aligned(w->csr_col, 16) && ptr_aligned(w->csr_val, 8) && w->csr_nnz < (int64_t(1) << 31),
                     "CSR columns must be 16-byte and values 8-byte aligned (nnz < 2^31)");
-  if (w->format == SPECTRA_FMT_NF4 && w->group_size < 32)
-    return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMV family needs an NF4 block of at least 32");
+  // the kernels pair each format with its own outlier kind and scale scheme: Format B
+  // (NF4, blocks >= 64, CSR outliers), Format A (groups of 32, dense outlier columns)
+  if (w->format == SPECTRA_FMT_NF4 && w->group_size < 64)
+    return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMV family needs an NF4 block of at least 64");
+  if (outliers && (w->format == SPECTRA_FMT_NF4) != csr)
+    return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMV family serves CSR outliers with NF4 and dense columns with Format A");
   GemvParams p;
   p.packed = w->packed; p.ldp = w->packed_stride;
   p.scales = w->scales; p.lds = w->scales_stride;

@@ -102,39 +102,44 @@ __device__ __forceinline__ int xp_pos(int k, int marlin) {
   return ((((q >> 6) * 4 + (j >> 2)) * 64 + (q & 63)) * 4 + (j & 3)) * 2 + half;
 }
 
-// value of lane (lane ^ MASK): DPP quad permutes for 1 and 2, ds_swizzle (xor mode, no
-// address register) for 4..16, a cross-lane permute for 32
-template <int MASK>
-__device__ __forceinline__ float lane_xor_c(float v) {
+// Value of the partner lane across lane-logical bit KB of the reflected lane numbering
+// (see reflect_chunk): DPP quad permutes for bits 0 and 1, the half-row and row mirrors
+// for bits 2 and 3 (no LDS), ds_swizzle (32-lane mirror) for bit 4 and a cross-lane
+// permute (64-lane mirror) for bit 5.
+template <int KB>
+__device__ __forceinline__ float lane_partner(float v, int lane) {
   const int iv = __builtin_bit_cast(int, v);
-  if constexpr (MASK == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
-  else if constexpr (MASK == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
-  else if constexpr (MASK < 32) return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, (MASK << 10) | 0x1F));
-  else return __shfl_xor(v, MASK, 64);
+  if constexpr (KB == 0) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+  else if constexpr (KB == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+  else if constexpr (KB == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false));
+  else if constexpr (KB == 3) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x140, 0xF, 0xF, false));
+  else if constexpr (KB == 4) return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, 0x7C1F));
+  else return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((63 - lane) << 2, iv));
 }
 
-// Transposed halving reduction of N values per lane across the 64 lanes: at the step
-// with offset OFF the lanes with bit OFF set keep the upper half of their values and add
-// their partner's upper half (the others the lower half), so N values cost N-1 exchanges
-// instead of 6N.  Offsets go 1, 2, 4, ... so the steps that move the most values use the
-// cheap DPP permutes.  At the end every lane holds the total number idx(lane).
-template <int N, int OFF>
-__device__ __forceinline__ void transposed_reduce(float* vals, int lane, int& idx) {
-  if constexpr (OFF <= 32) {
+// Transposed halving reduction of N values per lane across the 64 lanes: at the step on
+// lane-logical bit KB the lanes with that bit of lam set keep the upper half of their
+// values and add their partner's upper half (the others the lower half), so N values
+// cost N-1 exchanges instead of 6N.  Partners differ from each other only in bit KB of
+// lam, so both hold the same value indices when they combine.  At the end every lane
+// holds the total number idx, a bijection of the low log2(N) bits of lam.
+template <int N, int KB>
+__device__ __forceinline__ void transposed_reduce(float* vals, int lane, int lam, int& idx) {
+  if constexpr (KB <= 5) {
     if constexpr (N > 1) {
       constexpr int H = N / 2;
-      const bool upper = (lane & OFF) != 0;
+      const bool upper = (lam >> KB) & 1;
 #pragma unroll
       for (int q = 0; q < H; ++q) {
         const float send = upper ? vals[q] : vals[q + H];
         const float keep = upper ? vals[q + H] : vals[q];
-        vals[q] = keep + lane_xor_c<OFF>(send);
+        vals[q] = keep + lane_partner<KB>(send, lane);
       }
       if (upper) idx += H;
-      transposed_reduce<H, OFF * 2>(vals, lane, idx);
+      transposed_reduce<H, KB + 1>(vals, lane, lam, idx);
     } else {
-      vals[0] += lane_xor_c<OFF>(vals[0]);
-      transposed_reduce<1, OFF * 2>(vals, lane, idx);
+      vals[0] += lane_partner<KB>(vals[0], lane);
+      transposed_reduce<1, KB + 1>(vals, lane, lam, idx);
     }
   }
 }
@@ -143,11 +148,12 @@ __device__ __forceinline__ void transposed_reduce(float* vals, int lane, int& id
 // identity inside a quad, and for a top bit t >= 2 the chunk of the mirrored lane
 // (2^(t+1) - 1 - j) with bit t set.  With this numbering lane-logical bit 0/1 pairs the
 // lanes of DPP quad_perm [1,0,3,2] / [2,3,0,1], bit 2 the lanes of row_half_mirror, bit 3
-// those of row_mirror and bit 4 those of a 32-lane mirror (j <-> 31 - j).
+// those of row_mirror, bit 4 those of a 32-lane mirror (j <-> 31 - j) and bit 5 those of
+// the 64-lane mirror (j <-> 63 - j).
 __device__ __forceinline__ int reflect_chunk(int j, int b) {
   int out = 0;
 #pragma unroll
-  for (int t = 4; t >= 2; --t) {
+  for (int t = 5; t >= 2; --t) {
     if (t < b && ((j >> t) & 1)) {
       out |= 1 << t;
       j ^= (1 << t) - 1;
@@ -260,9 +266,9 @@ __device__ __forceinline__ void fwht_half(float (&v)[16], int log_had, bool marl
   if (log_had > 8) fly_x<4>(v, sgn(4));
 }
 
-// Sum over the 64 lanes with DPP only (no LDS): quad permutes, half-row and row mirrors,
-// then row broadcasts; the total ends in lane 63 and is read back as a scalar.
-__device__ __forceinline__ float wave_sum(float v) {
+// Sum over each 16-lane row with DPP only: quad permutes, then the half-row and row
+// mirrors; every lane of the row ends with the row's total.
+__device__ __forceinline__ float row16_sum(float v) {
   int t;
   t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
   v += __builtin_bit_cast(float, t);
@@ -272,11 +278,7 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += __builtin_bit_cast(float, t);
   t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false);  // row_mirror
   v += __builtin_bit_cast(float, t);
-  t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false);  // row_bcast:15
-  v += __builtin_bit_cast(float, t);
-  t = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false);  // row_bcast:31
-  v += __builtin_bit_cast(float, t);
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+  return v;
 }
 
 template <int FMT, int MT, int RPW, bool BF>
@@ -324,30 +326,33 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     const uint16_t* src = (const uint16_t*)p.x + (ok ? (int64_t)m * p.ldx + (int64_t)(cl >> 1) * 32 : 0);
     // waves with no half-run in this slot skip its loads (a wave-uniform branch; the
     // loads come before every other load, so later wait counts are unaffected)
+    // (left undefined otherwise: those values are never read, and no copy or wait is
+    // needed where the branch joins)
     if (i == 0 || wave * 64 + i * BD < MT * hpr) {
       xr[i][0] = *(const uint4*)(src + (p.marlin ? 8 * hf : 16 * hf));
       xr[i][1] = *(const uint4*)(src + (p.marlin ? 16 + 8 * hf : 16 * hf + 8));
-    } else {
-      xr[i][0] = xr[i][1] = make_uint4(0, 0, 0, 0);
     }
   }
 
   // CSR row pointers, issued before the weights: the outlier loads need e0 before the
   // stream has arrived (the wait counts are in issue order)
-  int rp_v = 0, e0 = 0, e1 = 0;
-  if (p.okind == SPECTRA_OUTLIERS_CSR) {
-    rp_v = p.rowptr[r0 + min(tid, Rw)];
-    e0 = p.rowptr[r0];
-    e1 = p.rowptr[r0 + Rw];
-  }
+  // (one unconditional load per wave: lane 0 reads the first, lane 1 the last row
+  // pointer; without CSR it reads the packed tensor and the value is unused.  The
+  // values are read out of the lanes where they are needed, after the activation work.)
+  int rpe = 0;
+  if constexpr (FMT == SPECTRA_FMT_NF4)
+    rpe = *(p.okind == SPECTRA_OUTLIERS_CSR ? p.rowptr + r0 + (lane == 1 ? Rw : 0) : (const int32_t*)p.packed);
 
   // ---------------- (2) the weight stream: every row of this wave, up front ----------------
   const int kb = s * 2048 + lane * 32;  // first k of this lane (one 32-run)
   const bool kvalid = kb < K;
+  constexpr int RP2 = (RPW + 1) / 2;
   uint4 wq[RPW];
-  uint16_t sc[RPW];
+  uint32_t sc[RPW];   // one scale per row (blocks of 32)
+  uint16_t sc2[RP2];  // two rows per load (blocks of 64 and more)
   uint8_t zq[RPW];
   bool wok[RPW];
+  const int kk = kvalid ? kb : 0;
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const int rl = g + i * p.G;
@@ -355,13 +360,34 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     const bool rok = rl < Rw;
     wok[i] = rok && kvalid;
     const int64_t row = r0 + (rok ? rl : 0);
-    const int kk = kvalid ? kb : 0;
     wq[i] = *(const uint4*)(p.packed + row * p.ldp + (kk >> 1));
-    sc[i] = p.scales[row * p.lds + (kk >> p.gshift)];
     if (FMT == SPECTRA_FMT_ASYM_G32) zq[i] = p.zeros[row * p.ldz + (kk >> 5)];
   }
+  // Scales after the weights.  With blocks of 64 or more, lanes 2j and 2j+1 share a
+  // block: one load serves rows 2t (even lanes) and 2t+1 (odd lanes), and a DPP quad
+  // broadcast hands each lane its row's value (in the stream).
+  constexpr bool pair_sc = FMT == SPECTRA_FMT_NF4;  // the host serves NF4 blocks >= 64 only
+  const int64_t sk = kk >> p.gshift;
+  if constexpr (pair_sc) {
+#pragma unroll
+    for (int t = 0; t < RP2; ++t) {
+      const int i = 2 * t + 1 < RPW ? 2 * t + (lane & 1) : 2 * t;
+      const int rl = g + i * p.G;
+      const int64_t row = r0 + (rl < Rw ? rl : 0);
+      sc2[t] = p.scales[row * p.lds + sk];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) {
+      const int rl = g + i * p.G;
+      const int64_t row = r0 + (rl < Rw ? rl : 0);
+      sc[i] = p.scales[row * p.lds + sk];
+    }
+  }
 
-  // ---------------- (2b) bias: consumed after the stream ----------------
+  // ---------------- (2b) row pointers and bias: consumed after the stream ----------------
+  int rp_v = 0;  // row pointers of this workgroup's rows, for the per-row phase
+  if (p.okind == SPECTRA_OUTLIERS_CSR) rp_v = p.rowptr[r0 + min(tid, Rw)];
   uint32_t bias_raw = 0;
   if (p.bias != nullptr) {
     const int64_t bi = r0 + (tid < Rw ? tid : 0);
@@ -453,50 +479,44 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   }
 
   // ---------------- (5) outlier entries of this workgroup (consumed after the stream) ----------------
+  // Raw loaded words only (extracted where they are used, so nothing here waits for
+  // them), one unconditional load pair per thread (the wait counts never branch):
+  //  * Format B, CSR: four consecutive entries from the 4-aligned entry below e0 (a
+  //    dwordx4 of columns, a dwordx2 of fp16 values; entry e is el = e - e0).  Groups
+  //    that would run past the array end re-read group 0; the entries of a partial last
+  //    group are read in the per-row phase.
+  //  * Format A, dense columns: entry el = tid, row el / n_out, column el % n_out (the
+  //    low dword of the int64 index, the 16-bit weight).
+  // Without outliers the loads read the first bytes of the packed tensor.
+  const bool has_o = p.okind != SPECTRA_OUTLIERS_NONE;
+  int e0 = 0, e1 = 0;
+  if constexpr (FMT == SPECTRA_FMT_NF4) {
+    e0 = has_o ? __builtin_amdgcn_readlane(rpe, 0) : 0;
+    e1 = has_o ? __builtin_amdgcn_readlane(rpe, 1) : 0;
+  }
   // entries el < olim have their products staged in LDS; the rest (beyond the LDS share,
-  // or in a partial last CSR group of 4) are read from the side tensors per row
-  const int olim = p.okind == SPECTRA_OUTLIERS_CSR ? min(p.ocap, (p.csr_nnz & ~3) - e0) : p.ocap;
-  // raw bits, one load pair per thread, branch-free (the wait counts never branch).
-  // CSR: four consecutive entries per thread from the 4-aligned entry below e0 (one
-  // dwordx4 of columns, one dwordx2 of fp16 values; entry e covers el = e - e0).
-  // Dense columns: entry el = tid, row el / n_out, column el % n_out.
-  int ocol[4];
-  uint32_t oraw[4];
+  // or in a partial last CSR group) are read from the side tensors per row
+  const int olim = FMT == SPECTRA_FMT_NF4 ? min(p.ocap, (p.csr_nnz & ~3) - e0) : p.ocap;
+  int4 ocv;
+  uint2 ovv;
   int obase;  // el of this thread's first entry
-  {
-    const bool has_o = p.okind != SPECTRA_OUTLIERS_NONE;
-    const bool csr = p.okind == SPECTRA_OUTLIERS_CSR;
+  if constexpr (FMT == SPECTRA_FMT_NF4) {
+    const int g4 = (e0 & ~3) + 4 * tid;
+    const int gc = g4 + 4 <= p.csr_nnz ? g4 : 0;
+    ocv = *(has_o ? (const int4*)(p.ccol + gc) : (const int4*)p.packed);
+    ovv = *(has_o ? (const uint2*)(p.cval + gc) : (const uint2*)p.packed);
+    obase = g4 - e0;
+  } else {
     const int n_out = p.n_out > 0 ? p.n_out : 1;
-    // (row, column) of a dense-column entry: float reciprocal, exact after one correction
+    // (row, column) of entry tid: float reciprocal, exact after one correction
     const int ei = tid < Rw * n_out ? tid : 0;
     int r = (int)((float)ei * p.inv_n_out);
     int jj = ei - r * n_out;
     r = jj < 0 ? r - 1 : (jj >= n_out ? r + 1 : r);
     jj = ei - r * n_out;
-    const int b4 = e0 & ~3;
-    const int g4 = b4 + 4 * tid;
-    // CSR groups that would run past the array end re-read group 0 (entries of a partial
-    // last group are read in the per-row phase); without outliers the loads read the
-    // first bytes of the packed tensor
-    const int gc = g4 + 4 <= p.csr_nnz ? g4 : 0;
-    const int4* cptr = !has_o ? (const int4*)p.packed
-                              : (csr ? (const int4*)(p.ccol + gc) : (const int4*)(p.oidx + jj));
-    const uint2* vptr = !has_o ? (const uint2*)p.packed
-                               : (csr ? (const uint2*)(p.cval + gc)
-                                      : (const uint2*)((const uint16_t*)p.ow + (int64_t)(r0 + r) * p.ldow + jj));
-    if (csr || !has_o) {
-      const int4 c = *cptr;
-      const uint2 v = *vptr;
-      ocol[0] = c.x; ocol[1] = c.y; ocol[2] = c.z; ocol[3] = c.w;
-      oraw[0] = v.x & 0xffffu; oraw[1] = v.x >> 16; oraw[2] = v.y & 0xffffu; oraw[3] = v.y >> 16;
-      obase = g4 - e0;
-    } else {  // dense: the same two loads, one entry (the low dword of idx, the 16-bit weight)
-      const int c = *(const int*)cptr;
-      const uint32_t v = *(const uint16_t*)vptr;
-      ocol[0] = c; ocol[1] = ocol[2] = ocol[3] = 0;
-      oraw[0] = v; oraw[1] = oraw[2] = oraw[3] = 0;
-      obase = tid;
-    }
+    ocv.x = *(has_o ? (const int*)(p.oidx + jj) : (const int*)p.packed);
+    ovv.x = *(has_o ? (const uint16_t*)p.ow + (int64_t)(r0 + r) * p.ldow + jj : (const uint16_t*)p.packed);
+    obase = tid;
   }
 
   __syncthreads();  // --- barrier 1: LUT, activation pairs and run scales
@@ -529,7 +549,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   float vals[VP];
 #pragma unroll
   for (int q = 0; q < VP; ++q) vals[q] = 0.0f;
-  const uint32_t lanebits = (uint32_t)lane << 2;
+  const uint32_t lanebits = (uint32_t)lane << 2;  // this lane's LUT copy: conflict-free reads
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     float acc[MT];
@@ -546,7 +566,16 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
         acc[m] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, code2),
                                         __builtin_bit_cast(f16x2_t, xpair[m][b]), acc[m], false);
     }
-    const float sf = h2f(sc[i]);
+    // quad_perm [0,0,2,2] / [1,1,3,3]: the even / odd lane of each pair
+    // the empty asm pins the use here: no conversion of a scale can be hoisted above the
+    // barrier, where it would wait for the whole stream
+    uint16_t spr = sc2[i >> 1];
+    asm volatile("" : "+v"(spr));
+    const int sp = (int)spr;
+    const uint32_t sw = !pair_sc ? sc[i]
+                                 : (uint32_t)((i & 1) ? __builtin_amdgcn_mov_dpp(sp, 0xF5, 0xF, 0xF, false)
+                                                      : __builtin_amdgcn_mov_dpp(sp, 0xA0, 0xF, 0xF, false));
+    const float sf = h2f((uint16_t)sw);
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       float v;
@@ -558,11 +587,12 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
 
   // ---------------- (8) transposed halving reduction across the wave ----------------
   int idx = 0;
-  transposed_reduce<VP, 1>(vals, lane, idx);
-  // every lane now holds the total number idx (set by its low log2(VP) bits); lanes
-  // 0..VP-1 write them
+  const int lam = reflect_chunk(lane, 6);
+  transposed_reduce<VP, 0>(vals, lane, lam, idx);
+  // every lane now holds the total number idx (set by the low log2(VP) bits of lam); the
+  // lanes with lam < VP write them
   float* part = (float*)(smem + p.off_part);
-  if (lane < VP && idx < V) {
+  if (lam < VP && idx < V) {
     const int i = idx / MT, m = idx - i * MT;
     const int rl = g + i * p.G;
     if (rl < Rw) part[(rl * p.S + s) * MT + m] = vals[0];
@@ -571,16 +601,18 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   // ---------------- (9) outlier products, in the same scaled fp16 activation basis ----------------
   float* oprod = (float*)(smem + p.off_oprod);
   {
-    const bool csr = p.okind == SPECTRA_OUTLIERS_CSR;
-    const int cnt = p.okind == SPECTRA_OUTLIERS_NONE ? 0 : (csr ? e1 - e0 : Rw * p.n_out);
-    const int odt = csr ? SPECTRA_F16 : p.ow_dt;
+    const int cnt = !has_o ? 0 : (FMT == SPECTRA_FMT_NF4 ? e1 - e0 : Rw * p.n_out);
+    const int odt = FMT == SPECTRA_FMT_NF4 ? SPECTRA_F16 : p.ow_dt;
+    constexpr int NE = FMT == SPECTRA_FMT_NF4 ? 4 : 1;
+    const int cols[4] = {ocv.x, ocv.y, ocv.z, ocv.w};
+    const uint32_t vals4[4] = {ovv.x & 0xffffu, ovv.x >> 16, ovv.y & 0xffffu, ovv.y >> 16};
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < NE; ++u) {
       const int el = obase + u;  // workgroup-local entry index
-      if ((csr || u == 0) && el >= 0 && el < cnt && el < olim) {
-        const int col = ocol[u];
+      if (el >= 0 && el < cnt && el < olim) {
+        const int col = cols[u];
         const int pos = xp_pos(col, p.marlin);
-        const float ov = to_f32_16((uint16_t)oraw[u], odt);
+        const float ov = to_f32_16((uint16_t)vals4[u], odt);
 #pragma unroll
         for (int m = 0; m < MT; ++m)
           oprod[el * MT + m] = ov * (h2f(xp[m * XS + pos]) * xsc[m * qpr + (col >> 5)]);
@@ -595,42 +627,51 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
 
   __syncthreads();  // --- barrier 2: slice partials and outlier products
 
-  // ---------------- (10) per-row totals: one wave per row, fixed order ----------------
-  for (int r = wave; r < Rw; r += nwaves) {
-    int lo = 0, hi = 0;
-    if (p.okind == SPECTRA_OUTLIERS_CSR) {
-      lo = rps[r] - e0;
-      hi = rps[r + 1] - e0;
-    } else if (p.okind == SPECTRA_OUTLIERS_COLUMNS) {
-      lo = r * p.n_out;
-      hi = lo + p.n_out;
-    }
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      if (m >= p.m) break;
-      float v = lane < p.S ? part[(r * p.S + lane) * MT + m] : 0.0f;
-      for (int el = lo + lane; el < hi; el += 64) {
-        if (el < olim) {
-          v += oprod[el * MT + m];
-        } else {  // beyond the register-staged entries: read the side tensor directly
-          int col;
-          float val;
-          if (p.okind == SPECTRA_OUTLIERS_CSR) {
-            col = p.ccol[e0 + el];
-            val = h2f(p.cval[e0 + el]);
-          } else {
-            const int rr = el / p.n_out, jj = el - rr * p.n_out;
-            col = (int)p.oidx[jj];
-            val = load_elem(p.ow, (int64_t)(r0 + rr) * p.ldow + jj, p.ow_dt);
-          }
-          v += val * (h2f(xp[m * XS + xp_pos(col, p.marlin)]) * xsc[m * qpr + (col >> 5)]);
-        }
+  // ---------------- (10) per-row totals: 16 lanes per row, four rows per wave per pass ----------------
+  // fixed order (deterministic): lane gl of a group takes slice gl and outlier entries
+  // gl, gl + 16, ... of its row, then a DPP tree sums the 16 lanes
+  {
+    const int grp = lane >> 4, gl = lane & 15;
+    for (int rb = wave * 4; rb < Rw; rb += nwaves * 4) {
+      const int r = rb + grp;
+      const bool rv = r < Rw;
+      const int rr = rv ? r : Rw - 1;  // groups past the last row compute but do not store
+      int lo = 0, hi = 0;
+      if (p.okind == SPECTRA_OUTLIERS_CSR) {
+        lo = rps[rr] - e0;
+        hi = rps[rr + 1] - e0;
+      } else if (p.okind == SPECTRA_OUTLIERS_COLUMNS) {
+        lo = rr * p.n_out;
+        hi = lo + p.n_out;
       }
-      v = wave_sum(v);
-      if (lane == 0) {
-        float y = v * p.out_scale;
-        if (p.bias != nullptr) y += bl[r];
-        ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + r] = from_f32_16(y, BF ? SPECTRA_BF16 : SPECTRA_F16);
+      if (!rv) hi = lo;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        if (m >= p.m) break;
+        float v = (gl < p.S && rv) ? part[(rr * p.S + gl) * MT + m] : 0.0f;
+        for (int el = lo + gl; el < hi; el += 16) {
+          if (el < olim) {
+            v += oprod[el * MT + m];
+          } else {  // beyond the staged entries: read the side tensor directly
+            int col;
+            float val;
+            if (p.okind == SPECTRA_OUTLIERS_CSR) {
+              col = p.ccol[e0 + el];
+              val = h2f(p.cval[e0 + el]);
+            } else {
+              const int rw = el / p.n_out, jj = el - rw * p.n_out;
+              col = (int)p.oidx[jj];
+              val = load_elem(p.ow, (int64_t)(r0 + rw) * p.ldow + jj, p.ow_dt);
+            }
+            v += val * (h2f(xp[m * XS + xp_pos(col, p.marlin)]) * xsc[m * qpr + (col >> 5)]);
+          }
+        }
+        v = row16_sum(v);
+        if (gl == 0 && rv) {
+          float y = v * p.out_scale;
+          if (p.bias != nullptr) y += bl[rr];
+          ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + rr] = from_f32_16(y, BF ? SPECTRA_BF16 : SPECTRA_F16);
+        }
       }
     }
   }

@@ -150,9 +150,12 @@ def _run_linear(ops: QWeightOperands, x2: torch.Tensor, out2: torch.Tensor, fami
     adt = _DT[x2.dtype]
     stream = _stream(x2.device)
     if family == "gemv":
-        L.check("spectra_w4a16_gemv", lib.spectra_w4a16_gemv(ops.ptr(), x2.data_ptr(), x2.stride(0), m, adt,
-                                                              out2.data_ptr(), out2.stride(0), stream))
-        return
+        st = lib.spectra_w4a16_gemv(ops.ptr(), x2.data_ptr(), x2.stride(0), m, adt, out2.data_ptr(),
+                                    out2.stride(0), stream)
+        if st != L.ERR_UNSUPPORTED:  # operand combinations the GEMV family does not serve run on the GEMM
+            L.check("spectra_w4a16_gemv", st)
+            return
+        family = "gemm"
     ws_bytes = lib.spectra_w4a16_gemm_workspace(ops.ptr(), m, adt)
     ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=x2.device)
     fn = lib.spectra_w4a16_gemm if family == "gemm" else lib.spectra_w4a16_linear
