@@ -191,6 +191,8 @@ def main():
     ap.add_argument("--no-detail", action="store_true", help="skip the secondary configs")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only run the dominant kernel's timing loop (for rocprofv3 runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run plain device copies of COPY_BYTES each (PMC traffic calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -202,6 +204,9 @@ def main():
     lib = L.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate_copy:
+        calibrate_copy(dev)
+        return
 
     # ---- cfg2 operands
     log("bench: building cfg2 weights (QKV 3072->5120, down 8192->3072, NF4 b64, 0.5% CSR)")
@@ -289,6 +294,24 @@ def main():
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
+
+
+COPY_BYTES = 16 << 20  # plain copy of known size: FETCH_SIZE / WRITE_SIZE scale factors
+
+
+def calibrate_copy(dev) -> None:
+    """Plain device-to-device copies of COPY_BYTES, rotating over a pool larger than the
+    Infinity Cache so every copy reads from and writes to HBM.  The PMC counters of these
+    dispatches give bytes per counted KiB for reads and writes."""
+    n = 48
+    src = [torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(i) for i in range(n)]
+    dst = [torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev) for _ in range(n)]
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for i in range(n):
+            dst[i].copy_(src[(i + rep) % n])
+    torch.cuda.synchronize()
+    log(f"bench: {3 * n} copies of {COPY_BYTES} bytes")
 
 
 def secondary(lib, dev, pool_gb: float) -> dict:

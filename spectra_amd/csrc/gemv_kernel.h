@@ -482,9 +482,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   // Raw loaded words only (extracted where they are used, so nothing here waits for
   // them), one unconditional load pair per thread (the wait counts never branch):
   //  * Format B, CSR: four consecutive entries from the 4-aligned entry below e0 (a
-  //    dwordx4 of columns, a dwordx2 of fp16 values; entry e is el = e - e0).  Groups
-  //    that would run past the array end re-read group 0; the entries of a partial last
-  //    group are read in the per-row phase.
+  //    dwordx4 of columns, a dwordx2 of fp16 values; entry e is el = e - e0).  The
+  //    entries of a partial last group of the array are read in the per-row phase.
   //  * Format A, dense columns: entry el = tid, row el / n_out, column el % n_out (the
   //    low dword of the int64 index, the 16-bit weight).
   // Without outliers the loads read the first bytes of the packed tensor.
@@ -502,7 +501,9 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   int obase;  // el of this thread's first entry
   if constexpr (FMT == SPECTRA_FMT_NF4) {
     const int g4 = (e0 & ~3) + 4 * tid;
-    const int gc = g4 + 4 <= p.csr_nnz ? g4 : 0;
+    // groups past this workgroup's entries (or the array end) re-read group 0, a cached
+    // line, so the stream carries no CSR bytes beyond the workgroup's own
+    const int gc = (g4 < e1 && g4 + 4 <= p.csr_nnz) ? g4 : 0;
     ocv = *(has_o ? (const int4*)(p.ccol + gc) : (const int4*)p.packed);
     ovv = *(has_o ? (const uint2*)(p.cval + gc) : (const uint2*)p.packed);
     obase = g4 - e0;
