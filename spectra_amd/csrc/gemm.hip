@@ -309,6 +309,11 @@ __global__ void __launch_bounds__(kGemmThreads, 2) gemm_kernel(const GemmParams 
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// skinny.hip: the small-batch MFMA family (2 <= m <= 16)
+size_t skinny_workspace(const spectra_qweight_t* w, int64_t m);
+int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m, int act_dtype, void* out,
+                  int64_t ldo, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 }  // namespace spectra
 
 using namespace spectra;
@@ -316,7 +321,9 @@ using namespace spectra;
 extern "C" size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64_t m, int32_t act_dtype) {
   (void)act_dtype;
   if (w == nullptr || m <= 0) return 0;
-  return align256((size_t)m * (size_t)w->k * 2) + align256((size_t)m * 4);
+  const size_t gemm = align256((size_t)m * (size_t)w->k * 2) + align256((size_t)m * 4);
+  const size_t small = skinny_workspace(w, m);
+  return gemm > small ? gemm : small;
 }
 
 extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int64_t lda, int64_t m,
@@ -339,6 +346,10 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
     return fail(SPECTRA_ERR_WORKSPACE, "workspace missing or smaller than spectra_w4a16_gemm_workspace()");
   SPECTRA_REQUIRE((reinterpret_cast<uintptr_t>(workspace) % 256) == 0, "workspace must be 256-byte aligned");
   const hipStream_t s = (hipStream_t)stream;
+  if (m >= 2 && m <= 16) {  // HBM-bound small batches: the MFMA stream family when it serves the operands
+    const int sst = skinny_launch(w, a, lda, m, act_dtype, out, ldo, workspace, workspace_bytes, s);
+    if (sst != SPECTRA_ERR_UNSUPPORTED) return sst;
+  }
   uint16_t* a16 = (uint16_t*)workspace;
   int32_t* fexp = (int32_t*)((uint8_t*)workspace + align256((size_t)m * w->k * 2));
   const int had = w->hadamard_block;

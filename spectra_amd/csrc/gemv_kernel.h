@@ -503,9 +503,11 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     const int g4 = (e0 & ~3) + 4 * tid;
     // groups past this workgroup's entries (or the array end) re-read group 0, a cached
     // line, so the stream carries no CSR bytes beyond the workgroup's own
-    const int gc = (g4 < e1 && g4 + 4 <= p.csr_nnz) ? g4 : 0;
-    ocv = *(has_o ? (const int4*)(p.ccol + gc) : (const int4*)p.packed);
-    ovv = *(has_o ? (const uint2*)(p.cval + gc) : (const uint2*)p.packed);
+    // (arrays of fewer than 4 entries are never read this way: olim is 0 then)
+    const bool big = has_o && p.csr_nnz >= 4;
+    const int gc = (big && g4 < e1 && g4 + 4 <= p.csr_nnz) ? g4 : 0;
+    ocv = *(big ? (const int4*)(p.ccol + gc) : (const int4*)p.packed);
+    ovv = *(big ? (const uint2*)(p.cval + gc) : (const uint2*)p.packed);
     obase = g4 - e0;
   } else {
     const int n_out = p.n_out > 0 ? p.n_out : 1;
