@@ -125,6 +125,7 @@ __global__ void __launch_bounds__(kSkPrepThreads) skinny_prep_kernel(const void*
   F = F < -126 ? -126 : (F > 126 ? 126 : F);
   const float f = __builtin_bit_cast(float, (uint32_t)(F + 127) << 23);
   // A-operand units of this segment: (chunk c, MFMA t, lane group g) -> 8 fp16 at [c][t][g][mp][8]
+  // (a wave's load of one MFMA operand is 4 x mp x 16 contiguous bytes)
   const int units = (len >> 7) * 16, c0 = k0 >> 7;
   for (int u = tid; u < units; u += kSkPrepThreads) {
     const int c = u >> 4, t = (u >> 2) & 3, g = u & 3;
@@ -165,7 +166,7 @@ struct SkinnyParams {
   void* out;
   int64_t ldo;
   int m, mp, n, k, nchunks, nrounds, csr_nnz, okind, bias_dt, act_dt, ecap;
-  uint32_t off_codes, off_rp, off_bias, off_xe, off_ve;
+  uint32_t off_codes, off_rp, off_bias, off_xe, off_ve, off_sums;
 };
 
 template <int T, int CPW>
@@ -182,7 +183,10 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
   const int Rw = min(R, p.n - r0);
   const bool csr = p.okind == SPECTRA_OUTLIERS_CSR;
   const int mrow = n16 & (p.mp - 1);  // A-operand row of this lane (rows >= mp repeat)
-  const int last_chunk = p.nchunks - 1;
+  // every argument the prologue needs, fetched in one round trip before the first load
+  asm volatile("" ::"s"(p.packed), "s"(p.ldp), "s"(p.scales), "s"(p.lds32), "s"(p.xa), "s"(p.rowptr),
+               "s"(p.bias), "s"(p.n), "s"(p.mp), "s"(p.nchunks), "s"(p.nrounds), "s"(p.okind), "s"(p.bias_dt),
+               "s"(p.csr_nnz), "s"(p.ccol), "s"(p.cval), "s"(p.off_codes));
 
   // ---- (1) loads the tail needs first (wait counts are in issue order) ----
   // lanes 0/1: the workgroup's first / end CSR row pointer (packed bytes when no CSR)
@@ -209,32 +213,40 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
   const uint32_t lanebits = (uint32_t)lane << 2;
   constexpr int NJ = (CPW + 3) / 4;
 
+  // units (chunk c, tile t) of a round in consumption order u = c * T + t; the first D0
+  // units' weights are issued before the LUT is built, each later one while an earlier
+  // unit is decoded, so the LDS-bound decode runs under the stream instead of after it
+  constexpr int U = CPW * T;
+  constexpr int D0 = U < 4 ? U : (U + 1) / 2;
   for (int rd = 0; rd < p.nrounds; ++rd) {
     const int cb = (rd * nw + wave) * CPW;  // first chunk of this wave in this round
+    // loads start at cbl = min(cb, nchunks - CPW) so every address is in bounds and chunk
+    // c of the wave sits at a constant offset; slots below cb (only in a last, partial
+    // round) belong to another wave and are masked
+    const int cbl = min(cb, p.nchunks - CPW);
     // ---- (2) scales (one dword = the two block absmax of a chunk; lane group g loads
     //      chunk cb + 4 j + g of its row, redistributed per chunk with ds_bpermute),
-    //      then activations, then the weight stream in consumption order ----
+    //      then activations, then the first weight units ----
     uint32_t scw[T][NJ];
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
       for (int j = 0; j < NJ; ++j)
-        scw[t][j] = p.scales[rowoff[t] * p.lds32 + min(cb + 4 * j + g, last_chunk)];
+        scw[t][j] = p.scales[rowoff[t] * p.lds32 + min(cbl + 4 * j + g, p.nchunks - 1)];
     uint4 xr[CPW][4];
+    const uint4* xbase = p.xa + (int64_t)(cbl * 16 + g) * p.mp + mrow;
 #pragma unroll
     for (int c = 0; c < CPW; ++c) {
-      const int cc = min(cb + c, last_chunk);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) xr[c][s] = p.xa[(int64_t)((cc * 4 + s) * 4 + g) * p.mp + mrow];
+      for (int s = 0; s < 4; ++s) xr[c][s] = xbase[(c * 16 + s * 4) * p.mp];
     }
-    uint4 wq[CPW][T];
+    uint4 wq[U];
+    const uint8_t* wbase[T];
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const int cc = min(cb + c, last_chunk);
+    for (int t = 0; t < T; ++t) wbase[t] = p.packed + rowoff[t] * p.ldp + (int64_t)cbl * 64 + 16 * g;
+    auto issue = [&](int u) { wq[u] = *(const uint4*)(wbase[u % T] + (u / T) * 64); };
 #pragma unroll
-      for (int t = 0; t < T; ++t)
-        wq[c][t] = *(const uint4*)(p.packed + rowoff[t] * p.ldp + (int64_t)cc * 64 + 16 * g);
-    }
+    for (int u = 0; u < D0; ++u) issue(u);
 
     if (rd == 0) {
       // ---- (3) CSR entries of this workgroup: four per thread from the 4-aligned entry
@@ -271,41 +283,40 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
       __syncthreads();  // LUT complete
     }
 
-    // ---- (5) decode + MFMA, chunk by chunk as the stream arrives ----
+    // ---- (5) decode + MFMA unit by unit as the stream arrives ----
 #pragma unroll
-    for (int c = 0; c < CPW; ++c) {
-      const bool cvalid = cb + c < p.nchunks;  // wave-uniform
+    for (int u = 0; u < U; ++u) {
+      if (u + D0 < U) issue(u + D0);
+      const int c = u / T, t = u % T;
+      const bool cvalid = cbl + c >= cb;  // wave-uniform
+      const uint4 w = wq[u];
+      // lower lanes keep dwords 0-1 and take the upper lanes' 0-1; upper lanes take
+      // the lower lanes' 2-3 and keep their own 2-3
+      const auto sxz = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
+      const auto syw = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
+      const uint32_t slot[4] = {sxz[0], syw[0], sxz[1], syw[1]};
+      uint32_t bv[4][4];
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const uint4 w = wq[c][t];
-        // lower lanes keep dwords 0-1 and take the upper lanes' 0-1; upper lanes take
-        // the lower lanes' 2-3 and keep their own 2-3
-        const auto sxz = __builtin_amdgcn_permlane32_swap(w.x, w.z, false, false);
-        const auto syw = __builtin_amdgcn_permlane32_swap(w.y, w.w, false, false);
-        const uint32_t slot[4] = {sxz[0], syw[0], sxz[1], syw[1]};
-        uint32_t bv[4][4];
+      for (int sl = 0; sl < 4; ++sl)
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t addr = __builtin_amdgcn_perm(slot[s], lanebits, 0x0c0c0000u | ((4u + i) << 8));
-            bv[s][i] = *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr;
-          }
-        sf4_t t0 = {0.0f, 0.0f, 0.0f, 0.0f}, t1 = {0.0f, 0.0f, 0.0f, 0.0f};
-        t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][0]),
-                                                    __builtin_bit_cast(sh8_t, bv[0]), t0, 0, 0, 0);
-        t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][2]),
-                                                    __builtin_bit_cast(sh8_t, bv[2]), t1, 0, 0, 0);
-        t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][1]),
-                                                    __builtin_bit_cast(sh8_t, bv[1]), t0, 0, 0, 0);
-        t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][3]),
-                                                    __builtin_bit_cast(sh8_t, bv[3]), t1, 0, 0, 0);
-        const uint32_t sd = (uint32_t)__builtin_amdgcn_ds_bpermute((n16 + 16 * (c & 3)) << 2, (int)scw[t][c >> 2]);
-        const float s0 = h2f((uint16_t)(sd & 0xffffu)), s1 = h2f((uint16_t)(sd >> 16));
-        if (cvalid) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(t1[r], s1, __builtin_fmaf(t0[r], s0, acc[t][r]));
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t addr = __builtin_amdgcn_perm(slot[sl], lanebits, 0x0c0c0000u | ((4u + i) << 8));
+          bv[sl][i] = *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr;
         }
+      sf4_t t0 = {0.0f, 0.0f, 0.0f, 0.0f}, t1 = {0.0f, 0.0f, 0.0f, 0.0f};
+      t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][0]),
+                                                  __builtin_bit_cast(sh8_t, bv[0]), t0, 0, 0, 0);
+      t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][2]),
+                                                  __builtin_bit_cast(sh8_t, bv[2]), t1, 0, 0, 0);
+      t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][1]),
+                                                  __builtin_bit_cast(sh8_t, bv[1]), t0, 0, 0, 0);
+      t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(sh8_t, xr[c][3]),
+                                                  __builtin_bit_cast(sh8_t, bv[3]), t1, 0, 0, 0);
+      const uint32_t sd = (uint32_t)__builtin_amdgcn_ds_bpermute((n16 + 16 * (c & 3)) << 2, (int)scw[t][c >> 2]);
+      const float s0 = h2f((uint16_t)(sd & 0xffffu)), s1 = h2f((uint16_t)(sd >> 16));
+      if (cvalid) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(t1[r], s1, __builtin_fmaf(t0[r], s0, acc[t][r]));
       }
     }
   }
@@ -351,12 +362,24 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
   }
   __syncthreads();
 
-  // ---- (7) per output (row, m): waves in a fixed order, outliers in entry order ----
+  // ---- (7) cross-wave sums in a fixed wave order: thread (t, lane) adds the float4 of
+  //      every wave (conflict-free 16-byte reads) into sums[m][row] (m-major) ----
+  float* sums = (float*)(smem + p.off_sums);
+  for (int i = tid; i < T * 64; i += BD) {
+    const int t = i >> 6, l = i & 63;
+    sf4_t v = red[t * 64 + l];
+    for (int w = 1; w < nw; ++w) v += red[(w * T + t) * 64 + l];
+    const int row = 16 * t + (l & 15), mq = 4 * (l >> 4);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (mq + r < p.m) sums[(mq + r) * R + row] = v[r];
+  }
+  __syncthreads();
+
+  // ---- (8) per output (row, m): outliers in entry order, scale, bias, store ----
   for (int idx = tid; idx < Rw * p.m; idx += BD) {
     const int m = idx / Rw, row = idx - m * Rw;
-    const int t = row >> 4, srcl = (row & 15) + 16 * (m >> 2), r = m & 3;
-    float v = 0.0f;
-    for (int w = 0; w < nw; ++w) v += red[(w * T + t) * 64 + srcl][r];
+    float v = sums[m * R + row];
     if (csr) {
       const int lo = rps[row], hi = rps[row + 1];
       const int hs = min(hi, e_stage);
@@ -501,6 +524,8 @@ int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_
     ecap = want;
     stage_end = red_bytes + (uint32_t)ecap * (uint32_t)(2 * mp + 2) + 32;
   }
+  p.off_sums = (stage_end + 15u) & ~15u;  // [16][16 T] fp32 cross-wave sums
+  stage_end = p.off_sums + (uint32_t)(16 * 16 * pl.T * 4);
   const uint32_t base = stage_end > (uint32_t)kSkLut ? ((stage_end + 15u) & ~15u) : (uint32_t)kSkLut;
   p.off_xe = red_bytes;
   p.off_ve = (red_bytes + (uint32_t)ecap * (uint32_t)(2 * mp) + 15u) & ~15u;
