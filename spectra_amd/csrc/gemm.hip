@@ -1,18 +1,22 @@
 // Batched / prefill GEMM family for gfx950 (replaces kernels.py:187-389):
 //   out = FWHT(a) . W_eff^T + bias
 //
-// 1. act_prep_kernel: one workgroup per activation row rotates it (blockwise FWHT,
-//    fp32, reference butterfly order), scales it by a power of two so max|a| lands in
-//    [2^14, 2^15) and stores fp16 -- exact scaling, so fp16 keeps 11 significant bits
-//    for fp16 and bf16 inputs alike.
-// 2. gemm_kernel: 128x128 output tile per workgroup, 4 waves of 64x64, K step 64.
-//    Each step the workgroup loads the fp16 activation tile into LDS and dequantizes
-//    the packed weight tile into LDS: packed byte -> (code_lo, code_hi) fp16 pair via a
-//    32-column LUT (lane l reads column l & 31, conflict-free), times the block scale
-//    with packed fp16 math (Format A: (q - z) * s, exact for fp16 output), then the
-//    outliers of the tile (CSR entries or dense outlier columns) overwrite their
-//    positions.  MFMA v_mfma_f32_32x32x16_f16 accumulates in fp32; the epilogue
-//    undoes the row scale, adds the bias in fp32 and rounds once.
+// 1. gemm_prep_kernel (one workgroup per activation row): blockwise FWHT in fp32 (the
+//    reference's butterfly order), division by sqrt(block), a power-of-two row scale and
+//    fp16 rounding.  The row is stored in packed-byte pair order: position 2 b + h holds
+//    the element that nibble h of packed byte b multiplies, so a decoded byte (an fp16
+//    code pair) and the activations it meets sit at the same positions.
+// 2. gemm_kernel<FMT, BN>: a 256 x BN output tile per workgroup, K step 32, 8 waves of
+//    128 x BN/4 (v_mfma_f32_32x32x16_f16, fp32 accumulators; two waves per SIMD so one
+//    wave's decode and copies overlap the other's MFMAs).  Each step one thread
+//    decodes half (BN = 256) or a quarter (BN = 128) of one weight row's 16-byte run through the
+//    lane-replicated nibble-pair LUT, applies the block scale (Format A: (q - z) * s) with
+//    one fp16 rounding, and writes the row into LDS; CSR outliers / outlier columns of
+//    the run overwrite their positions there (the quantized code there is exactly 0).
+//    Activation and weight tiles are double-buffered in LDS with one barrier per step;
+//    global loads run two steps ahead, so the next step's decode and the copies overlap
+//    this step's MFMAs.  The epilogue undoes the row scale, adds the bias in fp32 and
+//    rounds once.
 #include <cmath>
 
 #include "common.h"
@@ -22,63 +26,177 @@ namespace spectra {
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef float f16v_t __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x2g_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kPad = 8;                  // fp16 elements of row padding in LDS tiles
-constexpr int kLdsRow = kBK + kPad;      // 72 fp16 = 144 bytes
-constexpr int kTileBytes = kBM * kLdsRow * 2;
-constexpr int kGemmThreads = 256;
+constexpr int kBM = 256, kBK = 32;
+constexpr int kGemmWaves = 8;  // two per SIMD (four waves of 128 x 128 measured slower)
+constexpr int kRowH = 40;         // fp16 per LDS tile row: 32 + 8 of padding (80 bytes)
 constexpr int kPrepThreads = 256;
-constexpr int kWin = 4;                  // outlier entries prefetched per weight row
+constexpr int kGLut = 65536;      // lane-replicated nibble-pair LUT at LDS address 0
+constexpr int kWin = 4;           // outlier entries prefetched per weight row
 
 // ---------------------------------------------------------------------------
 // activation pre-pass
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kPrepThreads) act_prep_kernel(const void* __restrict__ a, int64_t lda, int dt,
-                                                                 int64_t k, int had, float div,
-                                                                 uint16_t* __restrict__ a16, int32_t* __restrict__ fexp) {
-  extern __shared__ float fs[];
+// One workgroup of 256 threads per activation row.  The row's 8-element chunks are spread
+// over the threads (chunk c = tid + 256 u, up to 16 per thread), so a Hadamard block of b
+// <= 512 elements lies in b / 8 consecutive lanes of one wave: stages h = 1, 2, 4 run on
+// register bits and h = 8 .. 256 across lanes (each stage one fp32 add or subtract, the
+// reference's order and rounding); blocks of 1024 finish their last stage through LDS.
+// The row is scaled by a power of two (max |x_rot| -> [2^14, 2^15)), rounded to fp16 and
+// written in packed-byte pair order.
+constexpr int kPrepMaxU = 16;  // K <= 256 * 8 * 16 = 32768
+
+template <int kPrepU>
+__global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __restrict__ a, int64_t lda, int dt,
+                                                                  int k, int log_had, float div, int marlin, int vec,
+                                                                  uint16_t* __restrict__ a16,
+                                                                  int32_t* __restrict__ fexp) {
+  extern __shared__ float fs[];  // [k] fp32 (the 1024-block stage), then [k] fp16 (pair-order write)
   __shared__ float wmax[kPrepThreads / 64];
   const int64_t row = blockIdx.x;
-  for (int64_t i = threadIdx.x; i < k; i += blockDim.x) fs[i] = load_elem(a, row * lda + i, dt);
-  __syncthreads();
-  if (had) {
-    const int npairs = (int)(k >> 1);
-    for (int h = 1; h < had; h <<= 1) {
-      for (int p = threadIdx.x; p < npairs; p += blockDim.x) {
-        const int blk = p / (had >> 1), w = p % (had >> 1);
-        const int i = blk * had + (w / h) * 2 * h + (w % h);
-        const float u = fs[i], v = fs[i + h];
-        fs[i] = u + v;
-        fs[i + h] = u - v;
+  const int tid = threadIdx.x;
+  const int n8 = k >> 3;
+  float v[kPrepU][8];
+#pragma unroll
+  for (int u = 0; u < kPrepU; ++u) {
+    const int c = tid + u * kPrepThreads;
+    if (c < n8) {
+      if (vec) {
+        const uint4 q = ((const uint4*)((const uint16_t*)a + row * lda))[c];
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[u][2 * e] = to_f32_16((uint16_t)(w4[e] & 0xffffu), dt);
+          v[u][2 * e + 1] = to_f32_16((uint16_t)(w4[e] >> 16), dt);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[u][e] = load_elem(a, row * lda + 8 * c + e, dt);
       }
-      __syncthreads();
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = 0.0f;
     }
-    for (int64_t i = threadIdx.x; i < k; i += blockDim.x) fs[i] = fs[i] / div;
+  }
+  // compressor.py:34-39: stages h = 1, 2, 4, ...: (u, v) -> (u + v, u - v) in fp32
+  // (stage loops unrolled with compile-time strides: the register array stays in registers)
+#pragma unroll
+  for (int lh = 0; lh < 3; ++lh) {
+    if (lh < log_had) {
+      const int h = 1 << lh;
+#pragma unroll
+      for (int u = 0; u < kPrepU; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if ((e & h) == 0) {
+            const float x0 = v[u][e], x1 = v[u][e | h];
+            v[u][e] = x0 + x1;
+            v[u][e | h] = x0 - x1;
+          }
+    }
+  }
+#pragma unroll
+  for (int lh = 3; lh < 9; ++lh) {
+    if (lh < log_had) {
+      const int lb = 1 << (lh - 3);
+      const bool hi = (tid & lb) != 0;
+#pragma unroll
+      for (int u = 0; u < kPrepU; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float o = __shfl_xor(v[u][e], lb, 64);
+          v[u][e] = hi ? o - v[u][e] : v[u][e] + o;
+        }
+    }
+  }
+  if (log_had > 9) {  // 1024-blocks: the stage across waves through LDS
+#pragma unroll
+    for (int u = 0; u < kPrepU; ++u)
+      if (tid + u * kPrepThreads < n8)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fs[8 * (tid + u * kPrepThreads) + e] = v[u][e];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kPrepU; ++u) {
+      const int c = tid + u * kPrepThreads;
+      if (c < n8) {
+        const bool hi = (c & 64) != 0;  // element bit 9 = chunk bit 6
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float o = fs[8 * (c ^ 64) + e];
+          v[u][e] = hi ? o - v[u][e] : v[u][e] + o;
+        }
+      }
+    }
     __syncthreads();
   }
-  float m = 0.0f;
-  for (int64_t i = threadIdx.x; i < k; i += blockDim.x) m = fmaxf(m, fabsf(fs[i]));
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-  __syncthreads();
   float mx = 0.0f;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) mx = fmaxf(mx, wmax[w]);
+#pragma unroll
+  for (int u = 0; u < kPrepU; ++u)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (log_had > 0) v[u][e] = v[u][e] / div;  // compressor.py:40-41
+      mx = fmaxf(mx, fabsf(v[u][e]));
+    }
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
   const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
   const int eb = (int)(bits >> 23);
   const int E = eb == 0 ? -126 : eb - 127;
-  int F = bits == 0 ? 0 : 14 - E;
+  int F = bits == 0 ? 0 : 14 - E;  // max |x_rot| * 2^F in [2^14, 2^15): exact scaling, no overflow
   F = F < -126 ? -126 : (F > 126 ? 126 : F);
   const float f = __builtin_bit_cast(float, (uint32_t)(F + 127) << 23);
-  for (int64_t i = threadIdx.x; i < k; i += blockDim.x) a16[row * k + i] = f2h(fs[i] * f);
-  if (threadIdx.x == 0) fexp[row] = F;
+  uint16_t* xs = (uint16_t*)fs;
+  if (marlin) {  // natural order into LDS, then pairs (k, k + 16) of each 32-run
+#pragma unroll
+    for (int u = 0; u < kPrepU; ++u) {
+      const int c = tid + u * kPrepThreads;
+      if (c < n8) {
+        uint32_t d[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          d[e] = (uint32_t)f2h(v[u][2 * e] * f) | ((uint32_t)f2h(v[u][2 * e + 1] * f) << 16);
+        *(uint4*)(xs + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
+      }
+    }
+    __syncthreads();
+    // output chunk c (positions 8 c .. 8 c + 7) = bytes 4 c .. 4 c + 3: run c / 4, j = 4 (c % 4) + i
+#pragma unroll
+    for (int u = 0; u < kPrepU; ++u) {
+      const int c = tid + u * kPrepThreads;
+      if (c < n8) {
+        const uint16_t* run = xs + 32 * (c >> 2);
+        const int j0 = 4 * (c & 3);
+        uint32_t d[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) d[i] = (uint32_t)run[j0 + i] | ((uint32_t)run[j0 + i + 16] << 16);
+        *(uint4*)(a16 + row * k + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
+      }
+    }
+  } else {  // byte j = (k 2j, k 2j + 1): pair order is the natural order
+#pragma unroll
+    for (int u = 0; u < kPrepU; ++u) {
+      const int c = tid + u * kPrepThreads;
+      if (c < n8) {
+        uint32_t d[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          d[e] = (uint32_t)f2h(v[u][2 * e] * f) | ((uint32_t)f2h(v[u][2 * e + 1] * f) << 16);
+        *(uint4*)(a16 + row * k + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
+      }
+    }
+  }
+  if (tid == 0) fexp[row] = F;
 }
 
 // ---------------------------------------------------------------------------
 // MFMA GEMM
 // ---------------------------------------------------------------------------
 struct GemmParams {
-  const uint16_t* a16;  // [M, K] fp16, row stride K
+  const uint16_t* a16;  // [M, K] fp16 in pair order, row stride K
   const int32_t* fexp;  // [M]
   const uint8_t* packed;
   int64_t ldp;
@@ -99,208 +217,244 @@ struct GemmParams {
   int gshift, marlin, okind, n_out, ow_dt, bias_dt, act_dt;
 };
 
-template <int FMT>
-__device__ __forceinline__ uint32_t gemm_lut_entry(int v) {
-  const int lo = v & 15, hi = v >> 4;
-  if (FMT == SPECTRA_FMT_NF4) {
-    const uint16_t a = f2h(nf4_code_f32(lo)), b = f2h(nf4_code_f32(hi));
-    return (uint32_t)a | ((uint32_t)b << 16);
-  }
-  return (uint32_t)f2h((float)lo) | ((uint32_t)f2h((float)hi) << 16);
+__device__ __forceinline__ uint16_t gm_code_bits(int fmt, int i) {
+  return fmt == SPECTRA_FMT_NF4 ? f2h(nf4_code_f32(i)) : f2h((float)i);
 }
 
-template <int FMT>
-__global__ void __launch_bounds__(kGemmThreads, 2) gemm_kernel(const GemmParams p) {
+template <int FMT, int BN, int NW>
+__global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
+  constexpr int NTHR = 64 * NW;
+  constexpr int WNW = NW / 2;         // waves along N (two along M)
+  constexpr int WN = BN / WNW;        // wave tile: 128 x WN
+  constexpr int NT = WN / 32;         // 32-column MFMA tiles per wave
+  constexpr int BPT = 16 * BN / NTHR; // packed bytes one thread decodes per step
+  constexpr int AU = 4096 / NTHR / 4; // 16-byte activation chunks one thread copies per step
+  constexpr int TPR = 16 / BPT;       // threads per weight row
   extern __shared__ __align__(16) uint8_t smem[];
-  uint16_t* As = (uint16_t*)smem;                       // [kBM][kLdsRow]
-  uint16_t* Ws = (uint16_t*)(smem + kTileBytes);        // [kBN][kLdsRow]
-  uint8_t* lut = smem + 2 * kTileBytes;                 // 256 x 32 columns x 4 bytes
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.x * kBM, n0 = blockIdx.y * kBN;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;  // wave tile origin
-  const int K = p.k;
+  uint16_t* As = (uint16_t*)(smem + kGLut);       // [2][256][kRowH]
+  uint16_t* Ws = As + 2 * kBM * kRowH;            // [2][BN][kRowH]
+  int32_t* fx = (int32_t*)(Ws + 2 * BN * kRowH);  // [256] row exponents
+  uint16_t* codes = (uint16_t*)(fx + kBM);        // [8 waves][16]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * kBM;
+  const int wm = wave / WNW, wn = wave % WNW;
+  const int K = p.k, nk = K / kBK;
+  asm volatile("" ::"s"(p.a16), "s"(p.packed), "s"(p.ldp), "s"(p.scales), "s"(p.lds), "s"(p.m), "s"(p.n),
+               "s"(p.k), "s"(p.gshift), "s"(p.marlin), "s"(p.okind), "s"(p.rowptr), "s"(p.fexp));
 
-  for (int w = tid; w < 256 * 8; w += kGemmThreads) {  // 2048 x 16-byte stores
-    const int v = w >> 3, cq = w & 7;
-    const uint32_t e = gemm_lut_entry<FMT>(v);
-    *(uint4*)(lut + v * 128 + cq * 16) = make_uint4(e, e, e, e);
-  }
+  // ---- operand assignment: A row tid / 2, 32 of its 64 bytes a step; weight row
+  //      tid / TPR, bytes [(tid % TPR) * BPT, + BPT) of the row's 16-byte run ----
+  const int ar = tid / (4 / AU), ah = tid % (4 / AU);  // row, and which AU-chunk part of its 64 bytes
+  const uint16_t* asrc = p.a16 + (int64_t)min(m0 + ar, p.m - 1) * K + 8 * AU * ah;
+  const int wr = tid / TPR, wb0 = (tid % TPR) * BPT;
+  const int wrow = min(n0 + wr, p.n - 1);
+  const uint8_t* wsrc = p.packed + (int64_t)wrow * p.ldp + wb0;
+  const uint16_t* ssrc = p.scales + (int64_t)wrow * p.lds;
+  const uint8_t* zsrc = FMT == SPECTRA_FMT_ASYM_G32 ? p.zeros + (int64_t)wrow * p.ldz : nullptr;
 
-  // per-thread global load assignment
-  const int a_row = tid >> 1, a_half = tid & 1;        // A: 64 bytes of one row
-  const int am = min(m0 + a_row, p.m - 1);
-  const int w_row = tid >> 1, w_half = tid & 1;        // W: 16 packed bytes (32 k) of one row
-  const int wn_g = min(n0 + w_row, p.n - 1);
-  const bool w_row_ok = n0 + w_row < p.n;
-  const uint32_t lanebits = (uint32_t)(lane & 31) << 2;
-
-  // Outliers: a window of the next kWin entries (column, value) of this thread's row,
-  // refilled after it is consumed so the loads fly during the MFMAs.  CSR: cursor over
-  // the row's entries; dense columns: one cursor over idx shared by all rows.
+  // ---- outlier window of this thread's row (CSR cursor, or the shared column list) ----
   int cur = 0, cend = 0;
   if (p.okind == SPECTRA_OUTLIERS_CSR) {
-    cur = p.rowptr[wn_g];
-    cend = p.rowptr[wn_g + 1];
+    cur = p.rowptr[wrow];
+    cend = p.rowptr[wrow + 1];
   } else if (p.okind == SPECTRA_OUTLIERS_COLUMNS) {
     cend = p.n_out;
   }
-  int wc[kWin];
-  uint16_t wv[kWin];
-  auto fill_window = [&]() {
+  // the next kWin entries of the row in a register queue (q[0] = next); consuming one
+  // shifts the queue and loads the entry kWin further, which is read kWin entries later
+  int qc[kWin];
+  uint16_t qv[kWin];
+  int qe = cur + kWin;  // entry index of the next load
+  auto fetch = [&](int e, int& c, uint16_t& v) __attribute__((always_inline)) {
+    const bool ok = e < cend;
+    const int ei = ok ? e : 0;
+    if (p.okind == SPECTRA_OUTLIERS_CSR) {
+      c = ok ? p.ccol[ei] : 0x7fffffff;
+      v = p.cval[ei];
+    } else {
+      c = ok ? (int)p.oidx[ei] : 0x7fffffff;
+      v = f2h(load_elem(p.ow, (int64_t)wrow * p.ldow + ei, p.ow_dt));
+    }
+  };
 #pragma unroll
-    for (int q = 0; q < kWin; ++q) {
-      const int e = cur + q;
-      const bool ok = e < cend;
-      const int ei = ok ? e : 0;
-      if (p.okind == SPECTRA_OUTLIERS_CSR) {
-        wc[q] = ok ? p.ccol[ei] : 0x7fffffff;
-        wv[q] = p.cval[ei];
-      } else {
-        wc[q] = ok ? (int)p.oidx[ei] : 0x7fffffff;
-        wv[q] = f2h(load_elem(p.ow, (int64_t)wn_g * p.ldow + ei, p.ow_dt));
+  for (int q = 0; q < kWin; ++q) {
+    qc[q] = 0x7fffffff;
+    qv[q] = 0;
+  }
+  if (p.okind != SPECTRA_OUTLIERS_NONE)
+#pragma unroll
+    for (int q = 0; q < kWin; ++q) fetch(cur + q, qc[q], qv[q]);
+
+  // ---- global -> register staging, two steps ahead ----
+  // (two named register stages; an array of them would be placed in scratch memory)
+  u32x4_t sa0a, sa0b, sa0c, sa0d, sa1a, sa1b, sa1c, sa1d;
+  u32x4_t sw0, sw1;  // BPT packed bytes in the low BPT / 4 lanes
+  uint16_t ss0 = 0, ss1 = 0;
+  uint8_t sz0 = 0, sz1 = 0;
+  auto load = [&](u32x4_t& ga, u32x4_t& gb, u32x4_t& gc, u32x4_t& gd, u32x4_t& gw, uint16_t& gs, uint8_t& gz,
+                  int step) __attribute__((always_inline)) {
+    const u32x4_t* ap = (const u32x4_t*)(asrc + step * kBK);
+    ga = ap[0];
+    gb = ap[1];
+    if constexpr (AU == 4) {
+      gc = ap[2];
+      gd = ap[3];
+    }
+    if constexpr (BPT == 16) {
+      gw = *(const u32x4_t*)(wsrc + step * 16);
+    } else if constexpr (BPT == 8) {
+      const uint2 v = *(const uint2*)(wsrc + step * 16);
+      gw.x = v.x;
+      gw.y = v.y;
+    } else {
+      gw.x = *(const uint32_t*)(wsrc + step * 16);
+    }
+    gs = ssrc[(step * kBK) >> p.gshift];
+    if constexpr (FMT == SPECTRA_FMT_ASYM_G32) gz = zsrc[step];
+  };
+
+  // ---- nibble-pair LUT: 64 wave-instructions of 1 KB (lane l reads bank l) ----
+  if (lane < 16) codes[wave * 16 + lane] = gm_code_bits(FMT, lane);
+  {
+    uint4* lut = (uint4*)smem;
+    for (int i0 = wave; i0 < 64; i0 += 8 * NW) {
+      uint32_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + NW * j;
+        e[j] = (uint32_t)codes[wave * 16 + 4 * (i & 3) + (lane >> 4)] | ((uint32_t)codes[wave * 16 + (i >> 2)] << 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + NW * j;
+        lut[(16 * (i >> 2) + 4 * (i & 3) + (lane >> 4)) * 16 + (lane & 15)] = make_uint4(e[j], e[j], e[j], e[j]);
+      }
+    }
+  }
+  for (int r = tid; r < kBM; r += NTHR) fx[r] = p.fexp[min(m0 + r, p.m - 1)];
+  const uint32_t lanebits = (uint32_t)lane << 2;
+
+  // ---- register stage -> LDS buffer: activations as loaded, weights decoded ----
+  auto store = [&](u32x4_t ga, u32x4_t gb, u32x4_t gc, u32x4_t gd, u32x4_t gw, uint16_t gs, uint8_t gz, int step,
+                   int buf) __attribute__((always_inline)) {
+    u32x4_t* ad = (u32x4_t*)(As + (buf * kBM + ar) * kRowH + 8 * AU * ah);
+    ad[0] = ga;
+    ad[1] = gb;
+    if constexpr (AU == 4) {
+      ad[2] = gc;
+      ad[3] = gd;
+    }
+    const _Float16 sh = __builtin_bit_cast(_Float16, gs);
+    const f16x2g_t s2 = {sh, sh};
+    uint32_t d[BPT];
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const uint32_t addr = __builtin_amdgcn_perm(gw[b >> 2], lanebits, 0x0c0c0000u | ((4u + (b & 3)) << 8));
+      f16x2g_t c = __builtin_bit_cast(f16x2g_t, *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr);
+      if constexpr (FMT == SPECTRA_FMT_ASYM_G32) {
+        const _Float16 zh = (_Float16)(-(float)gz);
+        const f16x2g_t z2 = {zh, zh};
+        c = c + z2;  // q - z: exact in fp16
+      }
+      c = c * s2;  // one fp16 rounding
+      d[b] = __builtin_bit_cast(uint32_t, c);
+    }
+    uint16_t* wrow_l = Ws + (buf * BN + wr) * kRowH;
+    if constexpr (BPT == 16) {
+      uint4* wd = (uint4*)(wrow_l + 2 * wb0);
+      wd[0] = make_uint4(d[0], d[1], d[2], d[3]);
+      wd[1] = make_uint4(d[4], d[5], d[6], d[7]);
+      wd[2] = make_uint4(d[8], d[9], d[10], d[11]);
+      wd[3] = make_uint4(d[12], d[13], d[14], d[15]);
+    } else if constexpr (BPT == 8) {
+      uint4* wd = (uint4*)(wrow_l + 2 * wb0);
+      wd[0] = make_uint4(d[0], d[1], d[2], d[3]);
+      wd[1] = make_uint4(d[4], d[5], d[6], d[7]);
+    } else {
+      *(uint4*)(wrow_l + 2 * wb0) = make_uint4(d[0], d[1], d[2], d[3]);
+    }
+    // outliers of this row inside the step: the queue head while it lies below the
+    // step's end (ascending columns); the same thread wrote the decoded values above, so
+    // program order suffices
+    if (p.okind != SPECTRA_OUTLIERS_NONE) {
+      const int klo = step * kBK, khi = klo + kBK;
+      while (qc[0] < khi) {
+        const int kk = qc[0] - klo;
+        const int jb = p.marlin ? (kk & 15) : (kk >> 1), h = p.marlin ? (kk >> 4) : (kk & 1);
+        if (kk >= 0 && jb >= wb0 && jb < wb0 + BPT) wrow_l[2 * jb + h] = qv[0];
+#pragma unroll
+        for (int q = 0; q + 1 < kWin; ++q) {
+          qc[q] = qc[q + 1];
+          qv[q] = qv[q + 1];
+        }
+        fetch(qe, qc[kWin - 1], qv[kWin - 1]);
+        ++qe;
       }
     }
   };
-  if (p.okind != SPECTRA_OUTLIERS_NONE) fill_window();
 
-  uint4 ar0, ar1, ar2, ar3, wr;
-  uint16_t sr;
-  uint8_t zr = 0;
-#define SPECTRA_GLOAD(K0)                                                                   \
-  do {                                                                                      \
-    const uint4* asrc_ = (const uint4*)(p.a16 + (int64_t)am * K + (K0) + a_half * 32);      \
-    ar0 = asrc_[0];                                                                         \
-    ar1 = asrc_[1];                                                                         \
-    ar2 = asrc_[2];                                                                         \
-    ar3 = asrc_[3];                                                                         \
-    const int kk_ = (K0) + w_half * 32;                                                     \
-    wr = *(const uint4*)(p.packed + (int64_t)wn_g * p.ldp + (kk_ >> 1));                    \
-    sr = p.scales[(int64_t)wn_g * p.lds + (kk_ >> p.gshift)];                               \
-    if (FMT == SPECTRA_FMT_ASYM_G32) zr = p.zeros[(int64_t)wn_g * p.ldz + (kk_ >> 5)];      \
-  } while (0)
-
-  f16v_t acc[2][2];
+  f16v_t acc[4][NT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  const int nk = K / kBK;
-  SPECTRA_GLOAD(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int k0 = kt * kBK;
-    __syncthreads();  // previous tile fully consumed (and LUT written on the first pass)
-    // ---- activation tile -> LDS
-    {
-      uint4* dst = (uint4*)(As + a_row * kLdsRow + a_half * 32);
-      dst[0] = ar0;
-      dst[1] = ar1;
-      dst[2] = ar2;
-      dst[3] = ar3;
-    }
-    // ---- weight tile: LUT decode, block scale, k order -> LDS
-    {
-      const uint32_t bytes4[4] = {wr.x, wr.y, wr.z, wr.w};
-      uint32_t e[16];
-      const _Float16 sh = __builtin_bit_cast(_Float16, sr);
-      f16x2g_t s2 = {sh, sh};
-      f16x2g_t z2 = {(_Float16)(-(float)zr), (_Float16)(-(float)zr)};
-#pragma unroll
-      for (int b = 0; b < 16; ++b) {
-        const uint32_t byte = (bytes4[b >> 2] >> (8 * (b & 3))) & 0xffu;
-        const uint32_t code2 = *(const uint32_t*)(lut + ((byte << 7) | lanebits));
-        f16x2g_t c = __builtin_bit_cast(f16x2g_t, code2);
-        if (FMT == SPECTRA_FMT_ASYM_G32) c = c + z2;  // q - z, exact
-        c = c * s2;                                   // one fp16 rounding
-        e[b] = __builtin_bit_cast(uint32_t, c);
-      }
-      uint32_t d[16];
-      if (p.marlin) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          d[q] = __builtin_amdgcn_perm(e[2 * q + 1], e[2 * q], 0x05040100u);      // k = 2q, 2q+1
-          d[8 + q] = __builtin_amdgcn_perm(e[2 * q + 1], e[2 * q], 0x07060302u);  // k = 16 + 2q, +1
-        }
-      } else {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) d[q] = e[q];
-      }
-      uint4* dst = (uint4*)(Ws + w_row * kLdsRow + w_half * 32);
-      dst[0] = make_uint4(d[0], d[1], d[2], d[3]);
-      dst[1] = make_uint4(d[4], d[5], d[6], d[7]);
-      dst[2] = make_uint4(d[8], d[9], d[10], d[11]);
-      dst[3] = make_uint4(d[12], d[13], d[14], d[15]);
-      // outliers of this row inside this thread's 32 k (the dequant there is exactly 0):
-      // entries are ascending, so the ones below k0 + kBK are a prefix of the window
-      if (p.okind != SPECTRA_OUTLIERS_NONE) {
-        const int klo = k0 + w_half * 32, khi = klo + 32, kend = k0 + kBK;
-        int used = 0;
-#pragma unroll
-        for (int q = 0; q < kWin; ++q) {
-          if (wc[q] < kend) {
-            if (wc[q] >= klo && wc[q] < khi && w_row_ok) Ws[w_row * kLdsRow + (wc[q] - k0)] = wv[q];
-            ++used;
-          }
-        }
-        cur += used;
-        if (used == kWin) {  // more than kWin entries in one tile: read the rest directly
-          while (cur < cend) {
-            int c;
-            uint16_t v;
-            if (p.okind == SPECTRA_OUTLIERS_CSR) {
-              c = p.ccol[cur];
-              v = p.cval[cur];
-            } else {
-              c = (int)p.oidx[cur];
-              v = f2h(load_elem(p.ow, (int64_t)wn_g * p.ldow + cur, p.ow_dt));
-            }
-            if (c >= kend) break;
-            if (c >= klo && c < khi && w_row_ok) Ws[w_row * kLdsRow + (c - k0)] = v;
-            ++cur;
-          }
-        }
-        if (used > 0) fill_window();
-      }
-    }
-    __syncthreads();
-    if (kt + 1 < nk) SPECTRA_GLOAD(k0 + kBK);  // next tile's global loads fly during the MFMAs
-    // ---- MFMA: 4 k-steps of 16, 2x2 tiles of 32x32 per wave
-#pragma unroll
-    for (int ks = 0; ks < kBK; ks += 16) {
-      h8_t af[2], bf[2];
-      const int kof = ks + 8 * (lane >> 5);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        af[i] = *(const h8_t*)(As + (wm + i * 32 + (lane & 31)) * kLdsRow + kof);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        bf[j] = *(const h8_t*)(Ws + (wn + j * 32 + (lane & 31)) * kLdsRow + kof);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-    }
-  }
+  load(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 0);
+  if (nk > 1) load(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, 1);
+  __syncthreads();  // LUT and code tables
+  store(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 0, 0);
+  if (nk > 2) load(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 2);
+  __syncthreads();
 
-#undef SPECTRA_GLOAD
-  // ---- epilogue: C[row][col], row = 8*(r/4) + 4*(lane/32) + r%4, col = lane%32
+  const int arow = wm * 128 + (lane & 31), brow = wn * WN + (lane & 31), kq = 8 * (lane >> 5);
+  auto mfma_step = [&](int buf) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+    for (int s16 = 0; s16 < kBK; s16 += 16) {
+      h8_t af[4], bf[NT];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = n0 + wn + j * 32 + (lane & 31);
-      if (col >= p.n) continue;
-      const float bv = p.bias ? load_elem(p.bias, col, p.bias_dt) : 0.0f;
+      for (int i = 0; i < 4; ++i) af[i] = *(const h8_t*)(As + (buf * kBM + arow + 32 * i) * kRowH + s16 + kq);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) bf[j] = *(const h8_t*)(Ws + (buf * BN + brow + 32 * j) * kRowH + s16 + kq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  // two steps per iteration so the register stages have static indices
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    store(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, kt + 1, 1);  // step kt+1 -> buffer 1 (buffer 1 free since the last barrier)
+    if (kt + 3 < nk) load(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, kt + 3);
+    mfma_step(0);                          // step kt from buffer 0
+    __syncthreads();
+    if (kt + 2 < nk) {
+      store(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, kt + 2, 0);
+      if (kt + 4 < nk) load(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, kt + 4);
+    }
+    mfma_step(1);
+    __syncthreads();
+  }
+  if (kt < nk) mfma_step(0);  // odd step count: the last step sits in buffer 0
+
+  // ---- epilogue: D[row][col], row = 8 (r / 4) + 4 (lane / 32) + r % 4, col = lane % 32 ----
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int col = n0 + wn * WN + j * 32 + (lane & 31);
+    if (col >= p.n) continue;
+    const float bv = p.bias ? load_elem(p.bias, col, p.bias_dt) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < p.m) {
-          const int F = p.fexp[row];
-          const float y = acc[i][j][r] * __builtin_bit_cast(float, (uint32_t)(127 - F) << 23) + bv;
-          ((uint16_t*)p.out)[(int64_t)row * p.ldo + col] = from_f32_16(y, p.act_dt);
+        const int rl = wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m0 + rl < p.m) {
+          const float y = acc[i][j][r] * __builtin_bit_cast(float, (uint32_t)(127 - fx[rl]) << 23) + bv;
+          ((uint16_t*)p.out)[(int64_t)(m0 + rl) * p.ldo + col] = from_f32_16(y, p.act_dt);
         }
       }
     }
@@ -335,10 +489,11 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   SPECTRA_REQUIRE(m >= 1 && m < (1LL << 31) / kBM, "m out of range");
   SPECTRA_REQUIRE(act_dtype == SPECTRA_F16 || act_dtype == SPECTRA_BF16, "activations must be fp16 or bf16");
   SPECTRA_REQUIRE(lda >= w->k && ldo >= w->n, "row stride too small");
-  if (w->k % kBK != 0) return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family needs K % 64 == 0");
-  if (w->k > 40000) return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family serves K <= 40000");
+  if (w->k % 64 != 0) return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family needs K % 64 == 0");
+  if (w->k > 32768) return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family serves K <= 32768");
   if (w->format == SPECTRA_FMT_NF4 && w->group_size < 32)
     return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family needs an NF4 block of at least 32");
+  if (w->hadamard_block > 1024) return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family serves hadamard_block <= 1024");
   SPECTRA_REQUIRE((reinterpret_cast<uintptr_t>(w->packed) % 16) == 0 && w->packed_stride % 16 == 0,
                   "packed weights must be 16-byte aligned with a row stride multiple of 16");
   const size_t need = spectra_w4a16_gemm_workspace(w, m, act_dtype);
@@ -353,12 +508,23 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   uint16_t* a16 = (uint16_t*)workspace;
   int32_t* fexp = (int32_t*)((uint8_t*)workspace + align256((size_t)m * w->k * 2));
   const int had = w->hadamard_block;
-  const float div = had ? (float)std::sqrt((double)had) : 1.0f;
-  const size_t prep_lds = (size_t)w->k * 4;
-  int st2 = ensure_lds_limit((const void*)act_prep_kernel);
+  int log_had = 0;
+  while (had > 1 && (1 << log_had) < had) ++log_had;
+  const float div = had > 1 ? (float)std::sqrt((double)had) : 1.0f;
+  // chunks of 8 activations per prep thread, rounded up to a power of two
+  const int64_t n8 = w->k / 8;
+  const int pu = n8 <= 256 ? 1 : n8 <= 512 ? 2 : n8 <= 1024 ? 4 : n8 <= 2048 ? 8 : 16;
+  const void* prep = pu == 1 ? (const void*)gemm_prep_kernel<1> : pu == 2 ? (const void*)gemm_prep_kernel<2>
+                   : pu == 4 ? (const void*)gemm_prep_kernel<4> : pu == 8 ? (const void*)gemm_prep_kernel<8>
+                             : (const void*)gemm_prep_kernel<16>;
+  int st2 = ensure_lds_limit(prep);
   if (st2 != SPECTRA_OK) return st2;
-  hipLaunchKernelGGL(act_prep_kernel, dim3((unsigned)m), dim3(kPrepThreads), prep_lds, s, a, lda, (int)act_dtype,
-                     w->k, had, div, a16, fexp);
+  const int vec = (reinterpret_cast<uintptr_t>(a) % 16) == 0 && lda % 8 == 0;
+  const int kk32 = (int)w->k, marl = w->marlin_layout ? 1 : 0;
+  const size_t prep_lds = (size_t)w->k * (had > 512 ? 4 : 2);
+  void* pargs[] = {(void*)&a, (void*)&lda, (void*)&act_dtype, (void*)&kk32, (void*)&log_had, (void*)&div,
+                   (void*)&marl, (void*)&vec, (void*)&a16, (void*)&fexp};
+  SPECTRA_HIP_CHECK(hipLaunchKernel(prep, dim3((unsigned)m), dim3(kPrepThreads), pargs, prep_lds, s));
   SPECTRA_HIP_CHECK(hipGetLastError());
 
   GemmParams p;
@@ -378,16 +544,23 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   p.okind = csr ? SPECTRA_OUTLIERS_CSR
                 : (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS ? SPECTRA_OUTLIERS_COLUMNS : SPECTRA_OUTLIERS_NONE);
   p.n_out = w->num_outliers; p.ow_dt = w->outlier_w_dtype; p.bias_dt = w->bias_dtype; p.act_dt = act_dtype;
-  const size_t lds = 2 * kTileBytes + 256 * 128;
-  dim3 grid((unsigned)((m + kBM - 1) / kBM), (unsigned)((w->n + kBN - 1) / kBN));
-  const void* kern = w->format == SPECTRA_FMT_NF4 ? (const void*)gemm_kernel<SPECTRA_FMT_NF4>
-                                                  : (const void*)gemm_kernel<SPECTRA_FMT_ASYM_G32>;
-  st2 = ensure_lds_limit(kern);
-  if (st2 != SPECTRA_OK) return st2;
+  // 256-wide tiles when they fill the GPU, otherwise 128-wide (twice the workgroups)
+  const int64_t mt = (m + kBM - 1) / kBM;
+  const bool wide = mt * ((w->n + 255) / 256) >= 256;
+  const int BN = wide ? 256 : 128;
+  const size_t lds = (size_t)kGLut + (size_t)2 * (kBM + BN) * kRowH * 2 + kBM * 4 + kGemmWaves * 16 * 2;
+  dim3 grid((unsigned)((w->n + BN - 1) / BN), (unsigned)mt);
+  const void* kern;
   if (w->format == SPECTRA_FMT_NF4)
-    hipLaunchKernelGGL(gemm_kernel<SPECTRA_FMT_NF4>, grid, dim3(kGemmThreads), lds, s, p);
+    kern = wide ? (const void*)gemm_kernel<SPECTRA_FMT_NF4, 256, kGemmWaves>
+                : (const void*)gemm_kernel<SPECTRA_FMT_NF4, 128, kGemmWaves>;
   else
-    hipLaunchKernelGGL(gemm_kernel<SPECTRA_FMT_ASYM_G32>, grid, dim3(kGemmThreads), lds, s, p);
+    kern = wide ? (const void*)gemm_kernel<SPECTRA_FMT_ASYM_G32, 256, kGemmWaves>
+                : (const void*)gemm_kernel<SPECTRA_FMT_ASYM_G32, 128, kGemmWaves>;
+  st2 = ensure_lds_limit(kern, true);
+  if (st2 != SPECTRA_OK) return st2;
+  void* kargs[] = {(void*)&p};
+  SPECTRA_HIP_CHECK(hipLaunchKernel(kern, grid, dim3(64 * kGemmWaves), kargs, lds, s));
   SPECTRA_HIP_CHECK(hipGetLastError());
   return SPECTRA_OK;
 }
