@@ -18,6 +18,7 @@
  *   spectra_quantize_nf4    <- Format B quantizer (no reference code; built on
  *                              compressor.py:22-42 codebook and FWHT)
  *   spectra_fwht_rows       <- spectra/compressor.py:29-42 fast_walsh_hadamard_transform
+ *   spectra_outlier_columns <- spectra/compressor.py:158-215 _isolate_hdsq_outliers
  */
 #ifndef SPECTRA_HIP_H_
 #define SPECTRA_HIP_H_
@@ -152,6 +153,24 @@ int spectra_quantize_nf4(const void* w, int64_t ldw, int32_t w_dtype, int64_t n,
 int spectra_fwht_rows(const void* x, int64_t ldx, int32_t in_dtype, int64_t rows, int64_t k,
                       int32_t block, void* out, int64_t ldo, int32_t out_dtype,
                       spectra_stream_t stream);
+
+/*
+ * Outlier-column selection of the compressor (compressor.py:158-215): column saliency
+ * sqrt(sum_r w[r, j]^2) (times norm_vector[j] when given; fp32, 4096-row chunks),
+ * kurtosis of the saliencies (clamped to >= 1), ratio = base_ratio, or with `adaptive`
+ * clamp(fp32(base_ratio * (1 + 0.15 log1p(max(0, kurtosis - 3)))), 0.005, 0.03),
+ * n_out = max(1, round-half-even(K * ratio)) columns of largest saliency (ties at the
+ * threshold: lowest column first), written ascending.
+ * w [n, k] (F16/BF16/F32, row stride ldw); norm_vector fp32 [k] or NULL.
+ * Outputs (device): idx int32 [k] (the first *n_out entries are valid), n_out int32 [1],
+ * stats fp32 [2] = {ratio, kurtosis}.  workspace: spectra_outlier_columns_workspace(k)
+ * bytes.  k <= 32768.
+ */
+size_t spectra_outlier_columns_workspace(int64_t k);
+int spectra_outlier_columns(const void* w, int64_t ldw, int32_t w_dtype, int64_t n, int64_t k,
+                            const float* norm_vector, double base_ratio, int32_t adaptive, int32_t* idx,
+                            int32_t* n_out, float* stats, void* workspace, size_t workspace_bytes,
+                            spectra_stream_t stream);
 
 #ifdef __cplusplus
 }

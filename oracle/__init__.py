@@ -24,5 +24,8 @@ Pinning status per function:
                         reconstruction of every code point, monotonicity.
   nf4_dequant           pinned: closed form + torch evaluation.
   linear_ref            pinned: fp64 matmul (numpy) vs float32 torch matmul.
+  select_outlier_columns pinned: golden vectors written by the reference's own
+                        _isolate_hdsq_outliers (tests/golden/make_outlier_golden.py)
+                        + closed-form invariants (Gaussian kurtosis, dominant column).
 """
 from .spectra_oracle import *  # noqa: F401,F403

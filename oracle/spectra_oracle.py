@@ -34,8 +34,7 @@ __all__ = [
     "fwht", "rotate_blocks",
     "quantize_group32", "pack_nibbles", "unpack_nibbles", "pack_zeros", "unpack_zeros",
     "dequant_group32", "apply_outlier_columns", "compute_group32_quant",
-    "nf4_quantize", "nf4_dequant", "nearest_code", "csr_from_mask", "linear_ref", "format_a_linear_ref",
-]
+    "nf4_quantize", "nf4_dequant", "nearest_code", "csr_from_mask", "linear_ref", "format_a_linear_ref", "select_outlier_columns"]
 
 # compressor.py:22-27 -- the 16 NF4 levels as float32 literals (index 7 is 0.0).
 NF4_CODEBOOK = np.array([
@@ -354,3 +353,41 @@ def linear_ref(x: np.ndarray, x_dtype: str, w_eff: np.ndarray, w_dtype: str, had
     if bias is not None:
         y = y + to_f32(bias, bias_dtype).astype(np.float64)[None, :]
     return y
+
+
+# ---------------------------------------------------------------------------
+# Outlier-column selection (compressor.py:158-215, _isolate_hdsq_outliers)
+# ---------------------------------------------------------------------------
+def select_outlier_columns(w: np.ndarray, w_dtype: str = "float16", norm: Optional[np.ndarray] = None,
+                           base_ratio: float = 0.01, adaptive: bool = True) -> Tuple[np.ndarray, float, float]:
+    """Column saliency, kurtosis-adaptive ratio, top-k columns (compressor.py:158-206).
+
+    Saliency ``|gamma_j| * ||W[:, j]||_2`` (plain norm without a norm vector, :173-187);
+    kurtosis ``max(1, m4 / (var + 1e-8)^2)`` (:189-192); adaptive ratio
+    ``clamp(fp32(base * (1 + 0.15 log1p(max(0, kurt - 3)))), 0.005, 0.03)`` -- the
+    reference builds a float32 tensor from the product and clamps it in float32 (:193-197);
+    ``n_out = max(1, round(K * ratio))`` with Python's round-half-even (:201); the n_out
+    largest saliencies, ascending column order (:202-203; ties: lowest column first).
+    The norms and moments are computed in float64 here (the reference's float32
+    reduction order is unspecified; the selection agrees except at exact near-ties).
+    Returns (idx int32 [n_out], ratio, kurtosis).
+    """
+    w32 = to_f32(w, w_dtype).astype(np.float64)
+    sal = np.sqrt((w32 * w32).sum(axis=0))
+    if norm is not None and norm.size == w.shape[1]:
+        sal = norm.astype(np.float64) * sal
+    mu = sal.mean()
+    sigma2 = ((sal - mu) ** 2).mean() + 1e-8
+    m4 = ((sal - mu) ** 4).mean()
+    kurt = max(1.0, float(m4 / (sigma2 ** 2)))
+    if adaptive:
+        excess = max(0.0, kurt - 3.0)
+        k_mult = 1.0 + 0.15 * math.log1p(excess)
+        r32 = np.float32(base_ratio * k_mult)
+        ratio = float(min(max(r32, np.float32(0.005)), np.float32(0.03)))
+    else:
+        ratio = float(base_ratio)
+    k = w.shape[1]
+    n_out = min(k, max(1, int(round(k * ratio))))
+    order = np.lexsort((np.arange(k), -sal))  # descending saliency, lowest column first on ties
+    return np.sort(order[:n_out]).astype(np.int32), ratio, kurt

@@ -17,7 +17,7 @@ from . import _lib as L
 from .kernels import _DT, _dtype_code, _rows, _stream
 
 __all__ = ["SpectraCompressor", "quantize_group32", "compute_group32_quant", "unpack_zeros", "NF4Weight",
-           "quantize_nf4", "csr_from_mask"]
+           "quantize_nf4", "csr_from_mask", "select_outlier_columns"]
 
 
 class SpectraCompressor:
@@ -44,6 +44,20 @@ class SpectraCompressor:
     @staticmethod
     def _compute_group32_quant(w: torch.Tensor, group_size: int = 32, outlier_idx: Optional[torch.Tensor] = None):
         return compute_group32_quant(w, group_size=group_size, outlier_idx=outlier_idx)
+
+    def _isolate_hdsq_outliers(self, w: torch.Tensor, norm_vector: Optional[torch.Tensor] = None):
+        """compressor.py:158-215: returns (w with the outlier columns zeroed when N <= 4096, else
+        None; outlier column indices int32 on the CPU, ascending; the outlier columns in w's
+        dtype; ratio; kurtosis).  The selection runs on the GPU (spectra_outlier_columns)."""
+        idx, ratio, kurtosis = select_outlier_columns(w, norm_vector, self.base_outlier_ratio,
+                                                      self.adaptive_kurtosis)
+        idx_cpu = idx.cpu().contiguous()
+        outlier_w = w[:, idx_cpu.long().to(w.device)].contiguous()
+        w_dense = None
+        if w.shape[0] <= 4096:  # compressor.py:208-210
+            w_dense = w.clone()
+            w_dense[:, idx_cpu.long().to(w.device)] = 0.0
+        return w_dense, idx_cpu, outlier_w, ratio, kurtosis
 
 
 def _weights(w: torch.Tensor, device: Optional[torch.device]) -> Tuple[torch.Tensor, int]:
@@ -163,3 +177,29 @@ def quantize_nf4(w: torch.Tensor, blocksize: int = 64, hadamard_block: int = 0,
         int(bool(marlin_layout)), rowptr.data_ptr() if has else None, col.data_ptr() if has else None,
         val.data_ptr() if has else None, packed.data_ptr(), absmax.data_ptr(), _stream(dev)))
     return NF4Weight(packed, absmax, rowptr, col, val, k, blocksize, hadamard_block, bool(marlin_layout))
+
+
+def select_outlier_columns(w: torch.Tensor, norm_vector: Optional[torch.Tensor] = None, base_ratio: float = 0.01,
+                           adaptive: bool = True, device: Optional[torch.device] = None):
+    """Outlier-column selection on the GPU (compressor.py:158-206): returns (idx int32 [n_out]
+    ascending, on the GPU; ratio; kurtosis)."""
+    if w.dim() != 2:
+        raise ValueError("w must be 2-D")
+    n, k = w.shape
+    w2, ldw = _weights(w, device)
+    dev = w2.device
+    norm = None
+    if norm_vector is not None and norm_vector.numel() == k:  # compressor.py:183-184
+        norm = norm_vector.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+    lib = L.load()
+    ws = torch.empty(max(int(lib.spectra_outlier_columns_workspace(k)), 4), dtype=torch.uint8, device=dev)
+    idx = torch.empty(k, dtype=torch.int32, device=dev)
+    cnt = torch.empty(1, dtype=torch.int32, device=dev)
+    stats = torch.empty(2, dtype=torch.float32, device=dev)
+    L.check("spectra_outlier_columns", lib.spectra_outlier_columns(
+        w2.data_ptr(), ldw, _dtype_code(w2, _DT.keys(), "w"), n, k, norm.data_ptr() if norm is not None else None,
+        float(base_ratio), int(bool(adaptive)), idx.data_ptr(), cnt.data_ptr(), stats.data_ptr(), ws.data_ptr(),
+        ws.numel(), _stream(dev)))
+    n_out = int(cnt.item())
+    st = stats.cpu()
+    return idx[:n_out], float(st[0]), float(st[1])

@@ -494,3 +494,42 @@ def test_module_edge_cases(hip):
         C.SpectraCompressor(group_size=64)
     with pytest.raises(NotImplementedError):
         C.SpectraCompressor(hadamard_incoherence=True)
+
+
+# ---------------------------------------------------------------------------
+# outlier-column selection (compressor.py:158-215)
+# ---------------------------------------------------------------------------
+def test_outlier_selection_reference_vectors(hip):
+    """The GPU selection against the reference's own _isolate_hdsq_outliers outputs."""
+    sys.path.insert(0, os.path.join(HERE, "golden"))
+    from make_outlier_golden import cases, make_inputs
+    g = np.load(os.path.join(HERE, "golden", "outlier_select.npz"))
+    comp = C.SpectraCompressor()
+    for i, (name, n, k, dt, heavy, with_norm) in enumerate(cases()):
+        case(name=name, n=n, k=k)
+        w, norm = make_inputs(i, n, k, dt, heavy, with_norm)
+        w_dense, idx, ow, ratio, kurt = comp._isolate_hdsq_outliers(w.cuda(), norm)
+        assert idx.dtype == torch.int32 and idx.device.type == "cpu"
+        assert np.array_equal(idx.numpy(), g[f"{name}/idx"]), name
+        assert abs(ratio - float(g[f"{name}/ratio"])) <= 1e-6 * ratio
+        assert abs(kurt - float(g[f"{name}/kurtosis"])) <= 1e-4 * kurt
+        assert torch.equal(ow.cpu(), w[:, idx.long()])
+        if n <= 4096:
+            assert torch.equal(w_dense[:, idx.long().cuda()].cpu(), torch.zeros(n, idx.numel(), dtype=w.dtype))
+        else:
+            assert w_dense is None
+
+
+@pytest.mark.parametrize("adaptive", [True, False])
+def test_outlier_selection_against_oracle(hip, adaptive):
+    rng = np.random.default_rng(11 + adaptive)
+    n, k = 3072, 8192
+    w = rand_np(rng, (n, k), 0.02)
+    cols = rng.permutation(k)[:60]
+    w[:, cols] *= (1 + 10 * rng.random(60)).astype(np.float16)
+    norm = (rng.random(k) + 0.5).astype(np.float32)
+    case(n=n, k=k, adaptive=adaptive)
+    idx, ratio, kurt = C.select_outlier_columns(cuda(w), torch.from_numpy(norm), 0.01, adaptive)
+    o_idx, o_ratio, o_kurt = O.select_outlier_columns(w, "float16", norm, 0.01, adaptive)
+    assert np.array_equal(host(idx), o_idx)
+    assert abs(ratio - o_ratio) <= 1e-6 * o_ratio and abs(kurt - o_kurt) <= 1e-4 * o_kurt

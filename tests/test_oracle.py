@@ -13,6 +13,7 @@ butterfly pairing, float64 leaking into float32 arithmetic) fails it:
 import json
 import math
 import os
+import sys
 
 import numpy as np
 import pytest
@@ -299,3 +300,46 @@ def test_linear_ref_matches_torch():
     y = O.linear_ref(x, "float16", w, "float16", bias=b)
     t = torch.from_numpy(x).float() @ torch.from_numpy(w).float().T + torch.from_numpy(b).float()
     assert np.max(np.abs(y - t.double().numpy())) < 1e-4
+
+
+# ---------------------------------------------------------------------------
+# Outlier-column selection (compressor.py:158-215) against the reference's own vectors
+# ---------------------------------------------------------------------------
+def _outlier_cases():
+    import hashlib
+    import torch
+    sys.path.insert(0, os.path.join(HERE, "golden"))
+    from make_outlier_golden import cases, make_inputs
+    g = np.load(os.path.join(HERE, "golden", "outlier_select.npz"))
+    for i, (name, n, k, dt, heavy, with_norm) in enumerate(cases()):
+        w, norm = make_inputs(i, n, k, dt, heavy, with_norm)
+        assert hashlib.sha256(w.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest() == str(g[f"{name}/w_sha256"])
+        yield name, w, norm, g[f"{name}/idx"], float(g[f"{name}/ratio"]), float(g[f"{name}/kurtosis"])
+
+
+def test_outlier_selection_oracle_matches_reference_vectors():
+    import torch
+    for name, w, norm, idx, ratio, kurt in _outlier_cases():
+        wdt = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}[w.dtype]
+        wn = w.view(torch.int16).numpy().view(np.uint16) if w.dtype == torch.bfloat16 else w.numpy()
+        o_idx, o_ratio, o_kurt = O.select_outlier_columns(wn, wdt, norm.numpy() if norm is not None else None)
+        assert np.array_equal(o_idx, idx), name
+        # the reference's moments are float32 sums (unspecified order): the fp32 ratio may
+        # land one fp32 ulp apart; the selected columns must be identical
+        assert abs(o_ratio - ratio) <= 1e-6 * ratio, name
+        assert abs(o_kurt - kurt) <= 1e-4 * kurt, name
+
+
+def test_outlier_selection_invariants():
+    """Closed forms: a Gaussian matrix has kurtosis ~3 -> ratio = base (non-excess); a
+    single dominant column is always selected; the count follows round-half-even."""
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((4096, 512)).astype(np.float32)
+    idx, ratio, kurt = O.select_outlier_columns(w, "float32", None, 0.01, True)
+    assert 1.0 <= kurt < 3.5 and abs(ratio - 0.01) < 1e-3 and idx.size == round(512 * ratio)
+    w[:, 77] *= 50.0
+    idx, ratio, kurt = O.select_outlier_columns(w, "float32", None, 0.01, True)
+    assert 77 in idx and kurt > 100
+    _, r2, _ = O.select_outlier_columns(w, "float32", None, 0.01, False)
+    assert r2 == 0.01
+    assert np.all(np.diff(idx) > 0)
