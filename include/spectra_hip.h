@@ -19,6 +19,7 @@
  *                              compressor.py:22-42 codebook and FWHT)
  *   spectra_fwht_rows       <- spectra/compressor.py:29-42 fast_walsh_hadamard_transform
  *   spectra_outlier_columns <- spectra/compressor.py:158-215 _isolate_hdsq_outliers
+ *   spectra_w4_embedding    <- spectra/engine.py:127-212 SpectraFusedEmbedding.forward
  */
 #ifndef SPECTRA_HIP_H_
 #define SPECTRA_HIP_H_
@@ -120,6 +121,14 @@ int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, int64_t ldx,
  */
 int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t ldo, int32_t out_dtype,
                        spectra_stream_t stream);
+
+/*
+ * Embedding gather (engine.py:127-212): out[b, :] = W_eff[ids[b], :] for b < n_ids,
+ * bit-identical to the same rows of spectra_w4_dequant (ids: device int64 [n_ids]; an id
+ * outside [0, N) yields a row of zeros).  out: out_dtype [n_ids, K], row stride ldo.
+ */
+int spectra_w4_embedding(const spectra_qweight_t* w, const int64_t* ids, int64_t n_ids, void* out, int64_t ldo,
+                         int32_t out_dtype, spectra_stream_t stream);
 
 /*
  * Format A quantizer (compressor.py:71-156): w [n, k] (F16/BF16/F32, row stride ldw);

@@ -56,6 +56,8 @@ SIGNATURES = {
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "spectra_fwht_rows": (c_int32, [c_void_p, c_int64, c_int32, c_int64, c_int64, c_int32, c_void_p, c_int64,
                                     c_int32, c_void_p]),
+    "spectra_w4_embedding": (c_int32, [ctypes.POINTER(QWeight), c_void_p, c_int64, c_void_p, c_int64, c_int32,
+                                       c_void_p]),
     "spectra_outlier_columns_workspace": (c_size_t, [c_int64]),
     "spectra_outlier_columns": (c_int32, [c_void_p, c_int64, c_int32, c_int64, c_int64, c_void_p, ctypes.c_double,
                                           c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

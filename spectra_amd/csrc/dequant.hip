@@ -50,9 +50,62 @@ __global__ void __launch_bounds__(kDqThreads) scatter_csr_kernel(spectra_qweight
     store_elem(out, row * ldo + w.csr_col[e], out_dt, h2f(w.csr_val[e]));
 }
 
+// Embedding gather (engine.py:127-212, SpectraFusedEmbedding.forward): row ids[b] of
+// W_eff, bit-identical to the same row of spectra_w4_dequant.  One workgroup per id: the
+// dense values first, then (after the barrier) the row's outlier columns / CSR entries.
+// Ids outside [0, N) produce a row of zeros.
+__global__ void __launch_bounds__(kDqThreads) embed_kernel(spectra_qweight_t w, const int64_t* __restrict__ ids,
+                                                            void* __restrict__ out, int64_t ldo, int out_dt) {
+  const int64_t b = blockIdx.x;
+  const int64_t id = ids[b];
+  const bool ok = id >= 0 && id < w.n;
+  const int64_t row = ok ? id : 0;
+  const int64_t kb = w.k / 2;
+  for (int64_t j = threadIdx.x; j < kb; j += blockDim.x) {
+    const uint8_t byte = w.packed[row * w.packed_stride + j];
+    for (int half = 0; half < 2; ++half) {
+      const int q = half ? (byte >> 4) : (byte & 15);
+      const int64_t kk = nibble_k(j, half, w.marlin_layout);
+      float v;
+      if (w.format == SPECTRA_FMT_ASYM_G32) {
+        const int64_t g = kk / 32;
+        v = ((float)q - (float)w.zeros[row * w.zeros_stride + g]) * h2f(w.scales[row * w.scales_stride + g]);
+      } else {
+        v = nf4_code_f32(q) * h2f(w.scales[row * w.scales_stride + kk / w.group_size]);
+      }
+      store_elem(out, b * ldo + kk, out_dt, ok ? v : 0.0f);
+    }
+  }
+  __syncthreads();
+  if (!ok) return;
+  if (w.outlier_kind == SPECTRA_OUTLIERS_COLUMNS) {
+    for (int j = threadIdx.x; j < w.num_outliers; j += blockDim.x)
+      store_elem(out, b * ldo + w.outlier_idx[j], out_dt,
+                 load_elem(w.outlier_w, row * w.outlier_w_stride + j, w.outlier_w_dtype));
+  } else if (w.outlier_kind == SPECTRA_OUTLIERS_CSR) {
+    for (int e = w.csr_rowptr[row] + threadIdx.x; e < w.csr_rowptr[row + 1]; e += blockDim.x)
+      store_elem(out, b * ldo + w.csr_col[e], out_dt, h2f(w.csr_val[e]));
+  }
+}
+
 }  // namespace spectra
 
 using namespace spectra;
+
+extern "C" int spectra_w4_embedding(const spectra_qweight_t* w, const int64_t* ids, int64_t n_ids, void* out,
+                                    int64_t ldo, int32_t out_dtype, spectra_stream_t stream) {
+  int st = validate_qweight(w);
+  if (st != SPECTRA_OK) return st;
+  SPECTRA_REQUIRE(ids != nullptr && out != nullptr, "ids/out is NULL");
+  SPECTRA_REQUIRE(n_ids >= 0 && n_ids < (1LL << 31), "n_ids out of range");
+  SPECTRA_REQUIRE(ldo >= w->k, "out row stride smaller than K");
+  SPECTRA_REQUIRE(out_dtype >= SPECTRA_F16 && out_dtype <= SPECTRA_F32, "bad out dtype");
+  if (n_ids == 0) return SPECTRA_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3((unsigned)n_ids), dim3(kDqThreads), 0, (hipStream_t)stream, *w, ids, out, ldo,
+                     (int)out_dtype);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
 
 extern "C" int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t ldo, int32_t out_dtype,
                                   spectra_stream_t stream) {

@@ -25,7 +25,7 @@ import torch
 from . import _lib as L
 
 __all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_dequant", "fwht_rows",
-           "QWeightOperands", "GEMV_MAX_M"]
+           "QWeightOperands", "GEMV_MAX_M", "w4_embedding"]
 
 GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
 
@@ -253,6 +253,25 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch
                                                           _dtype_code(out, _DT.keys(), "out_dtype"),
                                                           _stream(out.device)))
     return out
+
+
+def w4_embedding(ops: QWeightOperands, ids: torch.Tensor, out_dtype: torch.dtype = torch.float16,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Gather-dequantize rows ``ids`` of a quantized weight (engine.py:167-212), bit-identical
+    to the same rows of ``w4_dequant``.  Returns ``ids.shape + (K,)``."""
+    if not ids.is_cuda:
+        raise ValueError("ids must be on the GPU")
+    flat = ids.reshape(-1)
+    if flat.dtype != torch.int64:
+        flat = flat.to(torch.int64)
+    flat = flat.contiguous()
+    if out is None:
+        out = torch.empty((flat.numel(), ops.k), device=ids.device, dtype=out_dtype)
+    lib = L.load()
+    L.check("spectra_w4_embedding", lib.spectra_w4_embedding(ops.ptr(), flat.data_ptr(), flat.numel(), out.data_ptr(),
+                                                              out.stride(0), _dtype_code(out, _DT.keys(), "out"),
+                                                              _stream(ids.device)))
+    return out.reshape(tuple(ids.shape) + (ops.k,))
 
 
 def fwht_rows(x: torch.Tensor, block: int, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
