@@ -20,6 +20,11 @@
  *   spectra_fwht_rows       <- spectra/compressor.py:29-42 fast_walsh_hadamard_transform
  *   spectra_outlier_columns <- spectra/compressor.py:158-215 _isolate_hdsq_outliers
  *   spectra_w4_embedding    <- spectra/engine.py:127-212 SpectraFusedEmbedding.forward
+ *   spectra_rmsnorm, spectra_rope_append, spectra_attend_decode, spectra_silu_mul
+ *                           <- the Inductor-fused RMSNorm / RoPE / SiLU submodules and the
+ *                              static-cache attention of the decode step (engine.py:1240-1250,
+ *                              :1387-1415)
+ *   spectra_greedy_next     <- spectra/engine.py:1690-1697 sample_token (temperature 0)
  */
 #ifndef SPECTRA_HIP_H_
 #define SPECTRA_HIP_H_
@@ -180,6 +185,53 @@ int spectra_outlier_columns(const void* w, int64_t ldw, int32_t w_dtype, int64_t
                             const float* norm_vector, double base_ratio, int32_t adaptive, int32_t* idx,
                             int32_t* n_out, float* stats, void* workspace, size_t workspace_bytes,
                             spectra_stream_t stream);
+
+/* ---- decode-layer kernels between the quantized linears ----------------------------------
+ * Replace the reference's Inductor-fused non-linear submodules (RMSNorm, SiLU, RoPE;
+ * spectra/engine.py:1240-1250) and its static-cache attention for graph replay
+ * (engine.py:1387-1415).  All activations fp16.  The token positions are device int64, so
+ * a decode step captures into a HIP graph with no host-side value.
+ */
+
+/* Optional residual add then RMSNorm of `rows` rows: when residual != NULL,
+ * h = fp16(h + residual) in place; x = fp16(h * rsqrt(mean(h^2) + eps) * weight).
+ * h, residual, x [rows, hidden] contiguous; weight fp32 [hidden]. */
+int spectra_rmsnorm(void* h, const void* residual, const float* weight, float eps, int64_t rows, int64_t hidden,
+                    void* x, spectra_stream_t stream);
+
+/* Rotary embedding (pairs (i, i + head_dim/2), fp32 math) of the q and k heads of `tokens`
+ * fused-QKV rows (row stride ldqkv: heads q heads, kv_heads k heads, kv_heads v heads), and
+ * the KV-cache append at pos[t]: q_rot [tokens, heads, head_dim]; k_cache and v_cache
+ * [kv_heads, max_seq, head_dim].  cos_t, sin_t fp32 [max_seq, head_dim/2].  A position
+ * outside [0, max_seq) writes nothing. */
+int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t tokens, const int64_t* pos, const float* cos_t,
+                        const float* sin_t, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq,
+                        void* q_rot, void* k_cache, void* v_cache, spectra_stream_t stream);
+
+/* Batch-1 decode attention of q_rot [heads, head_dim] over cache positions [0, *pos] of
+ * k_cache / v_cache [kv_heads, max_seq, head_dim] (grouped-query: query head h reads KV head
+ * h / (heads / kv_heads); 1, 2, 3, 4, 6 or 8 query heads per KV head; head_dim 64, 128 or
+ * 256; 16-byte aligned), scale 1/sqrt(head_dim), fp32 softmax, fp16 out [heads, head_dim].
+ * The sequence is split into spectra_attend_spans(max_seq) spans of 64 positions merged by
+ * log-sum-exp; workspace >= spectra_attend_workspace(heads, head_dim, max_seq) bytes. */
+int32_t spectra_attend_spans(int32_t max_seq);
+size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq);
+int spectra_attend_decode(const void* q_rot, const void* k_cache, const void* v_cache, const int64_t* pos,
+                          int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq, void* workspace,
+                          size_t workspace_bytes, void* out, spectra_stream_t stream);
+
+/* act [rows, inter] = fp16(silu(g) * u) where g = gate_up[:, :inter], u = gate_up[:, inter:]
+ * (row stride ldgu >= 2 * inter). */
+int spectra_silu_mul(const void* gate_up, int64_t ldgu, int64_t rows, int64_t inter, void* act,
+                     spectra_stream_t stream);
+
+/* Greedy sampling of one decode step (the temperature-0 branch of the reference's
+ * sample_token, engine.py:1690-1697):
+ * *token = index of the largest of n fp16 logits (16-byte aligned; lowest index among equal
+ * maxima, NaN counts as largest, as torch.argmax).  When pos != NULL: history[*pos + 1] =
+ * *token (if inside [0, hist_len) and history != NULL), then *pos += 1. */
+int spectra_greedy_next(const void* logits, int64_t n, int64_t* token, int64_t* history, int64_t hist_len,
+                        int64_t* pos, spectra_stream_t stream);
 
 #ifdef __cplusplus
 }

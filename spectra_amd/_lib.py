@@ -61,6 +61,16 @@ SIGNATURES = {
     "spectra_outlier_columns_workspace": (c_size_t, [c_int64]),
     "spectra_outlier_columns": (c_int32, [c_void_p, c_int64, c_int32, c_int64, c_int64, c_void_p, ctypes.c_double,
                                           c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "spectra_rmsnorm": (c_int32, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_int64, c_int64, c_void_p,
+                                  c_void_p]),
+    "spectra_rope_append": (c_int32, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_int32, c_int32,
+                                      c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "spectra_attend_spans": (c_int32, [c_int32]),
+    "spectra_attend_workspace": (c_size_t, [c_int32, c_int32, c_int32]),
+    "spectra_attend_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                        c_void_p, c_size_t, c_void_p, c_void_p]),
+    "spectra_silu_mul": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
+    "spectra_greedy_next": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

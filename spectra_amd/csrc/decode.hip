@@ -1,0 +1,515 @@
+// Fused kernels of a Llama-shaped layer between its quantized linears.  The reference
+// fuses the same non-linear submodules (RMSNorm, SiLU, RoPE) with Inductor
+// (engine.py:1240-1250) and keeps keys/values in a static cache for graph replay
+// (engine.py:1387-1415).  Here each is one HIP kernel:
+//
+//   rmsnorm_kernel      h (+)= r (the add rounds to fp16), x = fp16(h * rsqrt(mean h^2 + eps) * w)
+//   rope_append_kernel  rotates q and k of T tokens (pairs (i, i + d/2), fp32), writes the
+//                       rotated q and appends k and v to the caches [kv][L][d] at the tokens'
+//                       positions
+//   attend_kernel       batch-1 decode attention split over the sequence: one workgroup per
+//                       (KV head, span of <= 64 positions) scores the g = heads / kv_heads
+//                       query heads of the group, and keeps per head the span's max score,
+//                       sum of exponentials and exponential-weighted V sum (fp32)
+//   combine_kernel      merges the spans of every head (log-sum-exp) into fp16
+//   silu_mul_kernel     act = fp16(silu(g) * u) on the fused gate_up output
+//   greedy_kernel       greedy sampling: token = argmax(logits), appended to the history at
+//                       pos + 1, pos advanced (the decode step's whole sampling tail)
+//
+// The position of the decoded token is read from device memory, so a decode step has no
+// host-side value and is captured once as a HIP graph.
+#include <cmath>
+
+#include "common.h"
+
+namespace spectra {
+
+constexpr int kDecThreads = 256;
+constexpr int kSpanMax = 64;  // positions per attention workgroup (one per lane of wave 0)
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// One workgroup per row.  Rows of hidden % 8 == 0 (<= 8192) are read as 16-byte chunks, all
+// issued before the first use (every chunk of the row is in flight at once); other rows take
+// the element loop.
+template <bool VEC>
+__global__ void __launch_bounds__(kDecThreads) rmsnorm_kernel(uint16_t* __restrict__ h, const uint16_t* __restrict__ r,
+                                                               const float* __restrict__ w, float eps, int hidden,
+                                                               uint16_t* __restrict__ x) {
+  __shared__ float red[kDecThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  uint16_t* hr = h + row * hidden;
+  float ss = 0.0f;
+  if constexpr (VEC) {
+    constexpr int C = 4;  // chunks of 8 per thread: hidden <= 8192
+    const int nch = hidden >> 3;
+    uint4 hv[C], rv[C];
+    float4 w0[C], w1[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int ch = tid + c * kDecThreads;
+      if (ch < nch) {
+        hv[c] = ((const uint4*)hr)[ch];
+        if (r != nullptr) rv[c] = ((const uint4*)(r + row * hidden))[ch];
+        w0[c] = ((const float4*)w)[2 * ch];
+        w1[c] = ((const float4*)w)[2 * ch + 1];
+      }
+    }
+    float v[C][8];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int ch = tid + c * kDecThreads;
+      if (ch < nch) {
+        const uint32_t hw[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+        const uint32_t rw[4] = {rv[c].x, rv[c].y, rv[c].z, rv[c].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float t = h2f((uint16_t)(hw[e >> 1] >> (16 * (e & 1))));
+          if (r != nullptr) t = h2f(f2h(t + h2f((uint16_t)(rw[e >> 1] >> (16 * (e & 1))))));
+          v[c][e] = t;
+          ss += t * t;
+        }
+        if (r != nullptr) {
+          uint32_t o[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = (uint32_t)f2h(v[c][2 * e]) | ((uint32_t)f2h(v[c][2 * e + 1]) << 16);
+          ((uint4*)hr)[ch] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)hidden + eps);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int ch = tid + c * kDecThreads;
+      if (ch < nch) {
+        const float wv[8] = {w0[c].x, w0[c].y, w0[c].z, w0[c].w, w1[c].x, w1[c].y, w1[c].z, w1[c].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          o[e] = (uint32_t)f2h(v[c][2 * e] * inv * wv[2 * e]) | ((uint32_t)f2h(v[c][2 * e + 1] * inv * wv[2 * e + 1]) << 16);
+        ((uint4*)(x + row * hidden))[ch] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  } else {
+    for (int i = tid; i < hidden; i += kDecThreads) {
+      float v = h2f(hr[i]);
+      if (r != nullptr) {
+        v = h2f(f2h(v + h2f(r[row * hidden + i])));
+        hr[i] = f2h(v);
+      }
+      ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)hidden + eps);
+    for (int i = tid; i < hidden; i += kDecThreads) x[row * hidden + i] = f2h(h2f(hr[i]) * inv * w[i]);
+  }
+}
+
+// grid (heads + kv_heads, T), blockDim head_dim / 2.  Block b < heads rotates query head b;
+// b >= heads rotates key head b - heads and appends it and the matching value head to the
+// caches ([kv][L][d] both).
+__global__ void rope_append_kernel(const uint16_t* __restrict__ qkv, int64_t ldqkv, const int64_t* __restrict__ pos_p,
+                                   const float* __restrict__ cos_t, const float* __restrict__ sin_t, int heads,
+                                   int kv_heads, int hd, int lmax, uint16_t* __restrict__ q_rot,
+                                   uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache) {
+  const int b = blockIdx.x, t = blockIdx.y, i = threadIdx.x, h2 = hd >> 1;
+  const int64_t pos = pos_p[t];
+  if (pos < 0 || pos >= lmax) return;  // outside the cache: nothing is written
+  const float c = cos_t[pos * h2 + i], s = sin_t[pos * h2 + i];
+  const uint16_t* row = qkv + t * ldqkv;
+  const uint16_t* src = row + (int64_t)b * hd;  // q heads, then k heads, then v heads
+  const float a = h2f(src[i]), bb = h2f(src[i + h2]);
+  const uint16_t lo = f2h(a * c - bb * s), hi = f2h(bb * c + a * s);
+  if (b < heads) {
+    uint16_t* q = q_rot + ((int64_t)t * heads + b) * hd;
+    q[i] = lo;
+    q[i + h2] = hi;
+  } else {
+    const int kh = b - heads;
+    uint16_t* kc = k_cache + ((int64_t)kh * lmax + pos) * hd;
+    kc[i] = lo;
+    kc[i + h2] = hi;
+    const uint16_t* vs = row + (int64_t)(heads + kv_heads + kh) * hd;
+    uint16_t* vc = v_cache + ((int64_t)kh * lmax + pos) * hd;
+    vc[i] = vs[i];
+    vc[i + h2] = vs[i + h2];
+  }
+}
+
+// Sum over groups of W consecutive lanes (W a power of two <= 64): every lane of a group
+// ends with the group's total.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = 1; off < W; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = h2f((uint16_t)w[e]);
+    f[2 * e + 1] = h2f((uint16_t)(w[e] >> 16));
+  }
+}
+
+// grid (kv_heads, nspan), 256 threads; span sp covers positions [64 sp, 64 sp + 64) of [0, pos].
+// Thread = (dg: 8 consecutive head dims, pr: position row); pass i covers positions
+// pr + i * PPW.  Every K and V chunk of the span is loaded up front (16 bytes each).
+// part: [heads][nspan][hd + 2] fp32 = exponential-weighted V sum, max score, sum of exponentials.
+template <int G, int HD>
+__global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __restrict__ q_rot,
+                                                              const uint16_t* __restrict__ k_cache,
+                                                              const uint16_t* __restrict__ v_cache,
+                                                              const int64_t* __restrict__ pos_p, int lmax,
+                                                              float scale, float* __restrict__ part) {
+  constexpr int DG = HD / 8;               // lanes per position
+  constexpr int PPW = kDecThreads / DG;    // positions per pass
+  constexpr int NP = kSpanMax / PPW;       // passes
+  __shared__ float sc[G][kSpanMax];        // scores, then exponentials
+  __shared__ float wsum[4][G][HD];         // V sums of the four waves
+  const int kh = blockIdx.x, sp = blockIdx.y, nspan = gridDim.y, tid = threadIdx.x;
+  const int64_t pos = min(*pos_p, (int64_t)lmax - 1);
+  const int t0 = sp * kSpanMax;
+  const int n = (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform; <= 0 past the position
+  float* pbase = part + ((int64_t)kh * G * nspan + sp) * (HD + 2);  // head j: + j * nspan * (HD + 2)
+  if (n <= 0) {
+    if (tid < G) {
+      pbase[(int64_t)tid * nspan * (HD + 2) + HD] = -INFINITY;
+      pbase[(int64_t)tid * nspan * (HD + 2) + HD + 1] = 0.0f;
+    }
+    return;
+  }
+  const int dg = tid % DG, pr = tid / DG;
+  const uint16_t* kc = k_cache + ((int64_t)kh * lmax + t0) * HD + dg * 8;
+  const uint16_t* vc = v_cache + ((int64_t)kh * lmax + t0) * HD + dg * 8;
+  uint4 kr[NP], vr[NP], qr[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) qr[j] = *(const uint4*)(q_rot + (int64_t)(kh * G + j) * HD + dg * 8);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int tl = pr + i * PPW;
+    const int tc = tl < n ? tl : 0;  // positions past the end re-read the first (in bounds)
+    kr[i] = *(const uint4*)(kc + (int64_t)tc * HD);
+  }
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int tl = pr + i * PPW;
+    const int tc = tl < n ? tl : 0;
+    vr[i] = *(const uint4*)(vc + (int64_t)tc * HD);
+  }
+  // scores
+  float qf[G][8];
+#pragma unroll
+  for (int j = 0; j < G; ++j) unpack8(qr[j], qf[j]);
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    float kf[8];
+    unpack8(kr[i], kf);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      float d = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d += qf[j][e] * kf[e];
+      d = group_sum<DG>(d);
+      if (dg == 0) sc[j][pr + i * PPW] = d * scale;
+    }
+  }
+  __syncthreads();
+  if (tid < 64) {  // wave 0: lane = position of the span
+    float* pj0 = pbase;
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const float s = tid < n ? sc[j][tid] : -INFINITY;
+      const float m = wave_max(s);  // finite: n >= 1
+      const float e = tid < n ? __expf(s - m) : 0.0f;
+      sc[j][tid] = e;
+      const float l = wave_sum(e);
+      if (tid == 0) {
+        pj0[(int64_t)j * nspan * (HD + 2) + HD] = m;
+        pj0[(int64_t)j * nspan * (HD + 2) + HD + 1] = l;
+      }
+    }
+  }
+  __syncthreads();
+  // exponential-weighted V sums: per thread G x 8 partials over its passes, then across the
+  // position rows of the wave (lanes DG apart) and across the four waves
+  float acc[G][8];
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    float vf[8];
+    unpack8(vr[i], vf);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const float pw = sc[j][pr + i * PPW];  // 0 past the end
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] += pw * vf[e];
+    }
+  }
+  const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+  for (int j = 0; j < G; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = acc[j][e];
+#pragma unroll
+      for (int off = DG; off < 64; off <<= 1) a += __shfl_xor(a, off, 64);
+      acc[j][e] = a;
+    }
+  if (lane < DG) {
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wsum[wave][j][lane * 8 + e] = acc[j][e];
+  }
+  __syncthreads();
+  for (int o = tid; o < G * HD; o += kDecThreads) {
+    const int j = o / HD, d = o - j * HD;
+    pbase[(int64_t)j * nspan * (HD + 2) + d] = (wsum[0][j][d] + wsum[1][j][d]) + (wsum[2][j][d] + wsum[3][j][d]);
+  }
+}
+
+// grid heads, blockDim hd: out[h][d] = sum_s acc_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M).
+// The spans are read in groups of 8 with every load of a group in flight together.
+__global__ void combine_kernel(const float* __restrict__ part, int nspan, int hd, uint16_t* __restrict__ out) {
+  const int h = blockIdx.x, d = threadIdx.x;
+  const float* ph = part + (int64_t)h * nspan * (hd + 2);
+  float m = -INFINITY;
+  for (int s0 = 0; s0 < nspan; s0 += 8) {
+    float mv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mv[u] = s0 + u < nspan ? ph[(s0 + u) * (hd + 2) + hd] : -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) m = fmaxf(m, mv[u]);
+  }
+  float l = 0.0f, a = 0.0f;
+  for (int s0 = 0; s0 < nspan; s0 += 8) {
+    float mv[8], lv[8], av[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool ok = s0 + u < nspan;
+      const float* p = ph + (ok ? s0 + u : 0) * (hd + 2);
+      mv[u] = ok ? p[hd] : -INFINITY;
+      lv[u] = p[hd + 1];
+      av[u] = p[d];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (mv[u] == -INFINITY) continue;  // span past the position
+      const float f = __expf(mv[u] - m);
+      l += lv[u] * f;
+      a += av[u] * f;
+    }
+  }
+  out[h * hd + d] = f2h(a / l);
+}
+
+__global__ void __launch_bounds__(kDecThreads) silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t ldgu,
+                                                                int inter, int64_t total,
+                                                                uint16_t* __restrict__ act) {
+  const int64_t i = (int64_t)blockIdx.x * kDecThreads + threadIdx.x;
+  if (i >= total) return;
+  const int64_t r = i / inter, c = i - r * inter;
+  const float g = h2f(gu[r * ldgu + c]), u = h2f(gu[r * ldgu + inter + c]);
+  act[i] = f2h(g / (1.0f + __expf(-g)) * u);
+}
+
+// One workgroup of 1024 threads: token = index of the largest logit (lowest index among
+// equal maxima, NaN counts as largest, as torch.argmax); history[pos + 1] = token; pos += 1.
+constexpr int kArgThreads = 1024;
+__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+__global__ void __launch_bounds__(kArgThreads) greedy_kernel(const uint16_t* __restrict__ logits, int n,
+                                                              int64_t* __restrict__ token,
+                                                              int64_t* __restrict__ history, int64_t hist_len,
+                                                              int64_t* __restrict__ pos) {
+  __shared__ float bv[kArgThreads / 64];
+  __shared__ int bi[kArgThreads / 64];
+  const int tid = threadIdx.x;
+  float best = -INFINITY;
+  int besti = 0x7fffffff;
+  const int nch = n >> 3;
+  for (int c0 = 0; c0 < nch; c0 += 4 * kArgThreads) {  // 4 chunks of 8 in flight per thread
+    uint4 u[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ch = c0 + tid + q * kArgThreads;
+      u[q] = ((const uint4*)logits)[ch < nch ? ch : 0];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int ch = c0 + tid + q * kArgThreads;
+      if (ch < nch) {
+        float f[8];
+        unpack8(u[q], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (arg_better(f[e], 8 * ch + e, best, besti)) {
+            best = f[e];
+            besti = 8 * ch + e;
+          }
+      }
+    }
+  }
+  for (int i = (nch << 3) + tid; i < n; i += kArgThreads) {  // tail
+    const float f = h2f(logits[i]);
+    if (arg_better(f, i, best, besti)) {
+      best = f;
+      besti = i;
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(best, off, 64);
+    const int oi = __shfl_xor(besti, off, 64);
+    if (arg_better(ov, oi, best, besti)) {
+      best = ov;
+      besti = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    bv[tid >> 6] = best;
+    bi[tid >> 6] = besti;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < kArgThreads / 64; ++w)
+      if (arg_better(bv[w], bi[w], best, besti)) {
+        best = bv[w];
+        besti = bi[w];
+      }
+    *token = besti;
+    if (pos != nullptr) {
+      const int64_t p = *pos + 1;
+      if (history != nullptr && p >= 0 && p < hist_len) history[p] = besti;
+      *pos = p;
+    }
+  }
+}
+
+}  // namespace spectra
+
+using namespace spectra;
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+extern "C" int spectra_rmsnorm(void* h, const void* residual, const float* weight, float eps, int64_t rows,
+                               int64_t hidden, void* x, spectra_stream_t stream) {
+  SPECTRA_REQUIRE(h && weight && x, "NULL pointer");
+  SPECTRA_REQUIRE(rows >= 1 && rows < (int64_t(1) << 31) && hidden >= 1 && hidden < (1 << 24), "bad shape");
+  const bool vec = hidden % 8 == 0 && hidden <= 8 * 4 * kDecThreads && aligned16(h) && aligned16(x) &&
+                   aligned16(weight) && (residual == nullptr || aligned16(residual));
+  auto kern = vec ? rmsnorm_kernel<true> : rmsnorm_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)rows), dim3(kDecThreads), 0, (hipStream_t)stream, (uint16_t*)h,
+                     (const uint16_t*)residual, weight, eps, (int)hidden, (uint16_t*)x);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
+extern "C" int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t tokens, const int64_t* pos,
+                                   const float* cos_t, const float* sin_t, int32_t heads, int32_t kv_heads,
+                                   int32_t head_dim, int32_t max_seq, void* q_rot, void* k_cache, void* v_cache,
+                                   spectra_stream_t stream) {
+  SPECTRA_REQUIRE(qkv && pos && cos_t && sin_t && q_rot && k_cache && v_cache, "NULL pointer");
+  SPECTRA_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
+  SPECTRA_REQUIRE(head_dim >= 2 && head_dim <= 2048 && head_dim % 2 == 0, "head_dim must be even, <= 2048");
+  SPECTRA_REQUIRE(tokens >= 1 && tokens <= 65535 && max_seq >= 1, "bad token count");
+  SPECTRA_REQUIRE(ldqkv >= (int64_t)(heads + 2 * kv_heads) * head_dim, "qkv row stride too small");
+  hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(heads + kv_heads), (unsigned)tokens),
+                     dim3((unsigned)(head_dim / 2)), 0, (hipStream_t)stream, (const uint16_t*)qkv, ldqkv, pos, cos_t,
+                     sin_t, heads, kv_heads, head_dim, max_seq, (uint16_t*)q_rot, (uint16_t*)k_cache,
+                     (uint16_t*)v_cache);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
+extern "C" int32_t spectra_attend_spans(int32_t max_seq) { return (max_seq + kSpanMax - 1) / kSpanMax; }
+
+extern "C" size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq) {
+  return (size_t)heads * spectra_attend_spans(max_seq) * (head_dim + 2) * sizeof(float);
+}
+
+typedef void (*attend_fn)(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, int, float, float*);
+
+template <int HD>
+static attend_fn pick_attend(int g) {
+  switch (g) {
+    case 1: return attend_kernel<1, HD>;
+    case 2: return attend_kernel<2, HD>;
+    case 3: return attend_kernel<3, HD>;
+    case 4: return attend_kernel<4, HD>;
+    case 6: return attend_kernel<6, HD>;
+    case 8: return attend_kernel<8, HD>;
+    default: return nullptr;
+  }
+}
+
+extern "C" int spectra_attend_decode(const void* q_rot, const void* k_cache, const void* v_cache, const int64_t* pos,
+                                     int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq,
+                                     void* workspace, size_t workspace_bytes, void* out, spectra_stream_t stream) {
+  SPECTRA_REQUIRE(q_rot && k_cache && v_cache && pos && out, "NULL pointer");
+  SPECTRA_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
+  SPECTRA_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim must be 64, 128 or 256");
+  SPECTRA_REQUIRE(max_seq >= 1 && max_seq <= (1 << 20), "bad max_seq");
+  SPECTRA_REQUIRE(aligned16(q_rot) && aligned16(k_cache) && aligned16(v_cache), "q and the caches must be 16-byte aligned");
+  if (workspace == nullptr || workspace_bytes < spectra_attend_workspace(heads, head_dim, max_seq))
+    return fail(SPECTRA_ERR_WORKSPACE, "workspace missing or smaller than spectra_attend_workspace()");
+  const int g = heads / kv_heads;
+  const attend_fn fn = head_dim == 64 ? pick_attend<64>(g) : head_dim == 128 ? pick_attend<128>(g) : pick_attend<256>(g);
+  if (fn == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "decode attention serves 1, 2, 3, 4, 6 or 8 query heads per KV head");
+  const int nspan = spectra_attend_spans(max_seq);
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  const hipStream_t s = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  hipLaunchKernelGGL(fn, dim3((unsigned)kv_heads, (unsigned)nspan), dim3(kDecThreads), 0, s, (const uint16_t*)q_rot,
+                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, pos, max_seq, scale, part);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)heads), dim3((unsigned)head_dim), 0, s, part, nspan, head_dim,
+                     (uint16_t*)out);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
+extern "C" int spectra_silu_mul(const void* gate_up, int64_t ldgu, int64_t rows, int64_t inter, void* act,
+                                spectra_stream_t stream) {
+  SPECTRA_REQUIRE(gate_up && act, "NULL pointer");
+  SPECTRA_REQUIRE(rows >= 1 && inter >= 1 && inter < (int64_t(1) << 30) && ldgu >= 2 * inter, "bad shape");
+  const int64_t n = rows * inter;
+  SPECTRA_REQUIRE((n + kDecThreads - 1) / kDecThreads < (int64_t(1) << 31), "too many elements");
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + kDecThreads - 1) / kDecThreads)), dim3(kDecThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)gate_up, ldgu, (int)inter, n, (uint16_t*)act);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
+extern "C" int spectra_greedy_next(const void* logits, int64_t n, int64_t* token, int64_t* history, int64_t hist_len,
+                                   int64_t* pos, spectra_stream_t stream) {
+  SPECTRA_REQUIRE(logits && token, "NULL pointer");
+  SPECTRA_REQUIRE(n >= 1 && n < (int64_t(1) << 31), "bad logit count");
+  SPECTRA_REQUIRE(aligned16(logits), "logits must be 16-byte aligned");
+  SPECTRA_REQUIRE(history == nullptr || (pos != nullptr && hist_len >= 1), "history needs pos and a length");
+  hipLaunchKernelGGL(greedy_kernel, dim3(1), dim3(kArgThreads), 0, (hipStream_t)stream, (const uint16_t*)logits,
+                     (int)n, token, history, hist_len, pos);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}

@@ -26,6 +26,13 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   if (G < 1) G = 1;
   int rpw = (int)((want + G - 1) / G);
   const int rpw_max = mt == 4 ? 8 : kRpwMax;
+  if (rpw > rpw_max && mt == 1) {
+    // more rows than one resident workgroup per CU holds: size for two per CU (LDS <= 80 KB
+    // below; the one-row kernels stay within 128 VGPRs), so that one workgroup's set-up
+    // overlaps the other's stream
+    const int64_t want2 = (n + 511) / 512;
+    rpw = (int)((want2 + G - 1) / G);
+  }
   rpw = rpw < 1 ? 1 : (rpw > rpw_max ? rpw_max : rpw);
   const int R = G * rpw;
   const int BD = 64 * S * G;
@@ -56,6 +63,12 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   int ocap = outliers ? (csr ? 4 * BD - 3 : BD) : 0;
   const int fit = (int)((163840 - off) / (uint32_t)(mt * 4));
   if (ocap > fit) ocap = fit;
+  // grids beyond one workgroup per CU: keep two resident per CU when the staging still
+  // covers a useful share of the entries (the rest are read in the per-row phase)
+  if (pl->grid > 256 && mt == 1 && off < 81920) {
+    const int fit2 = (int)((81920 - off) / (uint32_t)(mt * 4));
+    if (fit2 >= 256 && ocap > fit2) ocap = fit2;
+  }
   pl->ocap = ocap;
   off = align16(off + (uint32_t)(ocap * mt * 4));
   pl->lds_bytes = off;

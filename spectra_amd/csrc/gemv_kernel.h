@@ -35,7 +35,7 @@ namespace spectra {
 
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kRpwMax = 12;  // rows per wave held in registers
+constexpr int kRpwMax = 11;  // rows per wave held in registers (<= 128 VGPRs: two 8-wave workgroups per CU)
 constexpr int kLutBytes = 65536;
 constexpr int kMaxWaves = 8;
 

@@ -15,7 +15,8 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .kernels import GEMV_MAX_M, QWeightOperands, w4_embedding, w4a16_linear
+from .kernels import (GEMV_MAX_M, QWeightOperands, attend_decode, attend_workspace_bytes, greedy_next, rmsnorm,
+                      rope_append, silu_mul, w4_embedding, w4a16_linear)
 
 __all__ = ["SpectraFusedLinear", "SpectraFusedEmbedding", "DecoderConfig", "SpectraDecoder"]
 
@@ -205,10 +206,12 @@ def _synthetic_nf4(n: int, k: int, gen: torch.Generator, had: int, ratio: float,
 class SpectraDecoder(nn.Module):
     """Batch-1 Llama-shaped decoder whose every linear is a Format B ``SpectraFusedLinear``
     (fused QKV and gate_up per layer, engine.py:409-437), with a tied quantized embedding /
-    lm_head (engine.py:1124-1168) and an fp16 KV cache.  Norms, RoPE, attention and the
-    sampling are torch ops.  A decode step is fully device-side (token, position and cache
-    index live in device tensors), so it is captured once as a HIP graph and replayed per
-    token (engine.py:1801-1860)."""
+    lm_head (engine.py:1124-1168) and an fp16 KV cache.  Between the linears a layer runs
+    the library's fused kernels (residual add + RMSNorm, RoPE + cache append, split-sequence
+    decode attention, SiLU-mul) where the reference relies on Inductor fusion
+    (engine.py:1240-1250); prefill attention over the prompt is a torch product.  A decode
+    step is fully device-side (token, position and cache index live in device tensors), so
+    it is captured once as a HIP graph and replayed per token (engine.py:1801-1860)."""
 
     def __init__(self, cfg: DecoderConfig = DecoderConfig(), device: Optional[torch.device] = None):
         super().__init__()
@@ -246,96 +249,83 @@ class SpectraDecoder(nn.Module):
         self.lm_head.set_weights(qe.packed, qe.absmax, None, outlier_idx=col, outlier_weight=val, marlin_layout=True,
                                  outlier_rowptr=qe.rowptr if col is not None else None)
         self.norm_w = [torch.ones(c.hidden, device=dev, dtype=torch.float32) for _ in range(2 * c.layers + 1)]
-        # KV cache: K stored transposed [kv, head_dim, max_seq] so the score product needs no copy
-        self.k_cache = torch.zeros(c.layers, c.kv_heads, hd, c.max_seq, device=dev, dtype=torch.float16)
+        # KV cache [layer, kv, max_seq, head_dim]: a position's head is one 16-byte-aligned run
+        self.k_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
         self.v_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
         inv = 1.0 / (c.rope_theta ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
         ang = torch.arange(c.max_seq, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)  # [max_seq, hd/2]
         self.arange = torch.arange(c.max_seq, device=dev)
+        self.attn_ws = torch.empty(attend_workspace_bytes(c.heads, hd, c.max_seq), device=dev, dtype=torch.uint8)
         # device-side decode state
         self.cur_id = torch.zeros(1, dtype=torch.int64, device=dev)
         self.cur_pos = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.history = torch.zeros(c.max_seq + 1, dtype=torch.int64, device=dev)  # token at each position
         self.graph: Optional[torch.cuda.CUDAGraph] = None
         self.graph_logits: Optional[torch.Tensor] = None
         self.device = dev
 
     # -- building blocks ---------------------------------------------------------------------
-    def _rms(self, x: torch.Tensor, i: int) -> torch.Tensor:
-        xf = x.float()
-        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.cfg.rms_eps) * self.norm_w[i]).half()
-
-    def _rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-        # x [T, h, hd]; rotate pairs (i, i + hd/2) (Llama rotate_half convention), fp32
-        h2 = x.shape[-1] // 2
-        xf = x.float()
-        a, b = xf[..., :h2], xf[..., h2:]
-        c, s = cos[:, None, :], sin[:, None, :]
-        return torch.cat([a * c - b * s, b * c + a * s], dim=-1).half()
-
-    def _layer(self, li: int, h: torch.Tensor, pos: torch.Tensor, causal_len: Optional[int]) -> torch.Tensor:
-        """One decoder layer for T tokens at positions ``pos`` (device int64 [T]).  Prefill:
-        causal_len = T (positions 0..T-1); decode: None (one token, masked over the cache)."""
+    def _layer(self, li: int, h: torch.Tensor, delta: Optional[torch.Tensor], pos: torch.Tensor,
+               causal_len: Optional[int]) -> torch.Tensor:
+        """One decoder layer for T tokens at positions ``pos`` (device int64 [T]).  ``h`` is the
+        residual stream, updated in place with the previous layer's output ``delta``; returns
+        this layer's MLP output (added by the next norm).  Prefill: causal_len = T (positions
+        0..T-1); decode: None (one token over the cache)."""
         c, blk = self.cfg, self.blocks[li]
         hd, T = c.head_dim, h.shape[0]
         g = c.heads // c.kv_heads
-        x = self._rms(h, 2 * li)
+        x = rmsnorm(h, self.norm_w[2 * li], c.rms_eps, residual=delta)
         qkv = blk["qkv"](x)
-        q = qkv[:, : c.hidden].reshape(T, c.heads, hd)
-        k = qkv[:, c.hidden: c.hidden + c.kv_heads * hd].reshape(T, c.kv_heads, hd)
-        v = qkv[:, c.hidden + c.kv_heads * hd:].reshape(T, c.kv_heads, hd)
-        cos, sin = self.cos.index_select(0, pos), self.sin.index_select(0, pos)
-        q, k = self._rope(q, cos, sin), self._rope(k, cos, sin)
-        self.k_cache[li].index_copy_(2, pos, k.permute(1, 2, 0).contiguous())
-        self.v_cache[li].index_copy_(1, pos, v.permute(1, 0, 2).contiguous())
-        qg = q.permute(1, 0, 2).reshape(c.kv_heads, g * T, hd).contiguous()  # head = kv * g + j
-        if causal_len is not None:
+        q = rope_append(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li])
+        if causal_len is None:
+            a = attend_decode(q.reshape(c.heads, hd), self.k_cache[li], self.v_cache[li], pos, self.attn_ws)
+            a = a.reshape(1, c.hidden)
+        else:
             L = causal_len
-            kt, vv = self.k_cache[li][:, :, :L].contiguous(), self.v_cache[li][:, :L, :].contiguous()
-        else:
-            kt, vv = self.k_cache[li], self.v_cache[li]
-        s = torch.matmul(qg, kt).float() * (1.0 / math.sqrt(hd))  # [kv, g*T, L]
-        if causal_len is not None:
+            qg = q.permute(1, 0, 2).reshape(c.kv_heads, g * T, hd).contiguous()  # head = kv * g + j
+            kt = self.k_cache[li][:, :L, :].transpose(1, 2).contiguous()  # [kv, hd, L]
+            vv = self.v_cache[li][:, :L, :].contiguous()
+            s = torch.matmul(qg, kt).float() * (1.0 / math.sqrt(hd))  # [kv, g*T, L]
             qpos = pos.repeat(g)  # row r = j * T + t -> position pos[t]
-            mask = self.arange[:L][None, :] > qpos[:, None]
-        else:
-            mask = (self.arange > pos[0])[None, :]
-        s = s.masked_fill(mask[None], float("-inf"))
-        p = torch.softmax(s, dim=-1).half()
-        a = torch.matmul(p, vv)  # [kv, g*T, hd]
-        a = a.reshape(c.heads, T, hd).permute(1, 0, 2).reshape(T, c.hidden)
-        h = h + blk["o"](a)
-        x = self._rms(h, 2 * li + 1)
-        gu = blk["gate_up"](x)
-        act = (torch.nn.functional.silu(gu[:, : c.inter].float()) * gu[:, c.inter:].float()).half()
-        return h + blk["down"](act)
+            s = s.masked_fill((self.arange[:L][None, :] > qpos[:, None])[None], float("-inf"))
+            a = torch.matmul(torch.softmax(s, dim=-1).half(), vv)  # [kv, g*T, hd]
+            a = a.reshape(c.heads, T, hd).permute(1, 0, 2).reshape(T, c.hidden)
+        o = blk["o"](a)
+        x = rmsnorm(h, self.norm_w[2 * li + 1], c.rms_eps, residual=o)
+        return blk["down"](silu_mul(blk["gate_up"](x)))
 
     def forward_tokens(self, ids: torch.Tensor, pos: torch.Tensor, causal_len: Optional[int]) -> torch.Tensor:
         h = self.embed(ids)
+        delta = None
         for li in range(self.cfg.layers):
-            h = self._layer(li, h, pos, causal_len)
-        return self.lm_head(self._rms(h[-1:], 2 * self.cfg.layers))  # logits of the last token [1, vocab]
+            delta = self._layer(li, h, delta, pos, causal_len)
+        x = rmsnorm(h[-1:], self.norm_w[2 * self.cfg.layers], self.cfg.rms_eps, residual=delta[-1:])
+        return self.lm_head(x)  # logits of the last token [1, vocab]
 
     # -- generation --------------------------------------------------------------------------
     @torch.no_grad()
     def prefill(self, prompt: torch.Tensor) -> torch.Tensor:
         T = prompt.numel()
-        pos = self.arange[:T]
-        logits = self.forward_tokens(prompt.reshape(-1).to(self.device), pos, T)
-        self.cur_id.copy_(torch.argmax(logits[0]).reshape(1))
-        self.cur_pos.fill_(T)
+        if T >= self.cfg.max_seq:
+            raise ValueError(f"prompt of {T} tokens does not fit max_seq={self.cfg.max_seq}")
+        ids = prompt.reshape(-1).to(self.device)
+        self.history[:T].copy_(ids)
+        self.cur_pos.fill_(T - 1)
+        logits = self.forward_tokens(ids, self.arange[:T], T)
+        greedy_next(logits[0], self.cur_id, self.history, self.cur_pos)  # history[T], cur_pos = T
         return logits
 
     def _decode_step(self) -> torch.Tensor:
         logits = self.forward_tokens(self.cur_id, self.cur_pos, None)
-        self.cur_id.copy_(torch.argmax(logits[0]).reshape(1))
-        self.cur_pos.add_(1)
+        greedy_next(logits[0], self.cur_id, self.history, self.cur_pos)
         return logits
 
     @torch.no_grad()
     def capture_decode(self) -> None:
-        """Capture one decode step (all linears, attention and the argmax) as a HIP graph."""
-        saved = (self.cur_id.clone(), self.cur_pos.clone(), self.k_cache.clone(), self.v_cache.clone())
+        """Capture one decode step (all linears, attention and the sampling) as a HIP graph."""
+        saved = (self.cur_id.clone(), self.cur_pos.clone(), self.history.clone(), self.k_cache.clone(),
+                 self.v_cache.clone())
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -349,19 +339,22 @@ class SpectraDecoder(nn.Module):
         # the capture does not execute: restore the state the warm-up changed
         self.cur_id.copy_(saved[0])
         self.cur_pos.copy_(saved[1])
-        self.k_cache.copy_(saved[2])
-        self.v_cache.copy_(saved[3])
+        self.history.copy_(saved[2])
+        self.k_cache.copy_(saved[3])
+        self.v_cache.copy_(saved[4])
 
     @torch.no_grad()
     def decode(self, steps: int, use_graph: bool = True) -> torch.Tensor:
-        """``steps`` greedy tokens after a prefill; returns them (device int64 [steps])."""
-        out = torch.empty(steps, dtype=torch.int64, device=self.device)
+        """``steps`` greedy decode steps after a prefill; returns the tokens they consumed (the
+        first is the prefill's prediction), a device int64 [steps] view of the history."""
+        p0 = int(self.cur_pos)  # one host read before the loop; the steps themselves never sync
+        if p0 + steps > self.cfg.max_seq:
+            raise ValueError(f"{steps} steps from position {p0} exceed max_seq={self.cfg.max_seq}")
         if use_graph and self.graph is None:
             self.capture_decode()
-        for i in range(steps):
-            out[i : i + 1].copy_(self.cur_id)
+        for _ in range(steps):
             if use_graph:
                 self.graph.replay()
             else:
                 self._decode_step()
-        return out
+        return self.history[p0: p0 + steps]

@@ -25,7 +25,8 @@ import torch
 from . import _lib as L
 
 __all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_dequant", "fwht_rows",
-           "QWeightOperands", "GEMV_MAX_M", "w4_embedding"]
+           "QWeightOperands", "GEMV_MAX_M", "w4_embedding", "rmsnorm", "rope_append", "attend_decode",
+           "attend_workspace_bytes", "silu_mul", "greedy_next"]
 
 GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
 
@@ -286,3 +287,130 @@ def fwht_rows(x: torch.Tensor, block: int, out_dtype: Optional[torch.dtype] = No
                                                         x2.shape[0], k, int(block), out.data_ptr(), out.stride(0),
                                                         _dtype_code(out, _DT.keys(), "out"), _stream(x.device)))
     return out.reshape(x.shape)
+
+
+# ---------------------------------------------------------------------------
+# decode-layer kernels between the linears (engine.py:1240-1250 fuses the same
+# submodules with Inductor; engine.py:1387-1415 keeps the static KV cache)
+# ---------------------------------------------------------------------------
+def _need_f16(t: torch.Tensor, name: str, contiguous: bool = True) -> None:
+    if not t.is_cuda or t.dtype != torch.float16:
+        raise ValueError(f"{name} must be an fp16 GPU tensor")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def rmsnorm(h: torch.Tensor, weight: torch.Tensor, eps: float, residual: Optional[torch.Tensor] = None,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``h`` += ``residual`` in place (fp16 rounding) when given, then returns
+    fp16(h * rsqrt(mean(h^2) + eps) * weight) over the last dimension."""
+    _need_f16(h, "h")
+    hidden = h.shape[-1]
+    if residual is not None:
+        _need_f16(residual, "residual")
+        if residual.shape != h.shape:
+            raise ValueError("residual must have h's shape")
+    if weight.dtype != torch.float32 or not weight.is_contiguous() or weight.numel() != hidden:
+        raise ValueError("weight must be contiguous fp32 [hidden]")
+    if out is None:
+        out = torch.empty_like(h)
+    _need_f16(out, "out")
+    lib = L.load()
+    L.check("spectra_rmsnorm", lib.spectra_rmsnorm(h.data_ptr(), residual.data_ptr() if residual is not None else None,
+                                                    weight.data_ptr(), float(eps), h.numel() // hidden, hidden,
+                                                    out.data_ptr(), _stream(h.device)))
+    return out
+
+
+def rope_append(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, heads: int,
+                kv_heads: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rotates the q/k heads of fused-QKV rows ``qkv`` [T, (heads + 2 kv_heads) * d] at
+    positions ``pos`` (int64 [T]), appends k and v to ``k_cache`` / ``v_cache`` [kv, L, d];
+    returns the rotated q [T, heads, d]."""
+    _need_f16(qkv, "qkv", contiguous=False)
+    _need_f16(k_cache, "k_cache")
+    _need_f16(v_cache, "v_cache")
+    kv, lmax, hd = k_cache.shape
+    if v_cache.shape != k_cache.shape or kv != kv_heads:
+        raise ValueError("k_cache and v_cache must be [kv_heads, L, d]")
+    qkv2, ld = _rows(qkv.reshape(-1, qkv.shape[-1]), "qkv")
+    T = qkv2.shape[0]
+    if pos.dtype != torch.int64 or not pos.is_contiguous() or pos.numel() != T:
+        raise ValueError("pos must be contiguous int64 [T]")
+    for t, name in ((cos, "cos"), (sin, "sin")):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.shape != (lmax, hd // 2):
+            raise ValueError(f"{name} must be contiguous fp32 [L, d/2]")
+    if q_out is None:
+        q_out = torch.empty((T, heads, hd), device=qkv.device, dtype=torch.float16)
+    _need_f16(q_out, "q_out")
+    lib = L.load()
+    L.check("spectra_rope_append", lib.spectra_rope_append(qkv2.data_ptr(), ld, T, pos.data_ptr(), cos.data_ptr(),
+                                                            sin.data_ptr(), heads, kv_heads, hd, lmax,
+                                                            q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                                            _stream(qkv.device)))
+    return q_out
+
+
+def attend_workspace_bytes(heads: int, head_dim: int, max_seq: int) -> int:
+    return int(L.load().spectra_attend_workspace(heads, head_dim, max_seq))
+
+
+def attend_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                  workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention of one query token ``q`` [heads, d] over positions [0, pos] of the caches
+    [kv, L, d] (``pos`` int64 [1] on the device); returns fp16 [heads, d]."""
+    _need_f16(q, "q")
+    _need_f16(k_cache, "k_cache")
+    _need_f16(v_cache, "v_cache")
+    kv, lmax, hd = k_cache.shape
+    heads = q.numel() // hd
+    if q.numel() != heads * hd or v_cache.shape != k_cache.shape:
+        raise ValueError("q must be [heads, d] and k_cache, v_cache [kv, L, d]")
+    if pos.dtype != torch.int64 or pos.numel() != 1:
+        raise ValueError("pos must be int64 [1]")
+    need = attend_workspace_bytes(heads, hd, lmax)
+    if workspace is None:
+        workspace = torch.empty(need, device=q.device, dtype=torch.uint8)
+    if out is None:
+        out = torch.empty((heads, hd), device=q.device, dtype=torch.float16)
+    _need_f16(out, "out")
+    lib = L.load()
+    L.check("spectra_attend_decode", lib.spectra_attend_decode(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                                                pos.data_ptr(), heads, kv, hd, lmax,
+                                                                workspace.data_ptr(),
+                                                                workspace.numel() * workspace.element_size(),
+                                                                out.data_ptr(), _stream(q.device)))
+    return out
+
+
+def silu_mul(gate_up: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """fp16(silu(g) * u) of fused gate_up rows [T, 2 I] -> [T, I]."""
+    _need_f16(gate_up, "gate_up", contiguous=False)
+    g2, ld = _rows(gate_up.reshape(-1, gate_up.shape[-1]), "gate_up")
+    inter = g2.shape[1] // 2
+    if out is None:
+        out = torch.empty((g2.shape[0], inter), device=gate_up.device, dtype=torch.float16)
+    _need_f16(out, "out")
+    lib = L.load()
+    L.check("spectra_silu_mul", lib.spectra_silu_mul(g2.data_ptr(), ld, g2.shape[0], inter, out.data_ptr(),
+                                                      _stream(gate_up.device)))
+    return out
+
+
+def greedy_next(logits: torch.Tensor, token: torch.Tensor, history: Optional[torch.Tensor] = None,
+                pos: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Temperature-0 sampling (engine.py:1690-1697): ``token`` (int64 [1]) = argmax of the fp16
+    ``logits`` (lowest index on ties, as torch.argmax); with ``pos`` (int64 [1]) also
+    ``history[pos + 1] = token`` and ``pos += 1``, all on the device."""
+    _need_f16(logits, "logits")
+    for t, name in ((token, "token"), (history, "history"), (pos, "pos")):
+        if t is not None and (t.dtype != torch.int64 or not t.is_cuda or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous int64 GPU tensor")
+    lib = L.load()
+    L.check("spectra_greedy_next", lib.spectra_greedy_next(logits.data_ptr(), logits.numel(), token.data_ptr(),
+                                                            history.data_ptr() if history is not None else None,
+                                                            history.numel() if history is not None else 0,
+                                                            pos.data_ptr() if pos is not None else None,
+                                                            _stream(logits.device)))
+    return token

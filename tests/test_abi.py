@@ -95,3 +95,24 @@ def test_entry_points_reject_bad_arguments():
                                         None) == L.ERR_INVALID
     assert "group_size=32" in lib.spectra_last_error().decode()
     assert lib.spectra_fwht_rows(0x1000, 96, L.F32, 2, 96, 96, 0x2000, 96, L.F32, None) == L.ERR_INVALID
+
+
+def test_decode_kernels_reject_bad_arguments():
+    lib = L.load()
+    p = ctypes.c_void_p(0x1000)
+    assert lib.spectra_rmsnorm(None, None, p, 1e-5, 1, 64, p, None) == L.ERR_INVALID
+    assert lib.spectra_rmsnorm(p, None, p, 1e-5, 0, 64, p, None) == L.ERR_INVALID
+    # heads must be a multiple of kv_heads; qkv rows must hold heads + 2 kv_heads heads
+    assert lib.spectra_rope_append(p, 1024, 1, p, p, p, 6, 4, 64, 128, p, p, p, None) == L.ERR_INVALID
+    assert lib.spectra_rope_append(p, 100, 1, p, p, p, 4, 2, 64, 128, p, p, p, None) == L.ERR_INVALID
+    assert "stride" in lib.spectra_last_error().decode()
+    # 64 spans of 64 positions for max_seq 4096; the partials are fp32 [heads][spans][d + 2]
+    assert lib.spectra_attend_spans(4096) == 64 and lib.spectra_attend_spans(4097) == 65
+    assert lib.spectra_attend_workspace(24, 128, 1000) == 24 * 16 * 130 * 4
+    assert lib.spectra_attend_decode(p, p, p, p, 24, 8, 128, 1024, None, 0, p, None) == L.ERR_WORKSPACE
+    assert lib.spectra_attend_decode(p, p, p, p, 24, 8, 32, 1024, p, 1 << 20, p, None) == L.ERR_INVALID
+    assert lib.spectra_attend_decode(p, p, p, p, 40, 8, 128, 1024, p, 1 << 24, p, None) == L.ERR_UNSUPPORTED
+    assert lib.spectra_attend_decode(p, p, p, p, 24, 8, 96, 1024, p, 1 << 24, p, None) == L.ERR_INVALID
+    assert lib.spectra_silu_mul(p, 100, 1, 64, p, None) == L.ERR_INVALID
+    assert lib.spectra_greedy_next(p, 0, p, None, 0, None, None) == L.ERR_INVALID
+    assert lib.spectra_greedy_next(p, 10, p, p, 10, None, None) == L.ERR_INVALID  # history needs pos

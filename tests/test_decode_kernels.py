@@ -1,0 +1,125 @@
+"""GPU tests of the decode-layer kernels between the quantized linears against fp32 torch
+restatements of the same math:
+
+* rmsnorm: residual add rounded to fp16 bit-exactly; the normalised row within fp16
+  rounding plus the difference of summation order (1 fp16 ulp, rel 2e-3);
+* rope_append: rotation bit-identical to the fp32 torch formula rounded to fp16 (the same
+  operations in the same order), cache rows written exactly at the given positions and
+  nowhere else;
+* greedy_next: the index torch.argmax returns (ties: the first), history and position
+  updated on the device;
+* attend_decode: within 2e-3 (times max|v|) of fp32 softmax attention over the cache
+  prefix, at positions on and around the 64-position span edges and at the last slot;
+* silu_mul: within rel 2e-3 of fp32 silu(g) * u.
+"""
+import math
+
+import pytest
+import torch
+
+from spectra_amd import kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+def case(**kw):
+    print("case:", ", ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 3072), (3, 100), (5, 4097)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_rmsnorm(hip, rows, hidden, with_res):
+    case(rows=rows, hidden=hidden, with_res=with_res)
+    g = torch.Generator(device="cuda").manual_seed(rows * hidden)
+    h = torch.randn(rows, hidden, device="cuda", generator=g).half()
+    r = torch.randn(rows, hidden, device="cuda", generator=g).half() if with_res else None
+    w = torch.rand(hidden, device="cuda", generator=g) + 0.5
+    h_ref = (h + r) if with_res else h.clone()  # fp16 add, one rounding
+    x = K.rmsnorm(h, w, 1e-5, residual=r)
+    assert torch.equal(h, h_ref)
+    hf = h_ref.float()
+    ref = hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-5) * w
+    torch.testing.assert_close(x.float(), ref, rtol=2e-3, atol=1e-3)
+
+
+def _rope_ref(x, cos, sin):
+    h2 = x.shape[-1] // 2
+    a, b = x[..., :h2].float(), x[..., h2:].float()
+    return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1).half()
+
+
+@pytest.mark.parametrize("heads,kv,hd,T", [(24, 8, 128, 1), (4, 2, 64, 9), (8, 8, 96, 3)])
+def test_rope_append(hip, heads, kv, hd, T):
+    case(heads=heads, kv=kv, hd=hd, T=T)
+    L = 200
+    g = torch.Generator(device="cuda").manual_seed(hd + T)
+    qkv = torch.randn(T, (heads + 2 * kv) * hd + 8, device="cuda", generator=g).half()[:, 8:]  # strided rows
+    pos = torch.randperm(L, device="cuda", generator=g)[:T].contiguous()
+    inv = 1.0 / (5e5 ** (torch.arange(0, hd, 2, device="cuda", dtype=torch.float32) / hd))
+    ang = torch.arange(L, device="cuda", dtype=torch.float32)[:, None] * inv[None, :]
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    kc = torch.full((kv, L, hd), 7.0, device="cuda", dtype=torch.float16)
+    vc = torch.full((kv, L, hd), 7.0, device="cuda", dtype=torch.float16)
+    q = K.rope_append(qkv, pos, cos, sin, heads, kv, kc, vc)
+    c, s = cos[pos][:, None, :], sin[pos][:, None, :]
+    q_ref = _rope_ref(qkv[:, : heads * hd].reshape(T, heads, hd), c, s)
+    k_ref = _rope_ref(qkv[:, heads * hd: (heads + kv) * hd].reshape(T, kv, hd), c, s)
+    v_ref = qkv[:, (heads + kv) * hd:].reshape(T, kv, hd)
+    assert torch.equal(q, q_ref)
+    assert torch.equal(kc[:, pos, :].permute(1, 0, 2), k_ref)
+    assert torch.equal(vc[:, pos, :].permute(1, 0, 2), v_ref)
+    keep = torch.ones(L, dtype=torch.bool, device="cuda")
+    keep[pos] = False
+    assert bool((kc[:, keep, :] == 7.0).all()) and bool((vc[:, keep, :] == 7.0).all())
+
+
+@pytest.mark.parametrize("heads,kv,hd,L", [(24, 8, 128, 768), (4, 4, 64, 1000), (8, 2, 256, 130), (6, 3, 64, 64),
+                                           (32, 4, 128, 300), (12, 2, 64, 200)])
+def test_attend_decode(hip, heads, kv, hd, L):
+    g = torch.Generator(device="cuda").manual_seed(heads * L)
+    kc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+    vc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+    q = (torch.randn(heads, hd, device="cuda", generator=g) * 2).half()
+    ws = torch.empty(K.attend_workspace_bytes(heads, hd, L), device="cuda", dtype=torch.uint8)
+    grp = heads // kv
+    for p in sorted({0, 1, 62, 63, 64, 65, L // 2, L - 2, L - 1}):
+        if p >= L:
+            continue
+        case(heads=heads, kv=kv, hd=hd, L=L, pos=p)
+        pos = torch.tensor([p], device="cuda", dtype=torch.int64)
+        out = K.attend_decode(q, kc, vc, pos, ws)
+        kk = kc[:, : p + 1, :].float().transpose(1, 2).repeat_interleave(grp, dim=0)  # [heads, hd, n]
+        vv = vc[:, : p + 1, :].float().repeat_interleave(grp, dim=0)  # [heads, n, hd]
+        sc = torch.matmul(q.float()[:, None, :], kk.contiguous())[:, 0, :] / math.sqrt(hd)
+        ref = torch.matmul(torch.softmax(sc, -1)[:, None, :], vv.contiguous())[:, 0, :]
+        err = (out.float() - ref).abs().max().item()
+        assert err <= 2e-3 * vc.abs().max().item(), (p, err)
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 8192), (7, 300)])
+def test_silu_mul(hip, rows, inter):
+    case(rows=rows, inter=inter)
+    gen = torch.Generator(device="cuda").manual_seed(inter)
+    gu = (torch.randn(rows, 2 * inter, device="cuda", generator=gen) * 3).half()
+    act = K.silu_mul(gu)
+    gf, uf = gu[:, :inter].float(), gu[:, inter:].float()
+    ref = gf * torch.sigmoid(gf) * uf
+    torch.testing.assert_close(act.float(), ref, rtol=2e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("n", [128256, 1000, 5, 8])
+def test_greedy_next(hip, n):
+    case(n=n)
+    gen = torch.Generator(device="cuda").manual_seed(n)
+    logits = torch.randn(n, device="cuda", generator=gen).half()
+    token = torch.zeros(1, dtype=torch.int64, device="cuda")
+    K.greedy_next(logits, token)
+    assert int(token) == int(torch.argmax(logits))
+    # equal maxima: the first index, as torch.argmax
+    logits[n // 3] = 100.0
+    logits[n - 1] = 100.0
+    hist = torch.full((10,), -1, dtype=torch.int64, device="cuda")
+    pos = torch.tensor([3], dtype=torch.int64, device="cuda")
+    K.greedy_next(logits, token, hist, pos)
+    assert int(token) == n // 3 == int(torch.argmax(logits))
+    assert int(pos) == 4 and int(hist[4]) == n // 3 and int((hist == -1).sum()) == 9
