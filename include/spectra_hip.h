@@ -208,17 +208,21 @@ int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t tokens, const in
                         const float* sin_t, int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq,
                         void* q_rot, void* k_cache, void* v_cache, spectra_stream_t stream);
 
-/* Batch-1 decode attention of q_rot [heads, head_dim] over cache positions [0, *pos] of
- * k_cache / v_cache [kv_heads, max_seq, head_dim] (grouped-query: query head h reads KV head
- * h / (heads / kv_heads); 1, 2, 3, 4, 6 or 8 query heads per KV head; head_dim 64, 128 or
- * 256; 16-byte aligned), scale 1/sqrt(head_dim), fp32 softmax, fp16 out [heads, head_dim].
- * The sequence is split into spectra_attend_spans(max_seq) spans of 64 positions merged by
- * log-sum-exp; workspace >= spectra_attend_workspace(heads, head_dim, max_seq) bytes. */
+/* Batch-1 decode attention on the fused-QKV row of the decoded token (qkv: heads q heads,
+ * kv_heads k heads, kv_heads v heads of head_dim fp16 each) at position *pos (device int64):
+ * rotates q and the new k (as spectra_rope_append; cos_t / sin_t NULL = no rotation),
+ * appends k and v at *pos to k_cache / v_cache [kv_heads, max_seq, head_dim], and writes
+ * out [heads, head_dim] fp16 = softmax(q k^T / sqrt(head_dim)) v over positions [0, *pos]
+ * (fp32 softmax; grouped-query: query head h reads KV head h / (heads / kv_heads); 1, 2, 3,
+ * 4, 6 or 8 query heads per KV head; head_dim 64, 128 or 256; operands 16-byte aligned).
+ * Two kernels: spectra_attend_spans(max_seq) spans of 64 positions per KV head, then a
+ * log-sum-exp merge.  workspace: >= spectra_attend_workspace(heads, head_dim, max_seq)
+ * bytes, 16-byte aligned (span partials); calls sharing a workspace must not overlap. */
 int32_t spectra_attend_spans(int32_t max_seq);
 size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq);
-int spectra_attend_decode(const void* q_rot, const void* k_cache, const void* v_cache, const int64_t* pos,
-                          int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq, void* workspace,
-                          size_t workspace_bytes, void* out, spectra_stream_t stream);
+int spectra_attend_decode(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t, int32_t heads,
+                          int32_t kv_heads, int32_t head_dim, int32_t max_seq, void* k_cache, void* v_cache,
+                          void* workspace, size_t workspace_bytes, void* out, spectra_stream_t stream);
 
 /* act [rows, inter] = fp16(silu(g) * u) where g = gate_up[:, :inter], u = gate_up[:, inter:]
  * (row stride ldgu >= 2 * inter). */

@@ -68,7 +68,7 @@ SIGNATURES = {
     "spectra_attend_spans": (c_int32, [c_int32]),
     "spectra_attend_workspace": (c_size_t, [c_int32, c_int32, c_int32]),
     "spectra_attend_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
-                                        c_void_p, c_size_t, c_void_p, c_void_p]),
+                                        c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spectra_silu_mul": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "spectra_greedy_next": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
 }

@@ -7,10 +7,10 @@
 //   rope_append_kernel  rotates q and k of T tokens (pairs (i, i + d/2), fp32), writes the
 //                       rotated q and appends k and v to the caches [kv][L][d] at the tokens'
 //                       positions
-//   attend_kernel       batch-1 decode attention split over the sequence: one workgroup per
-//                       (KV head, span of <= 64 positions) scores the g = heads / kv_heads
-//                       query heads of the group, and keeps per head the span's max score,
-//                       sum of exponentials and exponential-weighted V sum (fp32)
+//   attend_kernel       batch-1 decode attention on the fused-QKV row: rotates q and the new
+//                       k, appends k and v to the caches, and attends over [0, pos] split
+//                       into spans of 64 positions (one workgroup per KV head and span,
+//                       fp32 softmax pieces)
 //   combine_kernel      merges the spans of every head (log-sum-exp) into fp16
 //   silu_mul_kernel     act = fp16(silu(g) * u) on the fused gate_up output
 //   greedy_kernel       greedy sampling: token = argmax(logits), appended to the history at
@@ -167,27 +167,62 @@ __device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
   }
 }
 
-// grid (kv_heads, nspan), 256 threads; span sp covers positions [64 sp, 64 sp + 64) of [0, pos].
-// Thread = (dg: 8 consecutive head dims, pr: position row); pass i covers positions
-// pr + i * PPW.  Every K and V chunk of the span is loaded up front (16 bytes each).
-// part: [heads][nspan][hd + 2] fp32 = exponential-weighted V sum, max score, sum of exponentials.
-template <int G, int HD>
-__global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __restrict__ q_rot,
-                                                              const uint16_t* __restrict__ k_cache,
-                                                              const uint16_t* __restrict__ v_cache,
-                                                              const int64_t* __restrict__ pos_p, int lmax,
-                                                              float scale, float* __restrict__ part) {
+// Rotation of the 8-dim chunk `own` of a head whose partner chunk (dims -+ head_dim/2) is
+// `partner`, with the cos/sin of the chunk's pair indices: the lower half takes
+// a*c - b*s, the upper half b*c + a*s (a = dim i, b = dim i + head_dim/2), each product and
+// the sum rounded in fp32 as written, the result to fp16 -- the rope_append arithmetic.
+__device__ __forceinline__ uint4 rope_chunk(const uint4& own, const uint4& partner, const float (&c)[8],
+                                            const float (&s)[8], bool upper) {
+  float x[8], y[8];
+  unpack8(own, x);
+  unpack8(partner, y);
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float r[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = 2 * e + h;
+      r[h] = upper ? x[i] * c[i] + y[i] * s[i] : x[i] * c[i] - y[i] * s[i];
+    }
+    o[e] = (uint32_t)f2h(r[0]) | ((uint32_t)f2h(r[1]) << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// grid (kv_heads, nspan), 256 threads.  Span sp covers positions [64 sp, 64 sp + 64) of
+// [0, pos]; spans past the position only mark themselves empty.  Each workgroup:
+//   * rotates the query heads of its group from the fused-QKV row (ROPE) -- every
+//     workgroup of the group computes the same values -- and, when its span holds pos,
+//     rotates the new key, appends key and value to the caches and uses them from registers;
+//   * thread = (dg: 8 consecutive head dims, pr: position row), pass i = positions
+//     pr + i * PPW; every K and V chunk of the span is loaded up front (16 bytes each);
+//   * writes its span's max score, sum of exponentials and exponential-weighted V sums
+//     to part [heads][nspan][hd + 2] (fp32), which combine_kernel merges.  (Merging in the
+//     last workgroup to finish needs device-scope fences, which write back the L2 of
+//     every XCD and cost more than the second launch.)
+template <int G, int HD, bool ROPE>
+__global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __restrict__ qkv,
+                                                              const int64_t* __restrict__ pos_p,
+                                                              const float* __restrict__ cos_t,
+                                                              const float* __restrict__ sin_t, int heads,
+                                                              int kv_heads, int lmax, float scale,
+                                                              uint16_t* __restrict__ k_cache,
+                                                              uint16_t* __restrict__ v_cache,
+                                                              float* __restrict__ part) {
   constexpr int DG = HD / 8;               // lanes per position
   constexpr int PPW = kDecThreads / DG;    // positions per pass
   constexpr int NP = kSpanMax / PPW;       // passes
+  constexpr int H2 = HD / 2;
   __shared__ float sc[G][kSpanMax];        // scores, then exponentials
   __shared__ float wsum[4][G][HD];         // V sums of the four waves
   const int kh = blockIdx.x, sp = blockIdx.y, nspan = gridDim.y, tid = threadIdx.x;
-  const int64_t pos = min(*pos_p, (int64_t)lmax - 1);
+  int64_t pos = *pos_p;
+  pos = pos < 0 ? 0 : (pos >= lmax ? lmax - 1 : pos);
   const int t0 = sp * kSpanMax;
-  const int n = (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform; <= 0 past the position
+  const int n = (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform
   float* pbase = part + ((int64_t)kh * G * nspan + sp) * (HD + 2);  // head j: + j * nspan * (HD + 2)
-  if (n <= 0) {
+  if (n <= 0) {  // span past the position: an empty piece for the merge
     if (tid < G) {
       pbase[(int64_t)tid * nspan * (HD + 2) + HD] = -INFINITY;
       pbase[(int64_t)tid * nspan * (HD + 2) + HD + 1] = 0.0f;
@@ -195,27 +230,66 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
     return;
   }
   const int dg = tid % DG, pr = tid / DG;
+  const bool upper = dg * 8 >= H2;
+  const int pdg = upper ? dg - H2 / 8 : dg + H2 / 8;  // partner chunk
+  const int tnew = (int)(pos - t0);                   // < 64 when this span holds pos
+  const bool mine = tnew < kSpanMax;
+  const int64_t ldh = (int64_t)HD;
+  // ---- loads: the group's query chunks, the new key / value, cos / sin, the span's cache
+  const uint16_t* qrow = qkv + (int64_t)kh * G * ldh;
+  const uint16_t* krow = qkv + (int64_t)(heads + kh) * ldh;
+  const uint16_t* vrow = qkv + (int64_t)(heads + kv_heads + kh) * ldh;
+  uint4 qo[G], qp[G], ko = make_uint4(0, 0, 0, 0), kp = ko, vo = ko;
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    qo[j] = *(const uint4*)(qrow + j * ldh + dg * 8);
+    if (ROPE) qp[j] = *(const uint4*)(qrow + j * ldh + pdg * 8);
+  }
+  if (mine) {
+    ko = *(const uint4*)(krow + dg * 8);
+    if (ROPE) kp = *(const uint4*)(krow + pdg * 8);
+    vo = *(const uint4*)(vrow + dg * 8);
+  }
+  float cs[8], sn[8];
+  if (ROPE) {
+    const int i0 = (upper ? dg * 8 - H2 : dg * 8);
+    const float4* cp = (const float4*)(cos_t + pos * H2 + i0);
+    const float4* spp = (const float4*)(sin_t + pos * H2 + i0);
+    const float4 c0 = cp[0], c1 = cp[1], s0 = spp[0], s1 = spp[1];
+    cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w; cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
+    sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+  }
   const uint16_t* kc = k_cache + ((int64_t)kh * lmax + t0) * HD + dg * 8;
   const uint16_t* vc = v_cache + ((int64_t)kh * lmax + t0) * HD + dg * 8;
-  uint4 kr[NP], vr[NP], qr[G];
-#pragma unroll
-  for (int j = 0; j < G; ++j) qr[j] = *(const uint4*)(q_rot + (int64_t)(kh * G + j) * HD + dg * 8);
+  uint4 kr[NP], vr[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int tl = pr + i * PPW;
-    const int tc = tl < n ? tl : 0;  // positions past the end re-read the first (in bounds)
-    kr[i] = *(const uint4*)(kc + (int64_t)tc * HD);
+    kr[i] = *(const uint4*)(kc + (int64_t)(tl < n ? tl : 0) * HD);  // past the end: re-read (in bounds)
   }
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int tl = pr + i * PPW;
-    const int tc = tl < n ? tl : 0;
-    vr[i] = *(const uint4*)(vc + (int64_t)tc * HD);
+    vr[i] = *(const uint4*)(vc + (int64_t)(tl < n ? tl : 0) * HD);
   }
-  // scores
+  // ---- the new token: rotate, append, and take it from registers
+  if (mine) {
+    const uint4 knew = ROPE ? rope_chunk(ko, kp, cs, sn, upper) : ko;
+    if (pr == tnew % PPW) {
+      *(uint4*)(kc + (int64_t)tnew * HD) = knew;
+      *(uint4*)(vc + (int64_t)tnew * HD) = vo;
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+      if (pr + i * PPW == tnew) {
+        kr[i] = knew;
+        vr[i] = vo;
+      }
+  }
+  // ---- scores
   float qf[G][8];
 #pragma unroll
-  for (int j = 0; j < G; ++j) unpack8(qr[j], qf[j]);
+  for (int j = 0; j < G; ++j) unpack8(ROPE ? rope_chunk(qo[j], qp[j], cs, sn, upper) : qo[j], qf[j]);
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     float kf[8];
@@ -231,7 +305,6 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
   }
   __syncthreads();
   if (tid < 64) {  // wave 0: lane = position of the span
-    float* pj0 = pbase;
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       const float s = tid < n ? sc[j][tid] : -INFINITY;
@@ -240,14 +313,14 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
       sc[j][tid] = e;
       const float l = wave_sum(e);
       if (tid == 0) {
-        pj0[(int64_t)j * nspan * (HD + 2) + HD] = m;
-        pj0[(int64_t)j * nspan * (HD + 2) + HD + 1] = l;
+        pbase[(int64_t)j * nspan * (HD + 2) + HD] = m;
+        pbase[(int64_t)j * nspan * (HD + 2) + HD + 1] = l;
       }
     }
   }
   __syncthreads();
-  // exponential-weighted V sums: per thread G x 8 partials over its passes, then across the
-  // position rows of the wave (lanes DG apart) and across the four waves
+  // ---- exponential-weighted V sums: G x 8 partials per thread, then across the position
+  // rows of the wave (lanes DG apart) and across the four waves
   float acc[G][8];
 #pragma unroll
   for (int j = 0; j < G; ++j)
@@ -287,37 +360,38 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
   }
 }
 
-// grid heads, blockDim hd: out[h][d] = sum_s acc_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M).
-// The spans are read in groups of 8 with every load of a group in flight together.
+// grid heads, blockDim hd: out[h][d] = sum_s acc_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M)
+// over the spans of head h (empty spans carry m = -inf); 16 spans' loads in flight at once.
 __global__ void combine_kernel(const float* __restrict__ part, int nspan, int hd, uint16_t* __restrict__ out) {
+  constexpr int B = 16;
   const int h = blockIdx.x, d = threadIdx.x;
   const float* ph = part + (int64_t)h * nspan * (hd + 2);
-  float m = -INFINITY;
-  for (int s0 = 0; s0 < nspan; s0 += 8) {
-    float mv[8];
+  float m = -INFINITY, l = 0.0f, a = 0.0f;
+  for (int s0 = 0; s0 < nspan; s0 += B) {
+    float mv[B], lv[B], av[B];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) mv[u] = s0 + u < nspan ? ph[(s0 + u) * (hd + 2) + hd] : -INFINITY;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) m = fmaxf(m, mv[u]);
-  }
-  float l = 0.0f, a = 0.0f;
-  for (int s0 = 0; s0 < nspan; s0 += 8) {
-    float mv[8], lv[8], av[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < B; ++u) {
       const bool ok = s0 + u < nspan;
-      const float* p = ph + (ok ? s0 + u : 0) * (hd + 2);
+      const float* p = ph + (int64_t)(ok ? s0 + u : 0) * (hd + 2);
       mv[u] = ok ? p[hd] : -INFINITY;
       lv[u] = p[hd + 1];
       av[u] = p[d];
     }
+    float mb = m;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (mv[u] == -INFINITY) continue;  // span past the position
-      const float f = __expf(mv[u] - m);
+    for (int u = 0; u < B; ++u) mb = fmaxf(mb, mv[u]);
+    if (mb == -INFINITY) continue;  // nothing yet
+    const float r = __expf(m - mb);  // rescale what came before (0 when m = -inf)
+    l *= r;
+    a *= r;
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+      if (mv[u] == -INFINITY) continue;  // empty span: its V sums were never written
+      const float f = __expf(mv[u] - mb);
       l += lv[u] * f;
       a += av[u] * f;
     }
+    m = mb;
   }
   out[h * hd + d] = f2h(a / l);
 }
@@ -446,43 +520,55 @@ extern "C" int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t token
 extern "C" int32_t spectra_attend_spans(int32_t max_seq) { return (max_seq + kSpanMax - 1) / kSpanMax; }
 
 extern "C" size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq) {
+  if (heads < 1 || head_dim < 1 || max_seq < 1) return 0;
   return (size_t)heads * spectra_attend_spans(max_seq) * (head_dim + 2) * sizeof(float);
 }
 
-typedef void (*attend_fn)(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, int, float, float*);
+typedef void (*attend_fn)(const uint16_t*, const int64_t*, const float*, const float*, int, int, int, float, uint16_t*,
+                          uint16_t*, float*);
 
-template <int HD>
+template <int HD, bool ROPE>
 static attend_fn pick_attend(int g) {
   switch (g) {
-    case 1: return attend_kernel<1, HD>;
-    case 2: return attend_kernel<2, HD>;
-    case 3: return attend_kernel<3, HD>;
-    case 4: return attend_kernel<4, HD>;
-    case 6: return attend_kernel<6, HD>;
-    case 8: return attend_kernel<8, HD>;
+    case 1: return attend_kernel<1, HD, ROPE>;
+    case 2: return attend_kernel<2, HD, ROPE>;
+    case 3: return attend_kernel<3, HD, ROPE>;
+    case 4: return attend_kernel<4, HD, ROPE>;
+    case 6: return attend_kernel<6, HD, ROPE>;
+    case 8: return attend_kernel<8, HD, ROPE>;
     default: return nullptr;
   }
 }
 
-extern "C" int spectra_attend_decode(const void* q_rot, const void* k_cache, const void* v_cache, const int64_t* pos,
+template <bool ROPE>
+static attend_fn pick_attend_hd(int hd, int g) {
+  return hd == 64 ? pick_attend<64, ROPE>(g) : hd == 128 ? pick_attend<128, ROPE>(g) : pick_attend<256, ROPE>(g);
+}
+
+extern "C" int spectra_attend_decode(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t,
                                      int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq,
-                                     void* workspace, size_t workspace_bytes, void* out, spectra_stream_t stream) {
-  SPECTRA_REQUIRE(q_rot && k_cache && v_cache && pos && out, "NULL pointer");
+                                     void* k_cache, void* v_cache, void* workspace, size_t workspace_bytes, void* out,
+                                     spectra_stream_t stream) {
+  SPECTRA_REQUIRE(qkv && pos && k_cache && v_cache && out, "NULL pointer");
+  SPECTRA_REQUIRE((cos_t == nullptr) == (sin_t == nullptr), "cos and sin must both be given or both be NULL");
   SPECTRA_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
   SPECTRA_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim must be 64, 128 or 256");
   SPECTRA_REQUIRE(max_seq >= 1 && max_seq <= (1 << 20), "bad max_seq");
-  SPECTRA_REQUIRE(aligned16(q_rot) && aligned16(k_cache) && aligned16(v_cache), "q and the caches must be 16-byte aligned");
-  if (workspace == nullptr || workspace_bytes < spectra_attend_workspace(heads, head_dim, max_seq))
-    return fail(SPECTRA_ERR_WORKSPACE, "workspace missing or smaller than spectra_attend_workspace()");
+  SPECTRA_REQUIRE(aligned16(qkv) && aligned16(k_cache) && aligned16(v_cache) &&
+                      (cos_t == nullptr || (aligned16(cos_t) && aligned16(sin_t))),
+                  "qkv, the caches and the cos / sin tables must be 16-byte aligned");
+  if (workspace == nullptr || workspace_bytes < spectra_attend_workspace(heads, head_dim, max_seq) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15))
+    return fail(SPECTRA_ERR_WORKSPACE, "workspace missing, unaligned or smaller than spectra_attend_workspace()");
   const int g = heads / kv_heads;
-  const attend_fn fn = head_dim == 64 ? pick_attend<64>(g) : head_dim == 128 ? pick_attend<128>(g) : pick_attend<256>(g);
+  const attend_fn fn = cos_t ? pick_attend_hd<true>(head_dim, g) : pick_attend_hd<false>(head_dim, g);
   if (fn == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "decode attention serves 1, 2, 3, 4, 6 or 8 query heads per KV head");
   const int nspan = spectra_attend_spans(max_seq);
   const float scale = 1.0f / sqrtf((float)head_dim);
-  const hipStream_t s = (hipStream_t)stream;
   float* part = (float*)workspace;
-  hipLaunchKernelGGL(fn, dim3((unsigned)kv_heads, (unsigned)nspan), dim3(kDecThreads), 0, s, (const uint16_t*)q_rot,
-                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, pos, max_seq, scale, part);
+  const hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(fn, dim3((unsigned)kv_heads, (unsigned)nspan), dim3(kDecThreads), 0, s, (const uint16_t*)qkv,
+                     pos, cos_t, sin_t, heads, kv_heads, max_seq, scale, (uint16_t*)k_cache, (uint16_t*)v_cache, part);
   SPECTRA_HIP_CHECK(hipGetLastError());
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)heads), dim3((unsigned)head_dim), 0, s, part, nspan, head_dim,
                      (uint16_t*)out);

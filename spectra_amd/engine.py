@@ -277,11 +277,11 @@ class SpectraDecoder(nn.Module):
         g = c.heads // c.kv_heads
         x = rmsnorm(h, self.norm_w[2 * li], c.rms_eps, residual=delta)
         qkv = blk["qkv"](x)
-        q = rope_append(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li])
-        if causal_len is None:
-            a = attend_decode(q.reshape(c.heads, hd), self.k_cache[li], self.v_cache[li], pos, self.attn_ws)
-            a = a.reshape(1, c.hidden)
+        if causal_len is None:  # one kernel: RoPE, cache append, attention over [0, pos]
+            a = attend_decode(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li],
+                              self.attn_ws).reshape(1, c.hidden)
         else:
+            q = rope_append(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li])
             L = causal_len
             qg = q.permute(1, 0, 2).reshape(c.kv_heads, g * T, hd).contiguous()  # head = kv * g + j
             kt = self.k_cache[li][:, :L, :].transpose(1, 2).contiguous()  # [kv, hd, L]

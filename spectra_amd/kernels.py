@@ -356,31 +356,37 @@ def attend_workspace_bytes(heads: int, head_dim: int, max_seq: int) -> int:
     return int(L.load().spectra_attend_workspace(heads, head_dim, max_seq))
 
 
-def attend_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+def attend_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: Optional[torch.Tensor], sin: Optional[torch.Tensor],
+                  heads: int, kv_heads: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
                   workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Attention of one query token ``q`` [heads, d] over positions [0, pos] of the caches
-    [kv, L, d] (``pos`` int64 [1] on the device); returns fp16 [heads, d]."""
-    _need_f16(q, "q")
+    """Decode attention of the fused-QKV row ``qkv`` [(heads + 2 kv_heads) * d] of the token at
+    position ``pos`` (int64 [1] on the device): rotates q and k (``cos``/``sin`` fp32 [L, d/2],
+    None = no rotation), appends k and v to the caches [kv, L, d], attends over [0, pos];
+    returns fp16 [heads, d].  ``workspace`` (uint8, span partials) defaults to a fresh buffer."""
+    _need_f16(qkv, "qkv")
     _need_f16(k_cache, "k_cache")
     _need_f16(v_cache, "v_cache")
     kv, lmax, hd = k_cache.shape
-    heads = q.numel() // hd
-    if q.numel() != heads * hd or v_cache.shape != k_cache.shape:
-        raise ValueError("q must be [heads, d] and k_cache, v_cache [kv, L, d]")
+    if v_cache.shape != k_cache.shape or kv != kv_heads or qkv.numel() != (heads + 2 * kv_heads) * hd:
+        raise ValueError("qkv must hold (heads + 2 kv_heads) * d values and the caches be [kv_heads, L, d]")
     if pos.dtype != torch.int64 or pos.numel() != 1:
         raise ValueError("pos must be int64 [1]")
+    if (cos is None) != (sin is None):
+        raise ValueError("cos and sin must both be given or both be None")
+    for t, name in ((cos, "cos"), (sin, "sin")):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or t.shape != (lmax, hd // 2)):
+            raise ValueError(f"{name} must be contiguous fp32 [L, d/2]")
     need = attend_workspace_bytes(heads, hd, lmax)
     if workspace is None:
-        workspace = torch.empty(need, device=q.device, dtype=torch.uint8)
+        workspace = torch.empty(need, device=qkv.device, dtype=torch.uint8)
     if out is None:
-        out = torch.empty((heads, hd), device=q.device, dtype=torch.float16)
+        out = torch.empty((heads, hd), device=qkv.device, dtype=torch.float16)
     _need_f16(out, "out")
     lib = L.load()
-    L.check("spectra_attend_decode", lib.spectra_attend_decode(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
-                                                                pos.data_ptr(), heads, kv, hd, lmax,
-                                                                workspace.data_ptr(),
-                                                                workspace.numel() * workspace.element_size(),
-                                                                out.data_ptr(), _stream(q.device)))
+    L.check("spectra_attend_decode", lib.spectra_attend_decode(
+        qkv.data_ptr(), pos.data_ptr(), cos.data_ptr() if cos is not None else None,
+        sin.data_ptr() if sin is not None else None, heads, kv, hd, lmax, k_cache.data_ptr(), v_cache.data_ptr(),
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(), _stream(qkv.device)))
     return out
 
 

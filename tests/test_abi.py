@@ -109,10 +109,12 @@ def test_decode_kernels_reject_bad_arguments():
     # 64 spans of 64 positions for max_seq 4096; the partials are fp32 [heads][spans][d + 2]
     assert lib.spectra_attend_spans(4096) == 64 and lib.spectra_attend_spans(4097) == 65
     assert lib.spectra_attend_workspace(24, 128, 1000) == 24 * 16 * 130 * 4
-    assert lib.spectra_attend_decode(p, p, p, p, 24, 8, 128, 1024, None, 0, p, None) == L.ERR_WORKSPACE
-    assert lib.spectra_attend_decode(p, p, p, p, 24, 8, 32, 1024, p, 1 << 20, p, None) == L.ERR_INVALID
-    assert lib.spectra_attend_decode(p, p, p, p, 40, 8, 128, 1024, p, 1 << 24, p, None) == L.ERR_UNSUPPORTED
-    assert lib.spectra_attend_decode(p, p, p, p, 24, 8, 96, 1024, p, 1 << 24, p, None) == L.ERR_INVALID
+    args = (p, p, p, p)
+    assert lib.spectra_attend_decode(*args, 24, 8, 128, 1024, p, p, None, 0, p, None) == L.ERR_WORKSPACE
+    assert lib.spectra_attend_decode(*args, 24, 8, 32, 1024, p, p, p, 1 << 20, p, None) == L.ERR_INVALID
+    assert lib.spectra_attend_decode(*args, 40, 8, 128, 1024, p, p, p, 1 << 24, p, None) == L.ERR_UNSUPPORTED
+    assert lib.spectra_attend_decode(*args, 24, 8, 96, 1024, p, p, p, 1 << 24, p, None) == L.ERR_INVALID
+    assert lib.spectra_attend_decode(p, p, p, None, 24, 8, 128, 1024, p, p, p, 1 << 24, p, None) == L.ERR_INVALID
     assert lib.spectra_silu_mul(p, 100, 1, 64, p, None) == L.ERR_INVALID
     assert lib.spectra_greedy_next(p, 0, p, None, 0, None, None) == L.ERR_INVALID
     assert lib.spectra_greedy_next(p, 10, p, p, 10, None, None) == L.ERR_INVALID  # history needs pos

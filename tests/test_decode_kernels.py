@@ -8,8 +8,10 @@ restatements of the same math:
   nowhere else;
 * greedy_next: the index torch.argmax returns (ties: the first), history and position
   updated on the device;
-* attend_decode: within 2e-3 (times max|v|) of fp32 softmax attention over the cache
-  prefix, at positions on and around the 64-position span edges and at the last slot;
+* attend_decode: the rotated key and the value appended bit-exactly at the position (and
+  nothing else written), the output within 2e-3 (times max|v|) of fp32 softmax attention
+  over the cache prefix, at positions on and around the 64-position span edges and at the
+  last slot, with one workspace reused across calls;
 * silu_mul: within rel 2e-3 of fp32 silu(g) * u.
 """
 import math
@@ -73,24 +75,43 @@ def test_rope_append(hip, heads, kv, hd, T):
     assert bool((kc[:, keep, :] == 7.0).all()) and bool((vc[:, keep, :] == 7.0).all())
 
 
+def _tables(L, hd):
+    inv = 1.0 / (5e5 ** (torch.arange(0, hd, 2, device="cuda", dtype=torch.float32) / hd))
+    ang = torch.arange(L, device="cuda", dtype=torch.float32)[:, None] * inv[None, :]
+    return torch.cos(ang), torch.sin(ang)
+
+
 @pytest.mark.parametrize("heads,kv,hd,L", [(24, 8, 128, 768), (4, 4, 64, 1000), (8, 2, 256, 130), (6, 3, 64, 64),
                                            (32, 4, 128, 300), (12, 2, 64, 200)])
-def test_attend_decode(hip, heads, kv, hd, L):
-    g = torch.Generator(device="cuda").manual_seed(heads * L)
+@pytest.mark.parametrize("rope", [True, False])
+def test_attend_decode(hip, heads, kv, hd, L, rope):
+    g = torch.Generator(device="cuda").manual_seed(heads * L + rope)
     kc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
     vc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
-    q = (torch.randn(heads, hd, device="cuda", generator=g) * 2).half()
-    ws = torch.empty(K.attend_workspace_bytes(heads, hd, L), device="cuda", dtype=torch.uint8)
+    cos, sin = _tables(L, hd) if rope else (None, None)
+    ws = torch.full((K.attend_workspace_bytes(heads, hd, L),), 255, device="cuda", dtype=torch.uint8)  # reused
     grp = heads // kv
     for p in sorted({0, 1, 62, 63, 64, 65, L // 2, L - 2, L - 1}):
         if p >= L:
             continue
-        case(heads=heads, kv=kv, hd=hd, L=L, pos=p)
+        case(heads=heads, kv=kv, hd=hd, L=L, rope=rope, pos=p)
+        qkv = (torch.randn((heads + 2 * kv) * hd, device="cuda", generator=g) * 2).half()
+        kc0, vc0 = kc.clone(), vc.clone()
         pos = torch.tensor([p], device="cuda", dtype=torch.int64)
-        out = K.attend_decode(q, kc, vc, pos, ws)
+        out = K.attend_decode(qkv, pos, cos, sin, heads, kv, kc, vc, ws)
+        q = qkv[: heads * hd].reshape(1, heads, hd)
+        k = qkv[heads * hd: (heads + kv) * hd].reshape(1, kv, hd)
+        v = qkv[(heads + kv) * hd:].reshape(kv, hd)
+        if rope:
+            q, k = _rope_ref(q, cos[p][None, None, :], sin[p][None, None, :]), _rope_ref(k, cos[p][None, None, :],
+                                                                                        sin[p][None, None, :])
+        # the append: row p of both caches, nothing else
+        kc0[:, p, :] = k[0]
+        vc0[:, p, :] = v
+        assert torch.equal(kc, kc0) and torch.equal(vc, vc0)
         kk = kc[:, : p + 1, :].float().transpose(1, 2).repeat_interleave(grp, dim=0)  # [heads, hd, n]
         vv = vc[:, : p + 1, :].float().repeat_interleave(grp, dim=0)  # [heads, n, hd]
-        sc = torch.matmul(q.float()[:, None, :], kk.contiguous())[:, 0, :] / math.sqrt(hd)
+        sc = torch.matmul(q[0].float()[:, None, :], kk.contiguous())[:, 0, :] / math.sqrt(hd)
         ref = torch.matmul(torch.softmax(sc, -1)[:, None, :], vv.contiguous())[:, 0, :]
         err = (out.float() - ref).abs().max().item()
         assert err <= 2e-3 * vc.abs().max().item(), (p, err)
