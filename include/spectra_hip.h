@@ -99,6 +99,38 @@ int spectra_w4a16_gemv(const spectra_qweight_t* w, const void* x, int64_t ldx, i
                        int32_t act_dtype, void* out, int64_t ldo, spectra_stream_t stream);
 
 /*
+ * The GEMV with the work around a decoder's linears fused in (no reference counterpart:
+ * the reference runs these as separate Inductor-fused submodules, engine.py:1240-1250):
+ *   prologue RMSNORM:  x is the residual stream h; the product uses
+ *                      rmsnorm(h) = h * rsqrt(mean(h^2) + eps) * norm_weight, with the
+ *                      row scale applied to the accumulated output (one fp16 rounding of
+ *                      the normalised activations fewer than the separate kernels);
+ *   prologue SILU_MUL: x rows hold [g | u] (2K values, ldx >= 2K); the product uses
+ *                      fp16(silu(g) * u), bit-identical to spectra_silu_mul;
+ *   residual:          out = act(residual + act(y)) (act = the activation dtype), residual
+ *                      [m, N] row stride residual_stride, may alias out (in-place update).
+ * Prologues serve m = 1, fp16 activations and NF4 weights (SPECTRA_ERR_UNSUPPORTED
+ * otherwise); the residual serves every GEMV.
+ */
+typedef enum {
+  SPECTRA_PROLOGUE_NONE = 0,
+  SPECTRA_PROLOGUE_RMSNORM = 1,
+  SPECTRA_PROLOGUE_SILU_MUL = 2
+} spectra_prologue_t;
+
+typedef struct spectra_gemv_fusion {
+  int32_t prologue;          /* spectra_prologue_t */
+  float eps;                 /* RMSNORM */
+  const uint16_t* norm_weight; /* RMSNORM: fp16 [K], 16-byte aligned */
+  const void* residual;      /* optional, act dtype [m, N] */
+  int64_t residual_stride;
+} spectra_gemv_fusion_t;
+
+int spectra_w4a16_gemv_fused(const spectra_qweight_t* w, const void* x, int64_t ldx, int32_t m,
+                             int32_t act_dtype, const spectra_gemv_fusion_t* fusion, void* out, int64_t ldo,
+                             spectra_stream_t stream);
+
+/*
  * Batched / prefill GEMM family (any M >= 1, MFMA):
  *   out = FWHT_hb(a) . W_eff^T + bias,   fp16 MFMA operands, fp32 accumulation.
  * a: act_dtype [m, K] row stride lda; out: act_dtype [m, N] row stride ldo.

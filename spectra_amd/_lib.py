@@ -38,12 +38,23 @@ class QWeight(ctypes.Structure):
     ]
 
 
+PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SILU_MUL = 0, 1, 2
+
+
+class GemvFusion(ctypes.Structure):
+    """Mirror of ``spectra_gemv_fusion_t``."""
+    _fields_ = [("prologue", c_int32), ("eps", ctypes.c_float), ("norm_weight", c_void_p),
+                ("residual", c_void_p), ("residual_stride", c_int64)]
+
+
 # name -> (restype, argtypes); every symbol include/spectra_hip.h declares
 SIGNATURES = {
     "spectra_version": (c_char_p, []),
     "spectra_last_error": (c_char_p, []),
     "spectra_w4a16_gemv": (c_int32, [ctypes.POINTER(QWeight), c_void_p, c_int64, c_int32, c_int32,
                                      c_void_p, c_int64, c_void_p]),
+    "spectra_w4a16_gemv_fused": (c_int32, [ctypes.POINTER(QWeight), c_void_p, c_int64, c_int32, c_int32,
+                                           ctypes.POINTER(GemvFusion), c_void_p, c_int64, c_void_p]),
     "spectra_w4a16_gemm_workspace": (c_size_t, [ctypes.POINTER(QWeight), c_int64, c_int32]),
     "spectra_w4a16_gemm": (c_int32, [ctypes.POINTER(QWeight), c_void_p, c_int64, c_int64, c_int32,
                                      c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),

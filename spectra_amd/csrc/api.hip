@@ -82,7 +82,7 @@ int ensure_lds_limit(const void* kernel, bool dyn_at_zero) {
 // gemv.hip / gemm.hip
 namespace spectra {
 int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, int act_dtype, void* out,
-                int64_t ldo, hipStream_t stream);
+                int64_t ldo, hipStream_t stream, const spectra_gemv_fusion_t* fusion);
 }
 
 extern "C" const char* spectra_version(void) { return "spectra_hip 0.1.0 gfx950"; }

@@ -11,11 +11,11 @@ static uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
 struct GemvPlan {
   int mt, S, G, rpw, R, BD, grid, ocap;
-  uint32_t off_xp, off_xsc, off_part, off_codes, off_rp, off_bias, off_oprod, lds_bytes;
+  uint32_t off_xp, off_xsc, off_part, off_codes, off_rp, off_bias, off_ss, off_res, off_oprod, lds_bytes;
 };
 
 // returns false when the shape does not fit this kernel family
-static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, GemvPlan* pl) {
+static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, GemvPlan* pl, int rpw_cap = kRpwMax) {
   const int mt = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
   if (m > 4 || k > 16384 || k % 32) return false;
   const int S = (int)((k + 2047) / 2048);
@@ -25,7 +25,7 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   if (G > want) G = (int)want;
   if (G < 1) G = 1;
   int rpw = (int)((want + G - 1) / G);
-  const int rpw_max = mt == 4 ? 8 : kRpwMax;
+  const int rpw_max = mt == 4 ? 8 : rpw_cap;
   if (rpw > rpw_max && mt == 1) {
     // more rows than one resident workgroup per CU holds: size for two per CU (LDS <= 80 KB
     // below; the one-row kernels stay within 128 VGPRs), so that one workgroup's set-up
@@ -55,6 +55,10 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   off = align16(off + (uint32_t)((R + 1) * 4));
   pl->off_bias = off;
   off = align16(off + (uint32_t)(R * 4));
+  pl->off_ss = off;  // per-wave sums of squares (fused RMSNorm)
+  off = align16(off + (uint32_t)(kMaxWaves * 4));
+  pl->off_res = off;  // residual values of the outputs (16-bit)
+  off = align16(off + (uint32_t)(R * mt * 2));
   pl->off_oprod = off;
   if (off > 163840) return false;
   // outlier products staged in LDS: the entries one load round covers (four per thread
@@ -78,12 +82,15 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
 static bool ptr_aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, int act_dtype, void* out,
-                int64_t ldo, hipStream_t stream) {
+                int64_t ldo, hipStream_t stream, const spectra_gemv_fusion_t* fu) {
   const bool outliers = w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS ||
                         (w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0);
   GemvPlan pl;
   const bool csr = outliers && w->outlier_kind == SPECTRA_OUTLIERS_CSR;
-  if (!plan_gemv(w->n, w->k, m, outliers, csr, &pl))
+  const int pro = fu ? fu->prologue : SPECTRA_PROLOGUE_NONE;
+  // the fused-RMSNorm kernels hold the norm weights through the stream issue: 9 rows per
+  // wave keep them within 128 VGPRs (two resident workgroups per CU)
+  if (!plan_gemv(w->n, w->k, m, outliers, csr, &pl, pro == SPECTRA_PROLOGUE_RMSNORM ? 9 : kRpwMax))
     return fail(SPECTRA_ERR_UNSUPPORTED, "shape not served by the GEMV family (use the GEMM family)");
   SPECTRA_REQUIRE(w->hadamard_block == 0 || w->hadamard_block <= 512, "GEMV serves hadamard_block <= 512");
   SPECTRA_REQUIRE(ptr_aligned(x, 16) && ldx % 8 == 0, "x must be 16-byte aligned with a row stride multiple of 8");
@@ -119,10 +126,16 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
   p.R = pl.R; p.S = pl.S; p.G = pl.G; p.ocap = pl.ocap;
   p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_part = pl.off_part; p.off_codes = pl.off_codes;
   p.off_rp = pl.off_rp; p.off_bias = pl.off_bias; p.off_oprod = pl.off_oprod;
+  p.off_ss = pl.off_ss; p.off_res = pl.off_res;
   p.out_scale = w->hadamard_block ? (float)(1.0 / std::sqrt((double)w->hadamard_block)) : 1.0f;
   p.inv_n_out = w->num_outliers > 0 ? 1.0f / (float)w->num_outliers : 1.0f;
-  gemv_fn fn = act_dtype == SPECTRA_BF16 ? gemv_pick_bf16(w->format, pl.mt, pl.rpw)
-                                         : gemv_pick_f16(w->format, pl.mt, pl.rpw);
+  p.nw = fu ? fu->norm_weight : nullptr;
+  p.eps = fu ? fu->eps : 0.0f;
+  p.res = fu ? fu->residual : nullptr;
+  p.ldr = fu ? fu->residual_stride : 0;
+  gemv_fn fn = pro != SPECTRA_PROLOGUE_NONE ? gemv_pick_f16_pro(pro == SPECTRA_PROLOGUE_RMSNORM ? kProRms : kProSiluMul, pl.rpw)
+               : act_dtype == SPECTRA_BF16 ? gemv_pick_bf16(w->format, pl.mt, pl.rpw)
+                                           : gemv_pick_f16(w->format, pl.mt, pl.rpw);
   const int st = ensure_lds_limit((const void*)fn, true);
   if (st != SPECTRA_OK) return st;
   hipLaunchKernelGGL(fn, dim3(pl.grid), dim3(pl.BD), pl.lds_bytes, stream, p);
@@ -140,5 +153,28 @@ extern "C" int spectra_w4a16_gemv(const spectra_qweight_t* w, const void* x, int
   SPECTRA_REQUIRE(m >= 1 && m <= 4, "the GEMV family serves 1 <= m <= 4");
   SPECTRA_REQUIRE(act_dtype == SPECTRA_F16 || act_dtype == SPECTRA_BF16, "activations must be fp16 or bf16");
   SPECTRA_REQUIRE(ldx >= w->k && ldo >= w->n, "row stride too small");
-  return spectra::gemv_launch(w, x, ldx, m, act_dtype, out, ldo, (hipStream_t)stream);
+  return spectra::gemv_launch(w, x, ldx, m, act_dtype, out, ldo, (hipStream_t)stream, nullptr);
+}
+
+extern "C" int spectra_w4a16_gemv_fused(const spectra_qweight_t* w, const void* x, int64_t ldx, int32_t m,
+                                        int32_t act_dtype, const spectra_gemv_fusion_t* fusion, void* out,
+                                        int64_t ldo, spectra_stream_t stream) {
+  int st = spectra::validate_qweight(w);
+  if (st != SPECTRA_OK) return st;
+  SPECTRA_REQUIRE(x != nullptr && out != nullptr && fusion != nullptr, "x/out/fusion is NULL");
+  SPECTRA_REQUIRE(m >= 1 && m <= 4, "the GEMV family serves 1 <= m <= 4");
+  SPECTRA_REQUIRE(act_dtype == SPECTRA_F16 || act_dtype == SPECTRA_BF16, "activations must be fp16 or bf16");
+  const int pro = fusion->prologue;
+  SPECTRA_REQUIRE(pro == SPECTRA_PROLOGUE_NONE || pro == SPECTRA_PROLOGUE_RMSNORM || pro == SPECTRA_PROLOGUE_SILU_MUL,
+                  "unknown prologue");
+  SPECTRA_REQUIRE(ldx >= (pro == SPECTRA_PROLOGUE_SILU_MUL ? 2 * w->k : w->k) && ldo >= w->n, "row stride too small");
+  if (pro != SPECTRA_PROLOGUE_NONE) {
+    if (m != 1 || act_dtype != SPECTRA_F16 || w->format != SPECTRA_FMT_NF4)
+      return spectra::fail(SPECTRA_ERR_UNSUPPORTED, "fused prologues serve one fp16 row of an NF4 weight");
+    if (pro == SPECTRA_PROLOGUE_RMSNORM)
+      SPECTRA_REQUIRE(fusion->norm_weight != nullptr && (reinterpret_cast<uintptr_t>(fusion->norm_weight) & 15) == 0,
+                      "RMSNorm needs a 16-byte aligned fp16 weight");
+  }
+  if (fusion->residual != nullptr) SPECTRA_REQUIRE(fusion->residual_stride >= w->n, "residual row stride too small");
+  return spectra::gemv_launch(w, x, ldx, m, act_dtype, out, ldo, (hipStream_t)stream, fusion);
 }

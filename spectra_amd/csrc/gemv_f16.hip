@@ -8,4 +8,8 @@ gemv_fn gemv_pick_f16(int fmt, int mt, int rpw) {
                                 : pick_kernel<SPECTRA_FMT_ASYM_G32, false>(mt, rpw);
 }
 
+gemv_fn gemv_pick_f16_pro(int pro, int rpw) {
+  return pro == kProRms ? pick_pro_rpw<kProRms>(rpw) : pick_pro_rpw<kProSiluMul>(rpw);
+}
+
 }  // namespace spectra

@@ -63,10 +63,20 @@ struct GemvParams {
   int okind, n_out, ow_dt, bias_dt, act_dt;
   int csr_nnz;
   int R, S, G, ocap;
-  uint32_t off_xp, off_xsc, off_part, off_codes, off_rp, off_bias, off_oprod;
+  uint32_t off_xp, off_xsc, off_part, off_codes, off_rp, off_bias, off_oprod, off_ss, off_res;
   float out_scale;  // 1/sqrt(hadamard_block) (1 without rotation)
   float inv_n_out;  // 1/n_out (dense outlier columns)
+  // fusions (kernels with PRO != 0 serve one fp16 row)
+  const uint16_t* nw;  // PRO 2: RMSNorm weight fp16 [K]
+  float eps;        // PRO 2
+  const void* res;  // optional residual [m, N] (act dtype, may alias out): out = res + out
+  int64_t ldr;
 };
+
+// activation prologues fused into the GEMV
+constexpr int kProNone = 0;     // x as given
+constexpr int kProSiluMul = 1;  // x row = [g | u] (2K values): fp16(silu(g) * u)
+constexpr int kProRms = 2;      // x = h: h * w_norm, times rsqrt(mean(h^2) + eps) in the epilogue
 
 __device__ __forceinline__ uint16_t nf4_f16_bits(int i) {
   // fp16 roundings of the NF4 levels (compressor.py:22-27)
@@ -281,7 +291,7 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-template <int FMT, int MT, int RPW, bool BF>
+template <int FMT, int MT, int RPW, bool BF, int PRO = kProNone>
 __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int XH = 2 * MT;  // 16-element half-runs of activations per thread (at most)
@@ -305,6 +315,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   const int hpr = K >> 4;  // half-runs per activation row
   const int bL = p.log_had >= 5 ? p.log_had - 4 : (p.marlin && p.log_had == 4 ? 1 : 0);
   uint4 xr[XH][2];
+  uint4 xu[PRO == kProSiluMul ? XH : 1][2];   // the u half of a fused gate_up row
+  uint4 nwv[PRO == kProRms ? XH : 1][2];      // RMSNorm weights of the half-run (fp16)
   int xm[XH], xq[XH], xcl[XH], xhf[XH];
 #pragma unroll
   for (int i = 0; i < XH; ++i) {
@@ -329,8 +341,18 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     // (left undefined otherwise: those values are never read, and no copy or wait is
     // needed where the branch joins)
     if (i == 0 || wave * 64 + i * BD < MT * hpr) {
-      xr[i][0] = *(const uint4*)(src + (p.marlin ? 8 * hf : 16 * hf));
-      xr[i][1] = *(const uint4*)(src + (p.marlin ? 16 + 8 * hf : 16 * hf + 8));
+      const int o0 = p.marlin ? 8 * hf : 16 * hf, o1 = p.marlin ? 16 + 8 * hf : 16 * hf + 8;
+      xr[i][0] = *(const uint4*)(src + o0);
+      xr[i][1] = *(const uint4*)(src + o1);
+      if constexpr (PRO == kProSiluMul) {
+        xu[i][0] = *(const uint4*)(src + K + o0);
+        xu[i][1] = *(const uint4*)(src + K + o1);
+      }
+      if constexpr (PRO == kProRms) {
+        const uint16_t* nw = p.nw + (ok ? (int64_t)(cl >> 1) * 32 : 0);
+        nwv[i][0] = *(const uint4*)(nw + o0);
+        nwv[i][1] = *(const uint4*)(nw + o1);
+      }
     }
   }
 
@@ -394,6 +416,12 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     if (p.bias_dt == SPECTRA_F32) bias_raw = ((const uint32_t*)p.bias)[bi];
     else bias_raw = ((const uint16_t*)p.bias)[bi];
   }
+  // residual of output (row tid / Rw, column r0 + tid % Rw), read before any output is written
+  uint16_t res_raw = 0;
+  if (p.res != nullptr) {
+    const int mm = tid / Rw, rr = tid - mm * Rw;
+    res_raw = ((const uint16_t*)p.res)[mm < p.m ? (int64_t)mm * p.ldr + r0 + rr : 0];
+  }
 
   // ---------------- (3) nibble-pair LUT from a wave-private 16-entry code table ----------------
   {
@@ -423,6 +451,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   uint16_t* xp = (uint16_t*)(smem + p.off_xp);
   const int XS = ((K + 2047) >> 11) << 11;  // xp row stride: whole 2048-element slices
   float* xsc = (float*)(smem + p.off_xsc);
+  float ssq = 0.0f;  // PRO kProRms: sum of h^2 over this thread's half-runs
 #pragma unroll
   for (int i = 0; i < XH; ++i) {
     // wave-uniform guard: the cross-lane stages need every lane of the wave
@@ -439,6 +468,25 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
         v[2 * e] = h2f((uint16_t)u[e]);
         v[2 * e + 1] = h2f((uint16_t)(u[e] >> 16));
       }
+    }
+    if constexpr (PRO == kProSiluMul) {  // fp16(silu(g) * u), the silu_mul arithmetic
+      const uint32_t uu[8] = {xu[i][0].x, xu[i][0].y, xu[i][0].z, xu[i][0].w,
+                              xu[i][1].x, xu[i][1].y, xu[i][1].z, xu[i][1].w};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float g = v[e], u = h2f((uint16_t)(uu[e >> 1] >> (16 * (e & 1))));
+        v[e] = h2f(f2h(g / (1.0f + __expf(-g)) * u));
+      }
+    }
+    if constexpr (PRO == kProRms) {
+      if (tid + i * BD < MT * hpr) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ssq += v[e] * v[e];
+      }
+      const uint32_t nw[8] = {nwv[i][0].x, nwv[i][0].y, nwv[i][0].z, nwv[i][0].w,
+                              nwv[i][1].x, nwv[i][1].y, nwv[i][1].z, nwv[i][1].w};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] *= h2f((uint16_t)(nw[e >> 1] >> (16 * (e & 1))));
     }
     const bool mar = p.marlin != 0;
     // straight-line code for the common blocks (none, 128), stage branches otherwise
@@ -520,6 +568,11 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     ocv.x = *(has_o ? (const int*)(p.oidx + jj) : (const int*)p.packed);
     ovv.x = *(has_o ? (const uint16_t*)p.ow + (int64_t)(r0 + r) * p.ldow + jj : (const uint16_t*)p.packed);
     obase = tid;
+  }
+
+  if constexpr (PRO == kProRms) {  // per-wave sums of h^2, fixed order
+    for (int off = 32; off >= 1; off >>= 1) ssq += __shfl_xor(ssq, off, 64);
+    if (lane == 0) ((float*)(smem + p.off_ss))[wave] = ssq;
   }
 
   __syncthreads();  // --- barrier 1: LUT, activation pairs and run scales
@@ -627,6 +680,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   float* bl = (float*)(smem + p.off_bias);
   if (p.bias != nullptr && tid < Rw)
     bl[tid] = p.bias_dt == SPECTRA_F32 ? __builtin_bit_cast(float, bias_raw) : to_f32_16((uint16_t)bias_raw, p.bias_dt);
+  uint16_t* rl = (uint16_t*)(smem + p.off_res);
+  if (p.res != nullptr && tid < Rw * p.m) rl[tid] = res_raw;
 
   __syncthreads();  // --- barrier 2: slice partials and outlier products
 
@@ -634,6 +689,13 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   // fixed order (deterministic): lane gl of a group takes slice gl and outlier entries
   // gl, gl + 16, ... of its row, then a DPP tree sums the 16 lanes
   {
+    float inv = 1.0f;  // PRO kProRms: rsqrt(mean(h^2) + eps) of the row
+    if constexpr (PRO == kProRms) {
+      const float* ss = (const float*)(smem + p.off_ss);
+      float t = 0.0f;
+      for (int w = 0; w < nwaves; ++w) t += ss[w];
+      inv = 1.0f / sqrtf(t / (float)K + p.eps);
+    }
     const int grp = lane >> 4, gl = lane & 15;
     for (int rb = wave * 4; rb < Rw; rb += nwaves * 4) {
       const int r = rb + grp;
@@ -671,9 +733,12 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
         }
         v = row16_sum(v);
         if (gl == 0 && rv) {
+          constexpr int odt = BF ? SPECTRA_BF16 : SPECTRA_F16;
           float y = v * p.out_scale;
+          if constexpr (PRO == kProRms) y *= inv;
           if (p.bias != nullptr) y += bl[rr];
-          ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + rr] = from_f32_16(y, BF ? SPECTRA_BF16 : SPECTRA_F16);
+          if (p.res != nullptr) y = to_f32_16(from_f32_16(y, odt), odt) + to_f32_16(rl[m * Rw + rr], odt);
+          ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + rr] = from_f32_16(y, odt);
         }
       }
     }
@@ -687,6 +752,7 @@ typedef void (*gemv_fn)(const GemvParams);
 
 gemv_fn gemv_pick_f16(int fmt, int mt, int rpw);
 gemv_fn gemv_pick_bf16(int fmt, int mt, int rpw);
+gemv_fn gemv_pick_f16_pro(int pro, int rpw);  // one fp16 row, NF4, fused prologue
 
 
 template <int FMT, int MT, bool BF>
@@ -702,8 +768,25 @@ gemv_fn pick_rpw(int rpw) {
     case 8: return gemv_kernel<FMT, MT, 8, BF>;
     case 9: return gemv_kernel<FMT, MT, 9, BF>;
     case 10: return gemv_kernel<FMT, MT, 10, BF>;
-    case 11: return gemv_kernel<FMT, MT, 11, BF>;
-    default: return gemv_kernel<FMT, MT, 12, BF>;
+    default: return gemv_kernel<FMT, MT, 11, BF>;
+  }
+}
+
+// one-row fp16 NF4 kernels with a fused prologue
+template <int PRO>
+gemv_fn pick_pro_rpw(int rpw) {
+  switch (rpw) {
+    case 1: return gemv_kernel<SPECTRA_FMT_NF4, 1, 1, false, PRO>;
+    case 2: return gemv_kernel<SPECTRA_FMT_NF4, 1, 2, false, PRO>;
+    case 3: return gemv_kernel<SPECTRA_FMT_NF4, 1, 3, false, PRO>;
+    case 4: return gemv_kernel<SPECTRA_FMT_NF4, 1, 4, false, PRO>;
+    case 5: return gemv_kernel<SPECTRA_FMT_NF4, 1, 5, false, PRO>;
+    case 6: return gemv_kernel<SPECTRA_FMT_NF4, 1, 6, false, PRO>;
+    case 7: return gemv_kernel<SPECTRA_FMT_NF4, 1, 7, false, PRO>;
+    case 8: return gemv_kernel<SPECTRA_FMT_NF4, 1, 8, false, PRO>;
+    case 9: return gemv_kernel<SPECTRA_FMT_NF4, 1, 9, false, PRO>;
+    case 10: return gemv_kernel<SPECTRA_FMT_NF4, 1, 10, false, PRO>;
+    default: return gemv_kernel<SPECTRA_FMT_NF4, 1, 11, false, PRO>;
   }
 }
 

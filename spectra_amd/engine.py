@@ -16,7 +16,7 @@ import torch
 import torch.nn as nn
 
 from .kernels import (GEMV_MAX_M, QWeightOperands, attend_decode, attend_workspace_bytes, greedy_next, rmsnorm,
-                      rope_append, silu_mul, w4_embedding, w4a16_linear)
+                      rope_append, silu_mul, w4_embedding, w4a16_gemv_fused, w4a16_linear)
 
 __all__ = ["SpectraFusedLinear", "SpectraFusedEmbedding", "DecoderConfig", "SpectraDecoder"]
 
@@ -249,6 +249,7 @@ class SpectraDecoder(nn.Module):
         self.lm_head.set_weights(qe.packed, qe.absmax, None, outlier_idx=col, outlier_weight=val, marlin_layout=True,
                                  outlier_rowptr=qe.rowptr if col is not None else None)
         self.norm_w = [torch.ones(c.hidden, device=dev, dtype=torch.float32) for _ in range(2 * c.layers + 1)]
+        self.norm_w16 = [w.half() for w in self.norm_w]  # the fused GEMV prologues read fp16 weights
         # KV cache [layer, kv, max_seq, head_dim]: a position's head is one 16-byte-aligned run
         self.k_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
         self.v_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
@@ -268,39 +269,54 @@ class SpectraDecoder(nn.Module):
     # -- building blocks ---------------------------------------------------------------------
     def _layer(self, li: int, h: torch.Tensor, delta: Optional[torch.Tensor], pos: torch.Tensor,
                causal_len: Optional[int]) -> torch.Tensor:
-        """One decoder layer for T tokens at positions ``pos`` (device int64 [T]).  ``h`` is the
-        residual stream, updated in place with the previous layer's output ``delta``; returns
-        this layer's MLP output (added by the next norm).  Prefill: causal_len = T (positions
-        0..T-1); decode: None (one token over the cache)."""
+        """One prefill layer for T tokens at positions 0..T-1 (``pos``, device int64 [T];
+        causal_len = T).  ``h`` is the residual stream, updated in place with the previous
+        layer's output ``delta``; returns this layer's MLP output (added by the next norm)."""
         c, blk = self.cfg, self.blocks[li]
         hd, T = c.head_dim, h.shape[0]
         g = c.heads // c.kv_heads
         x = rmsnorm(h, self.norm_w[2 * li], c.rms_eps, residual=delta)
         qkv = blk["qkv"](x)
-        if causal_len is None:  # one kernel: RoPE, cache append, attention over [0, pos]
-            a = attend_decode(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li],
-                              self.attn_ws).reshape(1, c.hidden)
-        else:
-            q = rope_append(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li])
-            L = causal_len
-            qg = q.permute(1, 0, 2).reshape(c.kv_heads, g * T, hd).contiguous()  # head = kv * g + j
-            kt = self.k_cache[li][:, :L, :].transpose(1, 2).contiguous()  # [kv, hd, L]
-            vv = self.v_cache[li][:, :L, :].contiguous()
-            s = torch.matmul(qg, kt).float() * (1.0 / math.sqrt(hd))  # [kv, g*T, L]
-            qpos = pos.repeat(g)  # row r = j * T + t -> position pos[t]
-            s = s.masked_fill((self.arange[:L][None, :] > qpos[:, None])[None], float("-inf"))
-            a = torch.matmul(torch.softmax(s, dim=-1).half(), vv)  # [kv, g*T, hd]
-            a = a.reshape(c.heads, T, hd).permute(1, 0, 2).reshape(T, c.hidden)
+        q = rope_append(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li])
+        L = causal_len
+        qg = q.permute(1, 0, 2).reshape(c.kv_heads, g * T, hd).contiguous()  # head = kv * g + j
+        kt = self.k_cache[li][:, :L, :].transpose(1, 2).contiguous()  # [kv, hd, L]
+        vv = self.v_cache[li][:, :L, :].contiguous()
+        s = torch.matmul(qg, kt).float() * (1.0 / math.sqrt(hd))  # [kv, g*T, L]
+        qpos = pos.repeat(g)  # row r = j * T + t -> position pos[t]
+        s = s.masked_fill((self.arange[:L][None, :] > qpos[:, None])[None], float("-inf"))
+        a = torch.matmul(torch.softmax(s, dim=-1).half(), vv)  # [kv, g*T, hd]
+        a = a.reshape(c.heads, T, hd).permute(1, 0, 2).reshape(T, c.hidden)
         o = blk["o"](a)
         x = rmsnorm(h, self.norm_w[2 * li + 1], c.rms_eps, residual=o)
         return blk["down"](silu_mul(blk["gate_up"](x)))
 
+    def _layer_decode(self, li: int, h: torch.Tensor, pos: torch.Tensor) -> None:
+        """One decoder layer for the token at device position ``pos``, six kernels: the
+        RMSNorms ride in the QKV / gate_up GEMV prologues, SiLU-mul in the down_proj prologue,
+        the residual adds in the o_proj / down_proj epilogues (``h`` updated in place)."""
+        c, blk = self.cfg, self.blocks[li]
+        qkv = w4a16_gemv_fused(blk["qkv"]._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[2 * li],
+                               eps=c.rms_eps)
+        a = attend_decode(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li],
+                          self.attn_ws)
+        w4a16_gemv_fused(blk["o"]._operands(), a.reshape(1, c.hidden), residual=h, out=h)
+        gu = w4a16_gemv_fused(blk["gate_up"]._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[2 * li + 1],
+                              eps=c.rms_eps)
+        w4a16_gemv_fused(blk["down"]._operands(), gu, prologue="silu_mul", residual=h, out=h)
+
     def forward_tokens(self, ids: torch.Tensor, pos: torch.Tensor, causal_len: Optional[int]) -> torch.Tensor:
         h = self.embed(ids)
+        c = self.cfg
+        if causal_len is None:  # decode: one token, fused GEMVs
+            for li in range(c.layers):
+                self._layer_decode(li, h, pos)
+            return w4a16_gemv_fused(self.lm_head._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[-1],
+                                    eps=c.rms_eps)
         delta = None
-        for li in range(self.cfg.layers):
+        for li in range(c.layers):
             delta = self._layer(li, h, delta, pos, causal_len)
-        x = rmsnorm(h[-1:], self.norm_w[2 * self.cfg.layers], self.cfg.rms_eps, residual=delta[-1:])
+        x = rmsnorm(h[-1:], self.norm_w[2 * c.layers], c.rms_eps, residual=delta[-1:])
         return self.lm_head(x)  # logits of the last token [1, vocab]
 
     # -- generation --------------------------------------------------------------------------

@@ -26,7 +26,7 @@ from . import _lib as L
 
 __all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_dequant", "fwht_rows",
            "QWeightOperands", "GEMV_MAX_M", "w4_embedding", "rmsnorm", "rope_append", "attend_decode",
-           "attend_workspace_bytes", "silu_mul", "greedy_next"]
+           "attend_workspace_bytes", "silu_mul", "greedy_next", "w4a16_gemv_fused"]
 
 GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
 
@@ -420,3 +420,47 @@ def greedy_next(logits: torch.Tensor, token: torch.Tensor, history: Optional[tor
                                                             pos.data_ptr() if pos is not None else None,
                                                             _stream(logits.device)))
     return token
+
+
+def w4a16_gemv_fused(ops: QWeightOperands, x: torch.Tensor, *, prologue: str = "none",
+                     norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
+                     residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One-row GEMV with a decoder layer's neighbouring work fused in:
+
+    * ``prologue="rmsnorm"``: x is the residual stream h; computes linear(rmsnorm(h)) with
+      ``norm_weight`` (fp16 [K]) and ``eps``;
+    * ``prologue="silu_mul"``: x is a fused gate_up row [2K]; computes linear(silu(g) * u);
+    * ``residual`` [1, N]: returns residual + linear(...) (fp16 roundings of both, as the
+      separate add); ``out`` may be ``residual`` itself (in-place update).
+    """
+    codes = {"none": L.PROLOGUE_NONE, "rmsnorm": L.PROLOGUE_RMSNORM, "silu_mul": L.PROLOGUE_SILU_MUL}
+    if prologue not in codes:
+        raise ValueError(f"prologue must be one of {list(codes)}")
+    _need_f16(x, "x", contiguous=False)
+    kin = 2 * ops.k if prologue == "silu_mul" else ops.k
+    if x.shape[-1] != kin:
+        raise ValueError(f"x must have {kin} values per row")
+    x2, ldx = _rows(x.reshape(-1, kin), "x", 16)
+    fu = L.GemvFusion()
+    fu.prologue = codes[prologue]
+    fu.eps = float(eps)
+    if prologue == "rmsnorm":
+        if norm_weight is None or norm_weight.dtype != torch.float16 or norm_weight.numel() != ops.k:
+            raise ValueError("rmsnorm needs an fp16 norm_weight of K values")
+        nw = norm_weight.contiguous()
+        fu.norm_weight = nw.data_ptr()
+    if out is None:
+        out = torch.empty((x2.shape[0], ops.n), device=x.device, dtype=torch.float16)
+    _need_f16(out, "out", contiguous=False)
+    out2 = out.reshape(-1, ops.n)
+    if residual is not None:
+        _need_f16(residual, "residual", contiguous=False)
+        r2 = residual.reshape(-1, ops.n)
+        if r2.stride(1) != 1:
+            raise ValueError("residual rows must be contiguous")
+        fu.residual, fu.residual_stride = r2.data_ptr(), r2.stride(0)
+    lib = L.load()
+    L.check("spectra_w4a16_gemv_fused", lib.spectra_w4a16_gemv_fused(ops.ptr(), x2.data_ptr(), ldx, x2.shape[0],
+                                                                      L.F16, ctypes.byref(fu), out2.data_ptr(),
+                                                                      out2.stride(0), _stream(x.device)))
+    return out

@@ -16,6 +16,8 @@ restatements of the same math:
 """
 import math
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -144,3 +146,79 @@ def test_greedy_next(hip, n):
     K.greedy_next(logits, token, hist, pos)
     assert int(token) == n // 3 == int(torch.argmax(logits))
     assert int(pos) == 4 and int(hist[4]) == n // 3 and int((hist == -1).sum()) == 9
+
+
+# ---------------------------------------------------------------------------
+# the GEMV with fused RMSNorm / SiLU-mul prologues and residual epilogue
+# ---------------------------------------------------------------------------
+from spectra_amd import compressor as C  # noqa: E402
+
+
+def _nf4_ops(n, k, had, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).half()
+    mask = torch.rand(n, k, device="cuda", generator=g) < 0.005
+    w = torch.where(mask, (torch.randn(n, k, device="cuda", generator=g) * 0.2).half(), w)
+    q = C.quantize_nf4(w, 64, 0, mask, True)
+    col, val = q.outliers()
+    ops = K.QWeightOperands(q.packed, q.absmax, None, k, codebook="nf4", group_size=64, hadamard_block=had,
+                            marlin_layout=True, outlier_idx=col, outlier_w=val,
+                            outlier_rowptr=q.rowptr if col is not None else None)
+    w_eff = K.w4_dequant(q.packed, q.absmax, None, out_dtype=torch.float32, codebook="nf4", marlin_layout=True,
+                         outlier_idx=col, outlier_w=val, outlier_rowptr=q.rowptr if col is not None else None)
+    return ops, w_eff.double().cpu()
+
+
+def _y_ref(x_eff, w_eff, had):
+    """fp64 FWHT(x) @ W_eff^T of one fp32/fp64 row (the library FWHT is bit-exact to the reference)."""
+    xr = K.fwht_rows(x_eff.float().reshape(1, -1).contiguous(), had, out_dtype=torch.float32) if had else x_eff
+    return (xr.double().cpu().reshape(1, -1) @ w_eff.T).reshape(-1)
+
+
+def _check(y, ref):
+    yv = y.double().cpu().reshape(-1)
+    ulp = torch.from_numpy(np.spacing(ref.abs().numpy().astype(np.float16)).astype(np.float64))
+    err = (yv - ref).abs()
+    assert bool((err <= torch.clamp(ulp, min=1e-2)).all()), float(err.max())
+    assert float((yv - ref).norm() / ref.norm()) <= 1e-3
+
+
+@pytest.mark.parametrize("n,k,had", [(640, 3072, 128), (16384, 3072, 128), (5000, 3072, 0), (512, 1024, 64)])
+def test_gemv_rmsnorm_prologue(hip, n, k, had):
+    case(n=n, k=k, had=had)
+    ops, w_eff = _nf4_ops(n, k, had, seed=n + k)
+    g = torch.Generator(device="cuda").manual_seed(k)
+    h = (torch.randn(1, k, device="cuda", generator=g) * 3).half()
+    nw = (torch.rand(k, device="cuda", generator=g) + 0.5).half()
+    y = K.w4a16_gemv_fused(ops, h, prologue="rmsnorm", norm_weight=nw, eps=1e-5)
+    hf = h.double()
+    x_eff = hf * torch.rsqrt(hf.pow(2).mean() + 1e-5) * nw.double()
+    _check(y, _y_ref(x_eff, w_eff, had))
+
+
+@pytest.mark.parametrize("n,k,had", [(3072, 8192, 128), (700, 2048, 128)])
+def test_gemv_silu_prologue_and_residual(hip, n, k, had):
+    case(n=n, k=k, had=had)
+    ops, w_eff = _nf4_ops(n, k, had, seed=n + 3 * k)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    gu = (torch.randn(1, 2 * k, device="cuda", generator=g) * 2).half()
+    act = K.silu_mul(gu)  # the prologue is bit-identical to the separate kernel
+    ref = _y_ref(act.float(), w_eff, had)
+    y = K.w4a16_gemv_fused(ops, gu, prologue="silu_mul")
+    _check(y, ref)
+    # residual epilogue, in place: h <- fp16(h + fp16(y)), bit-identical to the separate add
+    h = (torch.randn(1, n, device="cuda", generator=g) * 4).half()
+    h_sep = h + y
+    out = K.w4a16_gemv_fused(ops, gu, prologue="silu_mul", residual=h, out=h)
+    assert out.data_ptr() == h.data_ptr() and torch.equal(h, h_sep)
+
+
+def test_gemv_residual_without_prologue(hip):
+    case(n=1536, k=3072, had=128, m=3)
+    ops, w_eff = _nf4_ops(1536, 3072, 128, seed=9)
+    x = torch.randn(3, 3072, device="cuda", generator=torch.Generator(device="cuda").manual_seed(1)).half()
+    res = torch.randn(3, 1536, device="cuda", generator=torch.Generator(device="cuda").manual_seed(2)).half()
+    y = K.w4a16_gemv_fused(ops, x)  # plain
+    assert torch.equal(y, K.w4a16_linear(ops, x))
+    r = K.w4a16_gemv_fused(ops, x, residual=res)
+    assert torch.equal(r, res + y)
