@@ -193,6 +193,8 @@ def main():
                     help="only run the dominant kernel's timing loop (for rocprofv3 runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run plain device copies of COPY_BYTES each (PMC traffic calibration)")
+    ap.add_argument("--decode-e2e", action="store_true",
+                    help="only run the cfg5 end-to-end decode (for rocprofv3 runs); prints its JSON fields")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -206,6 +208,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.calibrate_copy:
         calibrate_copy(dev)
+        return
+    if args.decode_e2e:
+        print(json.dumps(decode_e2e(dev)), flush=True)
         return
 
     # ---- cfg2 operands
@@ -374,9 +379,16 @@ def secondary(lib, dev, pool_gb: float) -> dict:
     out["cfg5_decode_tok_s_linears_only"] = round(1.0 / t, 1)
     out["cfg5_note"] = "113 GEMVs of one decode token (28 layers + lm_head) in one graph; attention/norms excluded"
     del chain, keep, layer, head
-    # cfg5 end to end through the engine: random 512-token prompt, prefill, then greedy decode
-    # with one captured decode step replayed per token (all linears NF4 + FWHT-128 + 0.5% CSR)
+    out.update(decode_e2e(dev))
+    return out
+
+
+def decode_e2e(dev) -> dict:
+    """cfg5 end to end through the engine: random 512-token prompt, prefill, then 255 greedy
+    decode steps, one captured decode step replayed per token (all linears NF4 + FWHT-128 +
+    0.5% CSR outliers, fp16 KV cache)."""
     from spectra_amd.engine import DecoderConfig, SpectraDecoder
+    out = {}
     dec = SpectraDecoder(DecoderConfig(max_seq=768))
     prompt = torch.randint(0, dec.cfg.vocab, (512,), generator=torch.Generator().manual_seed(5)).to(dev)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
