@@ -215,6 +215,8 @@ struct GemmParams {
   int64_t ldo;
   int m, n, k;
   int gshift, marlin, okind, n_out, ow_dt, bias_dt, act_dt;
+  int ksplit, ksteps;  // K splits (blockIdx.z) and kBK-steps per split
+  float* part;         // ksplit > 1: fp32 partials [ksplit][m][n]
 };
 
 __device__ __forceinline__ uint16_t gm_code_bits(int fmt, int i) {
@@ -239,17 +241,20 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * kBM;
   const int wm = wave / WNW, wn = wave % WNW;
-  const int K = p.k, nk = K / kBK;
+  const int K = p.k;
+  // this workgroup's K range: steps [ks, ks + nk) of kBK
+  const int ks = blockIdx.z * p.ksteps;
+  const int nk = min(p.ksteps, K / kBK - ks);
   asm volatile("" ::"s"(p.a16), "s"(p.packed), "s"(p.ldp), "s"(p.scales), "s"(p.lds), "s"(p.m), "s"(p.n),
                "s"(p.k), "s"(p.gshift), "s"(p.marlin), "s"(p.okind), "s"(p.rowptr), "s"(p.fexp));
 
   // ---- operand assignment: A row tid / 2, 32 of its 64 bytes a step; weight row
   //      tid / TPR, bytes [(tid % TPR) * BPT, + BPT) of the row's 16-byte run ----
   const int ar = tid / (4 / AU), ah = tid % (4 / AU);  // row, and which AU-chunk part of its 64 bytes
-  const uint16_t* asrc = p.a16 + (int64_t)min(m0 + ar, p.m - 1) * K + 8 * AU * ah;
+  const uint16_t* asrc = p.a16 + (int64_t)min(m0 + ar, p.m - 1) * K + 8 * AU * ah + ks * kBK;
   const int wr = tid / TPR, wb0 = (tid % TPR) * BPT;
   const int wrow = min(n0 + wr, p.n - 1);
-  const uint8_t* wsrc = p.packed + (int64_t)wrow * p.ldp + wb0;
+  const uint8_t* wsrc = p.packed + (int64_t)wrow * p.ldp + wb0 + ks * 16;
   const uint16_t* ssrc = p.scales + (int64_t)wrow * p.lds;
   const uint8_t* zsrc = FMT == SPECTRA_FMT_ASYM_G32 ? p.zeros + (int64_t)wrow * p.ldz : nullptr;
 
@@ -260,6 +265,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
     cend = p.rowptr[wrow + 1];
   } else if (p.okind == SPECTRA_OUTLIERS_COLUMNS) {
     cend = p.n_out;
+  }
+  if (ks > 0 && p.okind != SPECTRA_OUTLIERS_NONE) {  // first entry at or past this split's K range
+    const int kfirst = ks * kBK;
+    int lo = cur, hi = cend;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      const int c = p.okind == SPECTRA_OUTLIERS_CSR ? p.ccol[mid] : (int)p.oidx[mid];
+      if (c < kfirst) lo = mid + 1;
+      else hi = mid;
+    }
+    cur = lo;
   }
   // the next kWin entries of the row in a register queue (q[0] = next); consuming one
   // shifts the queue and loads the entry kWin further, which is read kWin entries later
@@ -310,8 +326,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
     } else {
       gw.x = *(const uint32_t*)(wsrc + step * 16);
     }
-    gs = ssrc[(step * kBK) >> p.gshift];
-    if constexpr (FMT == SPECTRA_FMT_ASYM_G32) gz = zsrc[step];
+    gs = ssrc[((ks + step) * kBK) >> p.gshift];
+    if constexpr (FMT == SPECTRA_FMT_ASYM_G32) gz = zsrc[ks + step];
   };
 
   // ---- nibble-pair LUT: 64 wave-instructions of 1 KB (lane l reads bank l) ----
@@ -378,7 +394,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
     // step's end (ascending columns); the same thread wrote the decoded values above, so
     // program order suffices
     if (p.okind != SPECTRA_OUTLIERS_NONE) {
-      const int klo = step * kBK, khi = klo + kBK;
+      const int klo = (ks + step) * kBK, khi = klo + kBK;
       while (qc[0] < khi) {
         const int kk = qc[0] - klo;
         const int jb = p.marlin ? (kk & 15) : (kk >> 1), h = p.marlin ? (kk >> 4) : (kk & 1);
@@ -442,6 +458,24 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   if (kt < nk) mfma_step(0);  // odd step count: the last step sits in buffer 0
 
   // ---- epilogue: D[row][col], row = 8 (r / 4) + 4 (lane / 32) + r % 4, col = lane % 32 ----
+  if (p.ksplit > 1) {  // fp32 partials of this split (row exponent applied, no bias)
+    float* part = p.part + (int64_t)blockIdx.z * p.m * p.n;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int col = n0 + wn * WN + j * 32 + (lane & 31);
+      if (col >= p.n) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rl = wm * 128 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (m0 + rl < p.m)
+            part[(int64_t)(m0 + rl) * p.n + col] = acc[i][j][r] * __builtin_bit_cast(float, (uint32_t)(127 - fx[rl]) << 23);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
     const int col = n0 + wn * WN + j * 32 + (lane & 31);
@@ -461,7 +495,51 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   }
 }
 
+// out[r, c] = act(sum over splits of part[z][r][c] + bias[c]), splits summed in order
+constexpr int kRedThreads = 256;
+__global__ void __launch_bounds__(kRedThreads) splitk_reduce_kernel(const float* __restrict__ part, int ksplit, int m,
+                                                                     int n, const void* bias, int bias_dt, void* out,
+                                                                     int64_t ldo, int act_dt) {
+  const int64_t i = (int64_t)blockIdx.x * kRedThreads + threadIdx.x;  // 4 consecutive columns
+  const int64_t n4 = n >> 2;
+  if (i >= (int64_t)m * n4) return;
+  const int64_t r = i / n4, c = (i - r * n4) * 4;
+  const int64_t mn = (int64_t)m * n;
+  float4 a = *(const float4*)(part + r * n + c);
+  for (int z = 1; z < ksplit; ++z) {
+    const float4 b = *(const float4*)(part + z * mn + r * n + c);
+    a.x += b.x; a.y += b.y; a.z += b.z; a.w += b.w;
+  }
+  float v[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (bias) v[e] += load_elem(bias, c + e, bias_dt);
+    ((uint16_t*)out)[r * ldo + c + e] = from_f32_16(v[e], act_dt);
+  }
+}
+
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// tile plan: 256 x BN tiles (BN 256 when they fill the GPU), and K splits when even the
+// 128-wide tiles leave most CUs idle (each split >= 8 steps of 32; fp32 partials, a reduce)
+struct GemmPlan {
+  int BN, mt, nt, ksplit, ksteps;
+};
+static GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
+  GemmPlan g;
+  g.mt = (int)((m + kBM - 1) / kBM);
+  const bool wide = (int64_t)g.mt * ((n + 255) / 256) >= 256;
+  g.BN = wide ? 256 : 128;
+  g.nt = (int)((n + g.BN - 1) / g.BN);
+  const int tiles = g.mt * g.nt;
+  const int steps = (int)(k / kBK);
+  int ks = tiles < 128 && n % 4 == 0 ? 256 / tiles : 1;
+  ks = ks > 8 ? 8 : ks;
+  while (ks > 1 && steps / ks < 8) --ks;
+  g.ksteps = (steps + ks - 1) / ks;
+  g.ksplit = (steps + g.ksteps - 1) / g.ksteps;
+  return g;
+}
 
 // skinny.hip: the small-batch MFMA family (2 <= m <= 16)
 size_t skinny_workspace(const spectra_qweight_t* w, int64_t m);
@@ -475,7 +553,9 @@ using namespace spectra;
 extern "C" size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64_t m, int32_t act_dtype) {
   (void)act_dtype;
   if (w == nullptr || m <= 0) return 0;
-  const size_t gemm = align256((size_t)m * (size_t)w->k * 2) + align256((size_t)m * 4);
+  const GemmPlan g = plan_gemm(m, w->n, w->k);
+  const size_t gemm = align256((size_t)m * (size_t)w->k * 2) + align256((size_t)m * 4) +
+                      (g.ksplit > 1 ? align256((size_t)g.ksplit * m * w->n * 4) : 0);
   const size_t small = skinny_workspace(w, m);
   return gemm > small ? gemm : small;
 }
@@ -544,12 +624,14 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   p.okind = csr ? SPECTRA_OUTLIERS_CSR
                 : (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS ? SPECTRA_OUTLIERS_COLUMNS : SPECTRA_OUTLIERS_NONE);
   p.n_out = w->num_outliers; p.ow_dt = w->outlier_w_dtype; p.bias_dt = w->bias_dtype; p.act_dt = act_dtype;
-  // 256-wide tiles when they fill the GPU, otherwise 128-wide (twice the workgroups)
-  const int64_t mt = (m + kBM - 1) / kBM;
-  const bool wide = mt * ((w->n + 255) / 256) >= 256;
-  const int BN = wide ? 256 : 128;
+  const GemmPlan g = plan_gemm(m, w->n, w->k);
+  const bool wide = g.BN == 256;
+  const int BN = g.BN;
+  p.ksplit = g.ksplit;
+  p.ksteps = g.ksteps;
+  p.part = g.ksplit > 1 ? (float*)((uint8_t*)fexp + align256((size_t)m * 4)) : nullptr;
   const size_t lds = (size_t)kGLut + (size_t)2 * (kBM + BN) * kRowH * 2 + kBM * 4 + kGemmWaves * 16 * 2;
-  dim3 grid((unsigned)((w->n + BN - 1) / BN), (unsigned)mt);
+  dim3 grid((unsigned)g.nt, (unsigned)g.mt, (unsigned)g.ksplit);
   const void* kern;
   if (w->format == SPECTRA_FMT_NF4)
     kern = wide ? (const void*)gemm_kernel<SPECTRA_FMT_NF4, 256, kGemmWaves>
@@ -562,5 +644,12 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   void* kargs[] = {(void*)&p};
   SPECTRA_HIP_CHECK(hipLaunchKernel(kern, grid, dim3(64 * kGemmWaves), kargs, lds, s));
   SPECTRA_HIP_CHECK(hipGetLastError());
+  if (g.ksplit > 1) {
+    const int64_t work = m * (w->n / 4);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((work + kRedThreads - 1) / kRedThreads)),
+                       dim3(kRedThreads), 0, s, (const float*)p.part, g.ksplit, (int)m, (int)w->n, w->bias,
+                       w->bias_dtype, out, ldo, act_dtype);
+    SPECTRA_HIP_CHECK(hipGetLastError());
+  }
   return SPECTRA_OK;
 }

@@ -376,6 +376,31 @@ def test_dense_outlier_rows(hip):
         check_y(y, y_ref, torch.float16)
 
 
+@pytest.mark.parametrize("m", [40, 300])
+def test_gemm_split_k_outliers_across_splits(hip, m):
+    """Few output tiles -> the GEMM splits K (8 splits of 512 here); outlier runs that cross
+    split boundaries, a fully dense row and a bias must land in exactly one split each."""
+    case(m=m)
+    n, k = 256, 4096
+    rng = np.random.default_rng(m)
+    w = rand_np(rng, (n, k), 0.02)
+    mask = rng.random((n, k)) < 0.005
+    mask[3, 480:560] = True          # crosses the boundary at k = 512
+    mask[200, 1000:1100] = True      # crosses k = 1024
+    mask[77, :] = True               # every column
+    qq = O.nf4_quantize(w, "float16", 64, 0, mask, True)
+    w_eff = O.nf4_dequant(qq["packed"], qq["absmax"], True, "float16", qq["rowptr"], qq["col"], qq["val"])
+    x = rand_np(rng, (m, k), 1.0)
+    b = rand_np(rng, (n,), 0.5)
+    y_ref = O.linear_ref(x, "float16", w_eff, "float16", hadamard_block=128, bias=b)
+    lin = SpectraFusedLinear(k, n, 64, has_bias=True, codebook="nf4", hadamard_block=128).cuda()
+    lin.set_weights(cuda(qq["packed"]), cuda(qq["absmax"]), None, bias=cuda(b), outlier_idx=cuda(qq["col"]),
+                    outlier_weight=cuda(qq["val"]), marlin_layout=True, outlier_rowptr=cuda(qq["rowptr"]))
+    y = lin(cuda(x))
+    check_y(y, y_ref, torch.float16)
+    assert torch.equal(lin(cuda(x)), y)  # the split partials are summed in a fixed order
+
+
 # ---------------------------------------------------------------------------
 # BASELINE shapes (configs 1-3) at full size, M=1..16, against the oracle
 # ---------------------------------------------------------------------------
