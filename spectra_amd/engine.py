@@ -213,42 +213,39 @@ class SpectraDecoder(nn.Module):
     step is fully device-side (token, position and cache index live in device tensors), so
     it is captured once as a HIP graph and replayed per token (engine.py:1801-1860)."""
 
-    def __init__(self, cfg: DecoderConfig = DecoderConfig(), device: Optional[torch.device] = None):
+    def __init__(self, cfg: DecoderConfig = DecoderConfig(), device: Optional[torch.device] = None,
+                 weights: Optional[dict] = None):
+        """``weights`` (default: random init from ``cfg.seed``): ``layers`` = per layer
+        (qkv, o, gate_up, down) ``NF4Weight``s, ``embed`` (the gather's rows, no rotation),
+        ``lm_head`` (None = tied to ``embed``), ``norms`` = the 2 * layers + 1 RMSNorm weights."""
         super().__init__()
         dev = device or torch.device("cuda")
         self.cfg = cfg
         c = cfg
-        hd, kvd = c.head_dim, c.kv_heads * c.head_dim
-        gen = torch.Generator(device=dev).manual_seed(c.seed)
-        self.layers_q = []
+        hd = c.head_dim
+        if weights is None:
+            weights = self._random_weights(c, dev)
+        if len(weights["layers"]) != c.layers or len(weights["norms"]) != 2 * c.layers + 1:
+            raise ValueError("weights do not match the config's layer count")
 
-        def linear(n, k):
-            q = _synthetic_nf4(n, k, gen, c.hadamard_block, c.outlier_ratio, dev)
-            lin = SpectraFusedLinear(k, n, 64, codebook="nf4", hadamard_block=c.hadamard_block).to(dev)
+        def linear(q):
+            lin = SpectraFusedLinear(q.k, q.n, q.blocksize, codebook="nf4", hadamard_block=q.hadamard_block).to(dev)
             col, val = q.outliers()
-            lin.set_weights(q.packed, q.absmax, None, outlier_idx=col, outlier_weight=val, marlin_layout=True,
+            lin.set_weights(q.packed, q.absmax, None, outlier_idx=col, outlier_weight=val, marlin_layout=q.marlin_layout,
                             outlier_rowptr=q.rowptr if col is not None else None)
-            return lin, q
+            return lin
 
-        self.blocks = []
-        for _ in range(c.layers):
-            qkv, q1 = linear(c.hidden + 2 * kvd, c.hidden)
-            o, q2 = linear(c.hidden, c.hidden)
-            gu, q3 = linear(2 * c.inter, c.hidden)
-            down, q4 = linear(c.hidden, c.inter)
-            self.blocks.append(dict(qkv=qkv, o=o, gate_up=gu, down=down))
-            self.layers_q.append((q1, q2, q3, q4))
-        # tied embedding / lm_head: NF4 without rotation (the gather returns the stored rows)
-        qe = _synthetic_nf4(c.vocab, c.hidden, gen, 0, c.outlier_ratio, dev)
+        self.layers_q = [tuple(weights["layers"][i]) for i in range(c.layers)]
+        self.blocks = [dict(qkv=linear(a), o=linear(b), gate_up=linear(g), down=linear(d)) for a, b, g, d in self.layers_q]
+        qe = weights["embed"]
         self.embed_q = qe
         col, val = qe.outliers()
-        self.embed = SpectraFusedEmbedding(c.vocab, c.hidden, 64, True, codebook="nf4")
-        self.embed.set_weights(qe.packed, qe.absmax, None, col, val, True,
+        self.embed = SpectraFusedEmbedding(c.vocab, c.hidden, qe.blocksize, qe.marlin_layout, codebook="nf4")
+        self.embed.set_weights(qe.packed, qe.absmax, None, col, val, qe.marlin_layout,
                                outlier_rowptr=qe.rowptr if col is not None else None)
-        self.lm_head = SpectraFusedLinear(c.hidden, c.vocab, 64, codebook="nf4").to(dev)
-        self.lm_head.set_weights(qe.packed, qe.absmax, None, outlier_idx=col, outlier_weight=val, marlin_layout=True,
-                                 outlier_rowptr=qe.rowptr if col is not None else None)
-        self.norm_w = [torch.ones(c.hidden, device=dev, dtype=torch.float32) for _ in range(2 * c.layers + 1)]
+        self.lm_q = weights.get("lm_head") or qe
+        self.lm_head = linear(self.lm_q)
+        self.norm_w = [w.to(device=dev, dtype=torch.float32).contiguous() for w in weights["norms"]]
         self.norm_w16 = [w.half() for w in self.norm_w]  # the fused GEMV prologues read fp16 weights
         # KV cache [layer, kv, max_seq, head_dim]: a position's head is one 16-byte-aligned run
         self.k_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
@@ -265,6 +262,68 @@ class SpectraDecoder(nn.Module):
         self.graph: Optional[torch.cuda.CUDAGraph] = None
         self.graph_logits: Optional[torch.Tensor] = None
         self.device = dev
+
+    @staticmethod
+    def _random_weights(c: DecoderConfig, dev) -> dict:
+        gen = torch.Generator(device=dev).manual_seed(c.seed)
+        kvd = c.kv_heads * c.head_dim
+
+        def nf4(n, k, had):
+            return _synthetic_nf4(n, k, gen, had, c.outlier_ratio, dev)
+
+        layers = []
+        for _ in range(c.layers):
+            layers.append((nf4(c.hidden + 2 * kvd, c.hidden, c.hadamard_block), nf4(c.hidden, c.hidden, c.hadamard_block),
+                           nf4(2 * c.inter, c.hidden, c.hadamard_block), nf4(c.hidden, c.inter, c.hadamard_block)))
+        # tied embedding / lm_head: NF4 without rotation (the gather returns the stored rows)
+        embed = nf4(c.vocab, c.hidden, 0)
+        norms = [torch.ones(c.hidden, device=dev, dtype=torch.float32) for _ in range(2 * c.layers + 1)]
+        return dict(layers=layers, embed=embed, lm_head=None, norms=norms)
+
+    @classmethod
+    def from_trdc(cls, path, device: Optional[torch.device] = None, max_seq: int = 1024) -> "SpectraDecoder":
+        """A decoder on the Format B tensors of a TRDC container (engine.py:798-1080 binds a
+        container's tensors to the model's modules by name): HF Llama names, the separate
+        q/k/v and gate/up projections concatenated along N at load (exact: every Format B
+        operand is row-local), norms from the lossless tensors, lm_head tied to the
+        embedding when the container has none."""
+        from .container import TrdcReader, nf4_concat
+        dev = device or torch.device("cuda")
+        with TrdcReader(path) as rd:
+            cf = rd.config
+            c = DecoderConfig(layers=cf["num_hidden_layers"], hidden=cf["hidden_size"],
+                              heads=cf["num_attention_heads"],
+                              kv_heads=cf.get("num_key_value_heads") or cf["num_attention_heads"],
+                              inter=cf["intermediate_size"], vocab=cf["vocab_size"],
+                              rope_theta=float(cf.get("rope_theta") or 10000.0),
+                              rms_eps=float(cf.get("rms_norm_eps") or 1e-6), max_seq=max_seq)
+            if cf.get("head_dim") not in (None, c.head_dim):
+                raise ValueError(f"head_dim {cf.get('head_dim')} != hidden / heads ({c.head_dim})")
+
+            def nf4(name):
+                if name not in rd.tensors:
+                    raise ValueError(f"container has no tensor {name!r}")
+                if not rd.tensors[name]["type"].startswith("nf4_"):
+                    raise ValueError(f"{name!r} is {rd.tensors[name]['type']!r}: the decoder runs Format B tensors")
+                return rd.load(name, dev)
+
+            def vec(name):
+                return rd.load(name, dev).float()
+
+            layers, norms = [], []
+            for i in range(c.layers):
+                p = f"model.layers.{i}."
+                a = p + "self_attn."
+                m = p + "mlp."
+                layers.append((nf4_concat([nf4(a + "q_proj.weight"), nf4(a + "k_proj.weight"), nf4(a + "v_proj.weight")]),
+                               nf4(a + "o_proj.weight"),
+                               nf4_concat([nf4(m + "gate_proj.weight"), nf4(m + "up_proj.weight")]),
+                               nf4(m + "down_proj.weight")))
+                norms += [vec(p + "input_layernorm.weight"), vec(p + "post_attention_layernorm.weight")]
+            norms.append(vec("model.norm.weight"))
+            embed = nf4("model.embed_tokens.weight")
+            head = nf4("lm_head.weight") if "lm_head.weight" in rd.tensors else None
+        return cls(c, dev, dict(layers=layers, embed=embed, lm_head=head, norms=norms))
 
     # -- building blocks ---------------------------------------------------------------------
     def _layer(self, li: int, h: torch.Tensor, delta: Optional[torch.Tensor], pos: torch.Tensor,

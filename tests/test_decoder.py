@@ -84,7 +84,10 @@ class RefDecoder:
     def __init__(self, dec: SpectraDecoder):
         self.c = dec.cfg
         self.w = [[_w_eff(q) for q in layer] for layer in dec.layers_q]
+        self.had = [[q.hadamard_block for q in layer] for layer in dec.layers_q]
         self.emb = _w_eff(dec.embed_q)
+        self.head = _w_eff(dec.lm_q)
+        self.norm = [w.float() for w in dec.norm_w]
         hd = self.c.head_dim
         inv = 1.0 / (self.c.rope_theta ** (torch.arange(0, hd, 2, device="cuda", dtype=torch.float32) / hd))
         ang = torch.arange(self.c.max_seq, device="cuda", dtype=torch.float32)[:, None] * inv[None, :]
@@ -95,8 +98,8 @@ class RefDecoder:
         xr = K.fwht_rows(x.contiguous(), had, out_dtype=torch.float32) if had else x
         return xr @ w.T
 
-    def rms(self, x):
-        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.c.rms_eps)
+    def rms(self, x, i):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.c.rms_eps) * self.norm[i]
 
     def rope(self, x, pos):
         h2 = x.shape[-1] // 2
@@ -105,13 +108,14 @@ class RefDecoder:
         return torch.cat([a * c - b * s, b * c + a * s], dim=-1)
 
     def forward(self, ids, pos0):
-        c, hd, had = self.c, self.c.head_dim, self.c.hadamard_block
+        c, hd = self.c, self.c.head_dim
         T = ids.numel()
         pos = torch.arange(pos0, pos0 + T, device="cuda")
         h = self.emb[ids]
         for li, (wqkv, wo, wgu, wd) in enumerate(self.w):
-            x = self.rms(h)
-            qkv = self.lin(x, wqkv, had)
+            hq, ho, hg, hdn = self.had[li]
+            x = self.rms(h, 2 * li)
+            qkv = self.lin(x, wqkv, hq)
             q = qkv[:, : c.hidden].reshape(T, c.heads, hd)
             k = qkv[:, c.hidden: c.hidden + c.kv_heads * hd].reshape(T, c.kv_heads, hd)
             v = qkv[:, c.hidden + c.kv_heads * hd:].reshape(T, c.kv_heads, hd)
@@ -131,11 +135,11 @@ class RefDecoder:
             s = s.masked_fill(mask[None], float("-inf"))
             a = torch.matmul(torch.softmax(s, -1), vv.permute(1, 0, 2).contiguous())  # [heads, T, hd]
             a = a.permute(1, 0, 2).reshape(T, c.hidden)
-            h = h + self.lin(a, wo, had)
-            x = self.rms(h)
-            gu = self.lin(x, wgu, had)
-            h = h + self.lin(torch.nn.functional.silu(gu[:, : c.inter]) * gu[:, c.inter:], wd, had)
-        return self.rms(h[-1:]) @ self.emb.T
+            h = h + self.lin(a, wo, ho)
+            x = self.rms(h, 2 * li + 1)
+            gu = self.lin(x, wgu, hg)
+            h = h + self.lin(torch.nn.functional.silu(gu[:, : c.inter]) * gu[:, c.inter:], wd, hdn)
+        return self.rms(h[-1:], 2 * c.layers) @ self.head.T
 
 
 def test_decoder_against_fp32_reference(hip):
