@@ -386,15 +386,25 @@ def secondary(lib, dev, pool_gb: float) -> dict:
 def decode_e2e(dev) -> dict:
     """cfg5 end to end through the engine: random 512-token prompt, prefill, then 255 greedy
     decode steps, one captured decode step replayed per token (all linears NF4 + FWHT-128 +
-    0.5% CSR outliers, fp16 KV cache)."""
+    0.5% CSR outliers, fp16 KV cache); then the same with the 4-bit KV cache
+    (kv_bits=4, 128-position fp16 window)."""
+    out = _decode_run(dev, 16)
+    q4 = _decode_run(dev, 4)
+    out["cfg5_kv4_decode_ms_per_token"] = q4["cfg5_decode_ms_per_token"]
+    out["cfg5_kv4_decode_tok_s"] = q4["cfg5_decode_tok_s"]
+    out["cfg5_kv4_note"] = "same run with the 4-bit KV cache: positions older than 128 read through the 4-bit codes"
+    return out
+
+
+def _decode_run(dev, kv_bits: int) -> dict:
     from spectra_amd.engine import DecoderConfig, SpectraDecoder
     out = {}
-    dec = SpectraDecoder(DecoderConfig(max_seq=768))
+    dec = SpectraDecoder(DecoderConfig(max_seq=768, kv_bits=kv_bits))
     prompt = torch.randint(0, dec.cfg.vocab, (512,), generator=torch.Generator().manual_seed(5)).to(dev)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     dec.prefill(prompt)  # first call: library set-up
-    dec.k_cache.zero_()
-    dec.v_cache.zero_()
+    for t in dec.cache_tensors():
+        t.zero_()
     ev[0].record()
     dec.prefill(prompt)
     ev[1].record()
@@ -409,6 +419,8 @@ def decode_e2e(dev) -> dict:
     out["cfg5_decode_tok_s"] = round(255 / dms * 1e3, 1)
     out["cfg5_e2e_note"] = ("28-layer Llama-3.2-3B-shaped decoder (random init) through spectra_amd.engine: 512-token "
                             "prompt, 256 greedy tokens, fp16 KV cache, decode step replayed as one HIP graph")
+    del dec
+    torch.cuda.empty_cache()
     return out
 
 

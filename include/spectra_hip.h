@@ -25,6 +25,8 @@
  *                              static-cache attention of the decode step (engine.py:1240-1250,
  *                              :1387-1415)
  *   spectra_greedy_next     <- spectra/engine.py:1690-1697 sample_token (temperature 0)
+ *   spectra_kv4_quantize, spectra_kv4_dequantize, spectra_attend_decode_q4
+ *                           <- spectra/engine.py:614-700 the 4-bit KV cache
  */
 #ifndef SPECTRA_HIP_H_
 #define SPECTRA_HIP_H_
@@ -255,6 +257,31 @@ size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq
 int spectra_attend_decode(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t, int32_t heads,
                           int32_t kv_heads, int32_t head_dim, int32_t max_seq, void* k_cache, void* v_cache,
                           void* workspace, size_t workspace_bytes, void* out, spectra_stream_t stream);
+
+/* The 4-bit KV cache (engine.py:614-680 SpectraGroup32QuantizedLayer / :683-700
+ * SpectraQuantizedCache).  Quantizer: per row of the head dimension, groups of 32,
+ * asymmetric min-max codes 0..15 with fp16 scale and uint8 zero point, two codes per byte
+ * (even index low nibble), bit-identical to the reference's _quantize on fp16 values (whose
+ * 1e-8 threshold and scale floor are 0 in fp16: a constant group gets scale 0).  Dequant:
+ * (q - z) * s rounded to bf16, the reference's _dequantize.
+ * spectra_kv4_quantize: x fp16 rows of d values, row r of head h at x + h * x_head_stride +
+ * r * ldx; outputs at row h * out_head_rows + r: codes uint8 [*, d/2], scales fp16
+ * [*, d/32], zeros uint8 [*, d/32].  spectra_kv4_dequantize: bf16 [rows, d].
+ * spectra_attend_decode_q4: spectra_attend_decode over a 4-bit cache: every position in
+ * codes / scales / zeros [kv_heads, max_seq, ...] (the new token quantized as it is
+ * appended), the last `window` positions also in fp16 rings k_window / v_window
+ * [kv_heads, window, head_dim] (slot = position % window), which attention reads for them
+ * (the reference keeps a recent window unquantized); older positions are read through the
+ * dequant.  RoPE tables required. */
+int spectra_kv4_quantize(const void* x, int64_t ldx, int64_t rows, int32_t heads, int64_t x_head_stride, int32_t d,
+                         void* codes, void* scales, void* zeros, int64_t out_head_rows, spectra_stream_t stream);
+int spectra_kv4_dequantize(const void* codes, const void* scales, const void* zeros, int64_t rows, int32_t d,
+                           void* out_bf16, spectra_stream_t stream);
+int spectra_attend_decode_q4(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t,
+                             int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq, int32_t window,
+                             void* k_window, void* v_window, void* k_codes, void* v_codes, void* k_scales,
+                             void* v_scales, void* k_zeros, void* v_zeros, void* workspace, size_t workspace_bytes,
+                             void* out, spectra_stream_t stream);
 
 /* act [rows, inter] = fp16(silu(g) * u) where g = gate_up[:, :inter], u = gate_up[:, inter:]
  * (row stride ldgu >= 2 * inter). */

@@ -34,7 +34,8 @@ __all__ = [
     "fwht", "rotate_blocks",
     "quantize_group32", "pack_nibbles", "unpack_nibbles", "pack_zeros", "unpack_zeros",
     "dequant_group32", "apply_outlier_columns", "compute_group32_quant",
-    "nf4_quantize", "nf4_dequant", "nearest_code", "csr_from_mask", "linear_ref", "format_a_linear_ref", "select_outlier_columns"]
+    "nf4_quantize", "nf4_dequant", "nearest_code", "csr_from_mask", "linear_ref", "format_a_linear_ref", "select_outlier_columns",
+    "kv4_quantize", "kv4_dequantize"]
 
 # compressor.py:22-27 -- the 16 NF4 levels as float32 literals (index 7 is 0.0).
 NF4_CODEBOOK = np.array([
@@ -391,3 +392,64 @@ def select_outlier_columns(w: np.ndarray, w_dtype: str = "float16", norm: Option
     n_out = min(k, max(1, int(round(k * ratio))))
     order = np.lexsort((np.arange(k), -sal))  # descending saliency, lowest column first on ties
     return np.sort(order[:n_out]).astype(np.int32), ratio, kurt
+
+
+# ----------------------------------------------------------------------------
+# 4-bit KV cache -- engine.py:614-680 (SpectraGroup32QuantizedLayer)
+# ----------------------------------------------------------------------------
+def _rt(x32: np.ndarray, dtype: str) -> np.ndarray:
+    """float32 -> ``dtype`` -> float32 (one rounding, RNE)."""
+    return to_f32(round_to(x32, dtype), dtype)
+
+
+def _to_u8(x32: np.ndarray) -> np.ndarray:
+    """torch's float -> uint8 conversion of in-range values (the reference clamps to
+    [0, 15] first); NaN becomes 0."""
+    x = np.where(np.isnan(x32), 0.0, x32)
+    return x.astype(np.int64).astype(np.uint8)
+
+
+def kv4_quantize(x: np.ndarray, dtype: str, group: int = 32):
+    """``_quantize`` (engine.py:624-656) for rows of a ``dtype`` tensor [rows, D], D % 32 == 0.
+
+    Every torch op of the reference is restated with its rounding: tensor - tensor and
+    tensor / scalar round to ``dtype``; the Python scalars 1e-8 and 15.0 meet the tensor in
+    ``dtype`` (so for float16 the constant-group threshold and the scale floor are 0: a
+    constant group gets scale 0 and dequantizes to 0, the reference's float16 behaviour);
+    ``zeros.float() * scales`` promotes to float32, so the code computation
+    ``round((t + z * s) / s)`` runs in float32 (round half to even); clamps to [0, 15]; a
+    NaN code or zero point converts to 0.  Returns (packed uint8 [rows, D/32, 16], scales
+    float16 [rows, D/32, 1], zeros uint8 [rows, D/32, 1]).
+    """
+    t = to_f32(x, dtype).reshape(x.shape[0], -1, group)                # [rows, groups, 32]
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        tmin = t.min(axis=-1, keepdims=True)
+        tmax = t.max(axis=-1, keepdims=True)
+        diff = _rt(tmax - tmin, dtype)
+        eps = to_f32(round_to(np.float32(1e-8), dtype), dtype)           # 0 for float16
+        const = diff < eps
+        s_const = np.where(tmin == 0, np.float32(1.0), np.abs(tmin))
+        scales = np.where(const, s_const, _rt(diff / np.float32(15.0), dtype))
+        scales = np.maximum(scales, eps)
+        z_free = np.clip(np.round(_rt(-tmin / scales, dtype)), 0.0, 15.0)
+        z_free = np.where(np.isnan(_rt(-tmin / scales, dtype)), np.nan, z_free)
+        zeros = np.where(const, np.where(tmin < 0, 1.0, 0.0), z_free)
+        zeros_u8 = _to_u8(zeros.astype(np.float32))
+        zf = zeros_u8.astype(np.float32)
+        q_free = (t + zf * scales) / scales
+        q_free = np.where(np.isnan(q_free), np.nan, np.clip(np.round(q_free), 0.0, 15.0))
+        q = np.where(const, np.where(tmin > 0, 1.0, 0.0) * np.ones_like(t), q_free)
+        q_u8 = _to_u8(q.astype(np.float32))
+    packed = (q_u8[..., 0::2] | (q_u8[..., 1::2] << 4)).astype(np.uint8)
+    s16 = scales.astype(np.float16) if dtype == "float16" else to_f32(round_to(scales, dtype), dtype).astype(np.float16)
+    return packed, s16, zeros_u8
+
+
+def kv4_dequantize(packed: np.ndarray, scales: np.ndarray, zeros: np.ndarray) -> np.ndarray:
+    """``_dequantize`` (engine.py:658-672): (q - z) * s in float32, returned as bfloat16 bits
+    [rows, D]."""
+    q = np.empty(packed.shape[:-1] + (packed.shape[-1] * 2,), dtype=np.uint8)
+    q[..., 0::2] = packed & 0x0F
+    q[..., 1::2] = packed >> 4
+    deq = (q.astype(np.float32) - zeros.astype(np.float32)) * scales.astype(np.float32)
+    return f32_to_bf16_bits(deq.reshape(packed.shape[0], -1))

@@ -82,6 +82,11 @@ SIGNATURES = {
                                         c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spectra_silu_mul": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "spectra_greedy_next": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "spectra_kv4_quantize": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int64, c_int32, c_void_p, c_void_p,
+                                       c_void_p, c_int64, c_void_p]),
+    "spectra_kv4_dequantize": (c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
+    "spectra_attend_decode_q4": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
+                                           c_int32] + [c_void_p] * 8 + [c_void_p, c_size_t, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -167,6 +167,63 @@ __device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
   }
 }
 
+// KV cache of one layer.  fp16: k / v [kv][L][hd].  4-bit (Q4): every position quantized in
+// kq / vq (two codes per byte, [kv][L][hd/2]), ks / vs (fp16 scales) and kz / vz (zero
+// points) [kv][L][hd/32], and the last `window` positions also kept in fp16 in k / v, a ring
+// [kv][window][hd] indexed by position % window.
+struct KvCache {
+  uint16_t* k;
+  uint16_t* v;
+  uint8_t* kq;
+  uint8_t* vq;
+  uint16_t* ks;
+  uint16_t* vs;
+  uint8_t* kz;
+  uint8_t* vz;
+  int lmax, window;
+};
+
+// The reference's 4-bit KV quantizer (engine.py:624-656) on fp16 values, for the 8 values
+// of one lane; the 32-value group is 4 consecutive lanes.  Each torch op rounds where the
+// reference's does: range and scale to fp16 (range / 15), zero point fp16(-min / scale)
+// rounded half to even and clamped to [0, 15], codes round((t + z * s) / s) in fp32 clamped
+// to [0, 15]; in fp16 the reference's 1e-8 threshold and scale floor are 0, so a constant
+// group has scale 0 (its codes and zero point come from inf / NaN: NaN -> 0, +inf -> 15).
+__device__ __forceinline__ void kv4_quant_chunk(const uint4& x, uint32_t& packed, uint16_t& sbits, uint8_t& zero) {
+  float f[8];
+  unpack8(x, f);
+  float mn = f[0], mx = f[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) {
+    mn = fminf(mn, f[e]);
+    mx = fmaxf(mx, f[e]);
+  }
+  mn = fminf(mn, __shfl_xor(mn, 1, 64));
+  mn = fminf(mn, __shfl_xor(mn, 2, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+  const float diff = h2f(f2h(mx - mn));
+  const float sc = h2f(f2h(diff / 15.0f));
+  const float zq = h2f(f2h(-mn / sc));
+  const float zf = fminf(fmaxf(rintf(zq), 0.0f), 15.0f);  // NaN -> 0 (fmaxf returns the number)
+  uint32_t pk = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float qv = fminf(fmaxf(rintf((f[e] + zf * sc) / sc), 0.0f), 15.0f);
+    pk |= (uint32_t)qv << (4 * e);
+  }
+  packed = pk;
+  sbits = f2h(sc);
+  zero = (uint8_t)zf;
+}
+
+// (q - z) * s in fp32 rounded to bf16 (the reference's dequantized cache dtype), as fp32
+__device__ __forceinline__ void kv4_dequant_chunk(uint32_t packed, uint32_t sz, float (&f)[8]) {
+  const float s = h2f((uint16_t)sz), z = (float)(sz >> 16);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = bf2f(f2bf(((float)((packed >> (4 * e)) & 15u) - z) * s));
+}
+
 // Rotation of the 8-dim chunk `own` of a head whose partner chunk (dims -+ head_dim/2) is
 // `partner`, with the cos/sin of the chunk's pair indices: the lower half takes
 // a*c - b*s, the upper half b*c + a*s (a = dim i, b = dim i + head_dim/2), each product and
@@ -201,15 +258,14 @@ __device__ __forceinline__ uint4 rope_chunk(const uint4& own, const uint4& partn
 //     to part [heads][nspan][hd + 2] (fp32), which combine_kernel merges.  (Merging in the
 //     last workgroup to finish needs device-scope fences, which write back the L2 of
 //     every XCD and cost more than the second launch.)
-template <int G, int HD, bool ROPE>
+template <int G, int HD, bool ROPE, bool Q4>
 __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __restrict__ qkv,
                                                               const int64_t* __restrict__ pos_p,
                                                               const float* __restrict__ cos_t,
                                                               const float* __restrict__ sin_t, int heads,
-                                                              int kv_heads, int lmax, float scale,
-                                                              uint16_t* __restrict__ k_cache,
-                                                              uint16_t* __restrict__ v_cache,
+                                                              int kv_heads, float scale, const KvCache kvc,
                                                               float* __restrict__ part) {
+  const int lmax = kvc.lmax;
   constexpr int DG = HD / 8;               // lanes per position
   constexpr int PPW = kDecThreads / DG;    // positions per pass
   constexpr int NP = kSpanMax / PPW;       // passes
@@ -259,31 +315,62 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
     cs[0] = c0.x; cs[1] = c0.y; cs[2] = c0.z; cs[3] = c0.w; cs[4] = c1.x; cs[5] = c1.y; cs[6] = c1.z; cs[7] = c1.w;
     sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
   }
-  const uint16_t* kc = k_cache + ((int64_t)kh * lmax + t0) * HD + dg * 8;
-  const uint16_t* vc = v_cache + ((int64_t)kh * lmax + t0) * HD + dg * 8;
+  // fp16 rows of position t: the cache itself, or (Q4) the window ring
+  const int W = Q4 ? kvc.window : lmax;
+  auto row16 = [&](const uint16_t* base, int64_t t) __attribute__((always_inline)) {
+    return base + ((int64_t)kh * W + (Q4 ? t % W : t)) * HD + dg * 8;
+  };
   uint4 kr[NP], vr[NP];
+  uint32_t inwin = 0;  // Q4: bit i = pass i's position is in the fp16 window
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int tl = pr + i * PPW;
-    kr[i] = *(const uint4*)(kc + (int64_t)(tl < n ? tl : 0) * HD);  // past the end: re-read (in bounds)
-  }
-#pragma unroll
-  for (int i = 0; i < NP; ++i) {
-    const int tl = pr + i * PPW;
-    vr[i] = *(const uint4*)(vc + (int64_t)(tl < n ? tl : 0) * HD);
+    const int64_t t = t0 + (tl < n ? tl : 0);  // past the end: re-read the first (in bounds)
+    if (!Q4 || t > pos - W) {
+      if (Q4) inwin |= 1u << i;
+      kr[i] = *(const uint4*)row16(kvc.k, t);
+      vr[i] = *(const uint4*)row16(kvc.v, t);
+    } else {
+      const int64_t r = (int64_t)kh * lmax + t;
+      const int64_t sg = r * (HD / 32) + dg / 4;
+      kr[i] = make_uint4(*(const uint32_t*)(kvc.kq + r * (HD / 2) + dg * 4),
+                         (uint32_t)kvc.ks[sg] | ((uint32_t)kvc.kz[sg] << 16), 0, 0);
+      vr[i] = make_uint4(*(const uint32_t*)(kvc.vq + r * (HD / 2) + dg * 4),
+                         (uint32_t)kvc.vs[sg] | ((uint32_t)kvc.vz[sg] << 16), 0, 0);
+    }
   }
   // ---- the new token: rotate, append, and take it from registers
   if (mine) {
     const uint4 knew = ROPE ? rope_chunk(ko, kp, cs, sn, upper) : ko;
+    if constexpr (Q4) {  // every position is quantized as it is appended (all lanes: the group's lanes meet)
+      uint32_t kpk, vpk;
+      uint16_t ksb, vsb;
+      uint8_t kzb, vzb;
+      kv4_quant_chunk(knew, kpk, ksb, kzb);
+      kv4_quant_chunk(vo, vpk, vsb, vzb);
+      if (pr == tnew % PPW) {
+        const int64_t r = (int64_t)kh * lmax + pos;
+        *(uint32_t*)(kvc.kq + r * (HD / 2) + dg * 4) = kpk;
+        *(uint32_t*)(kvc.vq + r * (HD / 2) + dg * 4) = vpk;
+        if ((dg & 3) == 0) {
+          const int64_t sg = r * (HD / 32) + dg / 4;
+          kvc.ks[sg] = ksb;
+          kvc.vs[sg] = vsb;
+          kvc.kz[sg] = kzb;
+          kvc.vz[sg] = vzb;
+        }
+      }
+    }
     if (pr == tnew % PPW) {
-      *(uint4*)(kc + (int64_t)tnew * HD) = knew;
-      *(uint4*)(vc + (int64_t)tnew * HD) = vo;
+      *(uint4*)row16(kvc.k, pos) = knew;
+      *(uint4*)row16(kvc.v, pos) = vo;
     }
 #pragma unroll
     for (int i = 0; i < NP; ++i)
       if (pr + i * PPW == tnew) {
         kr[i] = knew;
         vr[i] = vo;
+        if (Q4) inwin |= 1u << i;
       }
   }
   // ---- scores
@@ -293,7 +380,8 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     float kf[8];
-    unpack8(kr[i], kf);
+    if (!Q4 || ((inwin >> i) & 1)) unpack8(kr[i], kf);
+    else kv4_dequant_chunk(kr[i].x, kr[i].y, kf);
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       float d = 0.0f;
@@ -329,7 +417,8 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     float vf[8];
-    unpack8(vr[i], vf);
+    if (!Q4 || ((inwin >> i) & 1)) unpack8(vr[i], vf);
+    else kv4_dequant_chunk(vr[i].x, vr[i].y, vf);
 #pragma unroll
     for (int j = 0; j < G; ++j) {
       const float pw = sc[j][pr + i * PPW];  // 0 past the end
@@ -394,6 +483,50 @@ __global__ void combine_kernel(const float* __restrict__ part, int nspan, int hd
     m = mb;
   }
   out[h * hd + d] = f2h(a / l);
+}
+
+// grid (ceil(rows * d / 8 / 256), heads): one lane per 8 values (groups of 32 = 4 lanes)
+__global__ void __launch_bounds__(kDecThreads) kv4_quantize_kernel(const uint16_t* __restrict__ x, int64_t ldx,
+                                                                    int64_t xhs, int64_t rows, int d,
+                                                                    int64_t out_rows, uint8_t* __restrict__ packed,
+                                                                    uint16_t* __restrict__ scales,
+                                                                    uint8_t* __restrict__ zeros) {
+  const int64_t gid = (int64_t)blockIdx.x * kDecThreads + threadIdx.x;
+  const int cpr = d >> 3;  // chunks per row (a multiple of 4: groups never straddle lanes of two rows)
+  const int64_t r = gid / cpr;
+  const int c = (int)(gid - r * cpr);
+  if (r >= rows) return;  // whole groups of 4 lanes leave together
+  const int h = blockIdx.y;
+  const uint4 v = *(const uint4*)(x + h * xhs + r * ldx + c * 8);
+  uint32_t pk;
+  uint16_t sb;
+  uint8_t zb;
+  kv4_quant_chunk(v, pk, sb, zb);
+  const int64_t orow = (int64_t)h * out_rows + r;
+  *(uint32_t*)(packed + orow * (d / 2) + c * 4) = pk;
+  if ((c & 3) == 0) {
+    scales[orow * (d / 32) + c / 4] = sb;
+    zeros[orow * (d / 32) + c / 4] = zb;
+  }
+}
+
+// the reference's dequantized values: bf16 [rows, d]
+__global__ void __launch_bounds__(kDecThreads) kv4_dequantize_kernel(const uint8_t* __restrict__ packed,
+                                                                      const uint16_t* __restrict__ scales,
+                                                                      const uint8_t* __restrict__ zeros, int64_t rows,
+                                                                      int d, uint16_t* __restrict__ out) {
+  const int64_t gid = (int64_t)blockIdx.x * kDecThreads + threadIdx.x;
+  const int cpr = d >> 3;
+  const int64_t r = gid / cpr;
+  const int c = (int)(gid - r * cpr);
+  if (r >= rows) return;
+  const int64_t sg = r * (d / 32) + c / 4;
+  float f[8];
+  kv4_dequant_chunk(*(const uint32_t*)(packed + r * (d / 2) + c * 4), (uint32_t)scales[sg] | ((uint32_t)zeros[sg] << 16), f);
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = (uint32_t)f2bf(f[2 * e]) | ((uint32_t)f2bf(f[2 * e + 1]) << 16);
+  *(uint4*)(out + r * d + c * 8) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 __global__ void __launch_bounds__(kDecThreads) silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t ldgu,
@@ -524,54 +657,130 @@ extern "C" size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int3
   return (size_t)heads * spectra_attend_spans(max_seq) * (head_dim + 2) * sizeof(float);
 }
 
-typedef void (*attend_fn)(const uint16_t*, const int64_t*, const float*, const float*, int, int, int, float, uint16_t*,
-                          uint16_t*, float*);
+typedef void (*attend_fn)(const uint16_t*, const int64_t*, const float*, const float*, int, int, float, const KvCache,
+                          float*);
 
-template <int HD, bool ROPE>
+template <int HD, bool ROPE, bool Q4>
 static attend_fn pick_attend(int g) {
   switch (g) {
-    case 1: return attend_kernel<1, HD, ROPE>;
-    case 2: return attend_kernel<2, HD, ROPE>;
-    case 3: return attend_kernel<3, HD, ROPE>;
-    case 4: return attend_kernel<4, HD, ROPE>;
-    case 6: return attend_kernel<6, HD, ROPE>;
-    case 8: return attend_kernel<8, HD, ROPE>;
+    case 1: return attend_kernel<1, HD, ROPE, Q4>;
+    case 2: return attend_kernel<2, HD, ROPE, Q4>;
+    case 3: return attend_kernel<3, HD, ROPE, Q4>;
+    case 4: return attend_kernel<4, HD, ROPE, Q4>;
+    case 6: return attend_kernel<6, HD, ROPE, Q4>;
+    case 8: return attend_kernel<8, HD, ROPE, Q4>;
     default: return nullptr;
   }
 }
 
-template <bool ROPE>
+template <bool ROPE, bool Q4>
 static attend_fn pick_attend_hd(int hd, int g) {
-  return hd == 64 ? pick_attend<64, ROPE>(g) : hd == 128 ? pick_attend<128, ROPE>(g) : pick_attend<256, ROPE>(g);
+  return hd == 64 ? pick_attend<64, ROPE, Q4>(g) : hd == 128 ? pick_attend<128, ROPE, Q4>(g)
+                                                             : pick_attend<256, ROPE, Q4>(g);
+}
+
+static int attend_launch(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t, int32_t heads,
+                         int32_t kv_heads, int32_t head_dim, const KvCache& kvc, bool q4, void* workspace,
+                         size_t workspace_bytes, void* out, spectra_stream_t stream) {
+  SPECTRA_REQUIRE(qkv && pos && kvc.k && kvc.v && out, "NULL pointer");
+  SPECTRA_REQUIRE((cos_t == nullptr) == (sin_t == nullptr), "cos and sin must both be given or both be NULL");
+  SPECTRA_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
+  SPECTRA_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim must be 64, 128 or 256");
+  SPECTRA_REQUIRE(kvc.lmax >= 1 && kvc.lmax <= (1 << 20), "bad max_seq");
+  SPECTRA_REQUIRE(aligned16(qkv) && aligned16(kvc.k) && aligned16(kvc.v) &&
+                      (cos_t == nullptr || (aligned16(cos_t) && aligned16(sin_t))),
+                  "qkv, the caches and the cos / sin tables must be 16-byte aligned");
+  if (q4) {
+    SPECTRA_REQUIRE(kvc.kq && kvc.vq && kvc.ks && kvc.vs && kvc.kz && kvc.vz, "NULL 4-bit cache pointer");
+    SPECTRA_REQUIRE(kvc.window >= 1 && kvc.window <= kvc.lmax, "window must be in [1, max_seq]");
+    SPECTRA_REQUIRE((reinterpret_cast<uintptr_t>(kvc.kq) & 3) == 0 && (reinterpret_cast<uintptr_t>(kvc.vq) & 3) == 0 &&
+                        (reinterpret_cast<uintptr_t>(kvc.ks) & 1) == 0 && (reinterpret_cast<uintptr_t>(kvc.vs) & 1) == 0,
+                    "4-bit codes must be 4-byte and scales 2-byte aligned");
+  }
+  if (workspace == nullptr || workspace_bytes < spectra_attend_workspace(heads, head_dim, kvc.lmax) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 15))
+    return fail(SPECTRA_ERR_WORKSPACE, "workspace missing, unaligned or smaller than spectra_attend_workspace()");
+  const int g = heads / kv_heads;
+  attend_fn fn;
+  if (q4) fn = cos_t ? pick_attend_hd<true, true>(head_dim, g) : nullptr;
+  else fn = cos_t ? pick_attend_hd<true, false>(head_dim, g) : pick_attend_hd<false, false>(head_dim, g);
+  if (fn == nullptr)
+    return fail(SPECTRA_ERR_UNSUPPORTED, "decode attention serves 1, 2, 3, 4, 6 or 8 query heads per KV head "
+                                         "(the 4-bit cache with RoPE)");
+  const int nspan = spectra_attend_spans(kvc.lmax);
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  float* part = (float*)workspace;
+  const hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(fn, dim3((unsigned)kv_heads, (unsigned)nspan), dim3(kDecThreads), 0, s, (const uint16_t*)qkv,
+                     pos, cos_t, sin_t, heads, kv_heads, scale, kvc, part);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)heads), dim3((unsigned)head_dim), 0, s, part, nspan, head_dim,
+                     (uint16_t*)out);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
 }
 
 extern "C" int spectra_attend_decode(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t,
                                      int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq,
                                      void* k_cache, void* v_cache, void* workspace, size_t workspace_bytes, void* out,
                                      spectra_stream_t stream) {
-  SPECTRA_REQUIRE(qkv && pos && k_cache && v_cache && out, "NULL pointer");
-  SPECTRA_REQUIRE((cos_t == nullptr) == (sin_t == nullptr), "cos and sin must both be given or both be NULL");
-  SPECTRA_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
-  SPECTRA_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim must be 64, 128 or 256");
-  SPECTRA_REQUIRE(max_seq >= 1 && max_seq <= (1 << 20), "bad max_seq");
-  SPECTRA_REQUIRE(aligned16(qkv) && aligned16(k_cache) && aligned16(v_cache) &&
-                      (cos_t == nullptr || (aligned16(cos_t) && aligned16(sin_t))),
-                  "qkv, the caches and the cos / sin tables must be 16-byte aligned");
-  if (workspace == nullptr || workspace_bytes < spectra_attend_workspace(heads, head_dim, max_seq) ||
-      (reinterpret_cast<uintptr_t>(workspace) & 15))
-    return fail(SPECTRA_ERR_WORKSPACE, "workspace missing, unaligned or smaller than spectra_attend_workspace()");
-  const int g = heads / kv_heads;
-  const attend_fn fn = cos_t ? pick_attend_hd<true>(head_dim, g) : pick_attend_hd<false>(head_dim, g);
-  if (fn == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "decode attention serves 1, 2, 3, 4, 6 or 8 query heads per KV head");
-  const int nspan = spectra_attend_spans(max_seq);
-  const float scale = 1.0f / sqrtf((float)head_dim);
-  float* part = (float*)workspace;
-  const hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(fn, dim3((unsigned)kv_heads, (unsigned)nspan), dim3(kDecThreads), 0, s, (const uint16_t*)qkv,
-                     pos, cos_t, sin_t, heads, kv_heads, max_seq, scale, (uint16_t*)k_cache, (uint16_t*)v_cache, part);
+  KvCache kvc{};
+  kvc.k = (uint16_t*)k_cache;
+  kvc.v = (uint16_t*)v_cache;
+  kvc.lmax = max_seq;
+  kvc.window = max_seq;
+  return attend_launch(qkv, pos, cos_t, sin_t, heads, kv_heads, head_dim, kvc, false, workspace, workspace_bytes, out,
+                       stream);
+}
+
+extern "C" int spectra_attend_decode_q4(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t,
+                                        int32_t heads, int32_t kv_heads, int32_t head_dim, int32_t max_seq,
+                                        int32_t window, void* k_window, void* v_window, void* k_codes, void* v_codes,
+                                        void* k_scales, void* v_scales, void* k_zeros, void* v_zeros,
+                                        void* workspace, size_t workspace_bytes, void* out, spectra_stream_t stream) {
+  KvCache kvc;
+  kvc.k = (uint16_t*)k_window;
+  kvc.v = (uint16_t*)v_window;
+  kvc.kq = (uint8_t*)k_codes;
+  kvc.vq = (uint8_t*)v_codes;
+  kvc.ks = (uint16_t*)k_scales;
+  kvc.vs = (uint16_t*)v_scales;
+  kvc.kz = (uint8_t*)k_zeros;
+  kvc.vz = (uint8_t*)v_zeros;
+  kvc.lmax = max_seq;
+  kvc.window = window;
+  return attend_launch(qkv, pos, cos_t, sin_t, heads, kv_heads, head_dim, kvc, true, workspace, workspace_bytes, out,
+                       stream);
+}
+
+extern "C" int spectra_kv4_quantize(const void* x, int64_t ldx, int64_t rows, int32_t heads, int64_t x_head_stride,
+                                    int32_t d, void* codes, void* scales, void* zeros, int64_t out_head_rows,
+                                    spectra_stream_t stream) {
+  SPECTRA_REQUIRE(x && codes && scales && zeros, "NULL pointer");
+  SPECTRA_REQUIRE(d >= 32 && d % 32 == 0 && d <= 4096, "d must be a multiple of 32 in [32, 4096]");
+  SPECTRA_REQUIRE(rows >= 1 && heads >= 1 && heads <= 65535 && ldx >= d && out_head_rows >= rows, "bad shape");
+  SPECTRA_REQUIRE(aligned16(x) && ldx % 8 == 0 && x_head_stride % 8 == 0, "x must be 16-byte aligned rows");
+  SPECTRA_REQUIRE((reinterpret_cast<uintptr_t>(codes) & 3) == 0 && (reinterpret_cast<uintptr_t>(scales) & 1) == 0,
+                  "codes must be 4-byte and scales 2-byte aligned");
+  const int64_t work = rows * (d / 8);
+  SPECTRA_REQUIRE((work + kDecThreads - 1) / kDecThreads < (int64_t(1) << 31), "too many rows");
+  hipLaunchKernelGGL(kv4_quantize_kernel, dim3((unsigned)((work + kDecThreads - 1) / kDecThreads), (unsigned)heads),
+                     dim3(kDecThreads), 0, (hipStream_t)stream, (const uint16_t*)x, ldx, x_head_stride, rows, d,
+                     out_head_rows, (uint8_t*)codes, (uint16_t*)scales, (uint8_t*)zeros);
   SPECTRA_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)heads), dim3((unsigned)head_dim), 0, s, part, nspan, head_dim,
-                     (uint16_t*)out);
+  return SPECTRA_OK;
+}
+
+extern "C" int spectra_kv4_dequantize(const void* codes, const void* scales, const void* zeros, int64_t rows, int32_t d,
+                                      void* out_bf16, spectra_stream_t stream) {
+  SPECTRA_REQUIRE(codes && scales && zeros && out_bf16, "NULL pointer");
+  SPECTRA_REQUIRE(d >= 32 && d % 32 == 0 && d <= 4096 && rows >= 1, "bad shape");
+  SPECTRA_REQUIRE(aligned16(out_bf16) && (reinterpret_cast<uintptr_t>(codes) & 3) == 0, "misaligned operands");
+  const int64_t work = rows * (d / 8);
+  SPECTRA_REQUIRE((work + kDecThreads - 1) / kDecThreads < (int64_t(1) << 31), "too many rows");
+  hipLaunchKernelGGL(kv4_dequantize_kernel, dim3((unsigned)((work + kDecThreads - 1) / kDecThreads)),
+                     dim3(kDecThreads), 0, (hipStream_t)stream, (const uint8_t*)codes, (const uint16_t*)scales,
+                     (const uint8_t*)zeros, rows, d, (uint16_t*)out_bf16);
   SPECTRA_HIP_CHECK(hipGetLastError());
   return SPECTRA_OK;
 }

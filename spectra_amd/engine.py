@@ -15,8 +15,9 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .kernels import (GEMV_MAX_M, QWeightOperands, attend_decode, attend_workspace_bytes, greedy_next, rmsnorm,
-                      rope_append, silu_mul, w4_embedding, w4a16_gemv_fused, w4a16_linear)
+from .kernels import (GEMV_MAX_M, QWeightOperands, attend_decode, attend_decode_q4, attend_workspace_bytes,
+                      greedy_next, kv4_quantize, rmsnorm, rope_append, silu_mul, w4_embedding, w4a16_gemv_fused,
+                      w4a16_linear)
 
 __all__ = ["SpectraFusedLinear", "SpectraFusedEmbedding", "DecoderConfig", "SpectraDecoder"]
 
@@ -177,6 +178,8 @@ class DecoderConfig:
     rope_theta: float = 500000.0
     rms_eps: float = 1e-5
     max_seq: int = 1024
+    kv_bits: int = 16        # 16: fp16 cache; 4: the reference's 4-bit cache (engine.py:614-700)
+    kv_window: int = 128     # kv_bits 4: recent positions also kept in fp16 (engine.py:685 residual_length)
     hadamard_block: int = 128
     outlier_ratio: float = 0.005
     seed: int = 0
@@ -248,8 +251,21 @@ class SpectraDecoder(nn.Module):
         self.norm_w = [w.to(device=dev, dtype=torch.float32).contiguous() for w in weights["norms"]]
         self.norm_w16 = [w.half() for w in self.norm_w]  # the fused GEMV prologues read fp16 weights
         # KV cache [layer, kv, max_seq, head_dim]: a position's head is one 16-byte-aligned run
-        self.k_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
-        self.v_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
+        if c.kv_bits not in (16, 4):
+            raise ValueError("kv_bits must be 16 or 4")
+        if c.kv_bits == 16:
+            self.k_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
+            self.v_cache = torch.zeros(c.layers, c.kv_heads, c.max_seq, hd, device=dev, dtype=torch.float16)
+        else:  # every position in 4 bits + fp16 rings of the last kv_window positions
+            w = min(c.kv_window, c.max_seq)
+            self.k_cache = torch.zeros(c.layers, c.kv_heads, w, hd, device=dev, dtype=torch.float16)
+            self.v_cache = torch.zeros(c.layers, c.kv_heads, w, hd, device=dev, dtype=torch.float16)
+
+            def q4():
+                return (torch.zeros(c.layers, c.kv_heads, c.max_seq, hd // 2, device=dev, dtype=torch.uint8),
+                        torch.zeros(c.layers, c.kv_heads, c.max_seq, hd // 32, device=dev, dtype=torch.float16),
+                        torch.zeros(c.layers, c.kv_heads, c.max_seq, hd // 32, device=dev, dtype=torch.uint8))
+            self.k4, self.v4 = q4(), q4()
         inv = 1.0 / (c.rope_theta ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
         ang = torch.arange(c.max_seq, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)  # [max_seq, hd/2]
@@ -336,11 +352,26 @@ class SpectraDecoder(nn.Module):
         g = c.heads // c.kv_heads
         x = rmsnorm(h, self.norm_w[2 * li], c.rms_eps, residual=delta)
         qkv = blk["qkv"](x)
-        q = rope_append(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li])
         L = causal_len
+        if c.kv_bits == 16:
+            kc, vc = self.k_cache[li], self.v_cache[li]
+        else:  # the prompt attends in full precision; the cache keeps it in 4 bits (+ the window)
+            kc = torch.empty(c.kv_heads, L, hd, device=h.device, dtype=torch.float16)
+            vc = torch.empty_like(kc)
+        q = rope_append(qkv, pos, self.cos[:kc.shape[1]].contiguous(), self.sin[:kc.shape[1]].contiguous(), c.heads,
+                        c.kv_heads, kc, vc)
+        if c.kv_bits == 4:
+            k4 = tuple(t[li] for t in self.k4)
+            v4 = tuple(t[li] for t in self.v4)
+            kv4_quantize(kc, out=k4, out_rows=c.max_seq)
+            kv4_quantize(vc, out=v4, out_rows=c.max_seq)
+            w = self.k_cache.shape[2]
+            last = self.arange[max(0, L - w):L]  # the window's positions -> ring slots position % window
+            self.k_cache[li].index_copy_(1, last % w, kc[:, last])
+            self.v_cache[li].index_copy_(1, last % w, vc[:, last])
         qg = q.permute(1, 0, 2).reshape(c.kv_heads, g * T, hd).contiguous()  # head = kv * g + j
-        kt = self.k_cache[li][:, :L, :].transpose(1, 2).contiguous()  # [kv, hd, L]
-        vv = self.v_cache[li][:, :L, :].contiguous()
+        kt = kc[:, :L, :].transpose(1, 2).contiguous()  # [kv, hd, L]
+        vv = vc[:, :L, :].contiguous()
         s = torch.matmul(qg, kt).float() * (1.0 / math.sqrt(hd))  # [kv, g*T, L]
         qpos = pos.repeat(g)  # row r = j * T + t -> position pos[t]
         s = s.masked_fill((self.arange[:L][None, :] > qpos[:, None])[None], float("-inf"))
@@ -357,8 +388,13 @@ class SpectraDecoder(nn.Module):
         c, blk = self.cfg, self.blocks[li]
         qkv = w4a16_gemv_fused(blk["qkv"]._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[2 * li],
                                eps=c.rms_eps)
-        a = attend_decode(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li],
-                          self.attn_ws)
+        if c.kv_bits == 16:
+            a = attend_decode(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li],
+                              self.attn_ws)
+        else:
+            a = attend_decode_q4(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li],
+                                 self.v_cache[li], tuple(t[li] for t in self.k4), tuple(t[li] for t in self.v4),
+                                 self.attn_ws)
         w4a16_gemv_fused(blk["o"]._operands(), a.reshape(1, c.hidden), residual=h, out=h)
         gu = w4a16_gemv_fused(blk["gate_up"]._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[2 * li + 1],
                               eps=c.rms_eps)
@@ -396,11 +432,16 @@ class SpectraDecoder(nn.Module):
         greedy_next(logits[0], self.cur_id, self.history, self.cur_pos)
         return logits
 
+    def cache_tensors(self):
+        """Every tensor of the KV cache (fp16 cache, or 4-bit codes / scales / zeros + rings)."""
+        extra = list(self.k4) + list(self.v4) if self.cfg.kv_bits == 4 else []
+        return [self.k_cache, self.v_cache] + extra
+
     @torch.no_grad()
     def capture_decode(self) -> None:
         """Capture one decode step (all linears, attention and the sampling) as a HIP graph."""
-        saved = (self.cur_id.clone(), self.cur_pos.clone(), self.history.clone(), self.k_cache.clone(),
-                 self.v_cache.clone())
+        saved = (self.cur_id.clone(), self.cur_pos.clone(), self.history.clone(),
+                 [t.clone() for t in self.cache_tensors()])
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
@@ -415,8 +456,8 @@ class SpectraDecoder(nn.Module):
         self.cur_id.copy_(saved[0])
         self.cur_pos.copy_(saved[1])
         self.history.copy_(saved[2])
-        self.k_cache.copy_(saved[3])
-        self.v_cache.copy_(saved[4])
+        for t, b in zip(self.cache_tensors(), saved[3]):
+            t.copy_(b)
 
     @torch.no_grad()
     def decode(self, steps: int, use_graph: bool = True) -> torch.Tensor:

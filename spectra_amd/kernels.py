@@ -26,7 +26,8 @@ from . import _lib as L
 
 __all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_dequant", "fwht_rows",
            "QWeightOperands", "GEMV_MAX_M", "w4_embedding", "rmsnorm", "rope_append", "attend_decode",
-           "attend_workspace_bytes", "silu_mul", "greedy_next", "w4a16_gemv_fused"]
+           "attend_workspace_bytes", "silu_mul", "greedy_next", "w4a16_gemv_fused", "kv4_quantize",
+           "kv4_dequantize", "attend_decode_q4"]
 
 GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
 
@@ -463,4 +464,75 @@ def w4a16_gemv_fused(ops: QWeightOperands, x: torch.Tensor, *, prologue: str = "
     L.check("spectra_w4a16_gemv_fused", lib.spectra_w4a16_gemv_fused(ops.ptr(), x2.data_ptr(), ldx, x2.shape[0],
                                                                       L.F16, ctypes.byref(fu), out2.data_ptr(),
                                                                       out2.stride(0), _stream(x.device)))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the 4-bit KV cache (engine.py:614-700)
+# ---------------------------------------------------------------------------
+def kv4_quantize(x: torch.Tensor, out: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None,
+                 out_rows: Optional[int] = None):
+    """Quantize fp16 rows ``x`` [..., rows, d] (leading dims = heads) like the reference's
+    ``_quantize``: returns (codes uint8 [..., out_rows, d/2], scales fp16 [..., out_rows, d/32],
+    zeros uint8 [..., out_rows, d/32]); with ``out`` the rows go to the first ``rows`` of
+    each head's ``out_rows`` (e.g. a cache of max_seq positions)."""
+    _need_f16(x, "x", contiguous=False)
+    d = x.shape[-1]
+    rows = x.shape[-2]
+    x3 = x.reshape(-1, rows, d) if x.dim() != 2 else x.reshape(1, rows, d)
+    if x3.stride(-1) != 1:
+        raise ValueError("x rows must be contiguous")
+    heads = x3.shape[0]
+    orows = out_rows or rows
+    if out is None:
+        lead = tuple(x.shape[:-2])
+        out = (torch.empty(lead + (orows, d // 2), device=x.device, dtype=torch.uint8),
+               torch.empty(lead + (orows, d // 32), device=x.device, dtype=torch.float16),
+               torch.empty(lead + (orows, d // 32), device=x.device, dtype=torch.uint8))
+    codes, scales, zeros = out
+    lib = L.load()
+    L.check("spectra_kv4_quantize", lib.spectra_kv4_quantize(x3.data_ptr(), x3.stride(1), rows, heads, x3.stride(0), d,
+                                                              codes.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
+                                                              orows, _stream(x.device)))
+    return out
+
+
+def kv4_dequantize(codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor) -> torch.Tensor:
+    """The reference's ``_dequantize``: (q - z) * s as bf16 [rows, d]."""
+    d = codes.shape[-1] * 2
+    rows = codes.numel() // (d // 2)
+    out = torch.empty(codes.shape[:-1] + (d,), device=codes.device, dtype=torch.bfloat16)
+    lib = L.load()
+    L.check("spectra_kv4_dequantize", lib.spectra_kv4_dequantize(codes.contiguous().data_ptr(),
+                                                                  scales.contiguous().data_ptr(),
+                                                                  zeros.contiguous().data_ptr(), rows, d,
+                                                                  out.data_ptr(), _stream(codes.device)))
+    return out
+
+
+def attend_decode_q4(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, heads: int,
+                     kv_heads: int, k_window: torch.Tensor, v_window: torch.Tensor, k4, v4,
+                     workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``attend_decode`` over a 4-bit cache: ``k4`` / ``v4`` = (codes [kv, L, d/2], scales
+    [kv, L, d/32], zeros [kv, L, d/32]) hold every position; ``k_window`` / ``v_window``
+    [kv, W, d] fp16 rings hold the last W positions (slot = position % W)."""
+    _need_f16(qkv, "qkv")
+    _need_f16(k_window, "k_window")
+    _need_f16(v_window, "v_window")
+    kv, w, hd = k_window.shape
+    lmax = k4[0].shape[1]
+    if v_window.shape != k_window.shape or kv != kv_heads or k4[0].shape != (kv, lmax, hd // 2):
+        raise ValueError("windows [kv_heads, W, d] and codes [kv_heads, L, d/2] expected")
+    if pos.dtype != torch.int64 or pos.numel() != 1:
+        raise ValueError("pos must be int64 [1]")
+    need = attend_workspace_bytes(heads, hd, lmax)
+    if workspace is None:
+        workspace = torch.empty(need, device=qkv.device, dtype=torch.uint8)
+    if out is None:
+        out = torch.empty((heads, hd), device=qkv.device, dtype=torch.float16)
+    ptrs = [t.data_ptr() for t in (k_window, v_window, k4[0], v4[0], k4[1], v4[1], k4[2], v4[2])]
+    lib = L.load()
+    L.check("spectra_attend_decode_q4", lib.spectra_attend_decode_q4(
+        qkv.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(), heads, kv, hd, lmax, w, *ptrs,
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(), out.data_ptr(), _stream(qkv.device)))
     return out

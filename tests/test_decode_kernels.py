@@ -15,6 +15,7 @@ restatements of the same math:
 * silu_mul: within rel 2e-3 of fp32 silu(g) * u.
 """
 import math
+import os
 
 import numpy as np
 
@@ -222,3 +223,79 @@ def test_gemv_residual_without_prologue(hip):
     assert torch.equal(y, K.w4a16_linear(ops, x))
     r = K.w4a16_gemv_fused(ops, x, residual=res)
     assert torch.equal(r, res + y)
+
+
+# ---------------------------------------------------------------------------
+# the 4-bit KV cache (reference engine.py:614-700)
+# ---------------------------------------------------------------------------
+GOLD_KV4 = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "kv4_quant.npz")
+
+
+@pytest.mark.parametrize("name", ["fp16_128", "fp16_64", "bf16_128", "bf16_96"])
+def test_kv4_quantize_and_dequant_reference_vectors(hip, name):
+    """Vectors from the reference's own _quantize / _dequantize (constant, zero and
+    one-signed groups included): the kernel's codes, scales and zero points for fp16 rows
+    and the dequant of the reference's codes, bit for bit."""
+    case(name=name)
+    g = np.load(GOLD_KV4)
+    packed, scales, zeros = g[name + "_packed"], g[name + "_scales"], g[name + "_zeros"]
+    rows, d = g[name + "_x"].shape
+    if name.startswith("fp16"):
+        x = torch.from_numpy(g[name + "_x"]).cuda()
+        c, s, z = K.kv4_quantize(x)
+        assert np.array_equal(c.cpu().numpy(), packed.reshape(rows, d // 2))
+        assert np.array_equal(s.cpu().numpy().view(np.uint16), scales.reshape(rows, d // 32).view(np.uint16))
+        assert np.array_equal(z.cpu().numpy(), zeros.reshape(rows, d // 32))
+    deq = K.kv4_dequantize(torch.from_numpy(packed.reshape(rows, d // 2)).cuda(),
+                           torch.from_numpy(scales.reshape(rows, d // 32)).cuda(),
+                           torch.from_numpy(zeros.reshape(rows, d // 32)).cuda())
+    assert np.array_equal(deq.cpu().view(torch.int16).numpy(), g[name + "_deq"])
+
+
+@pytest.mark.parametrize("heads,kv,hd,L,W", [(24, 8, 128, 300, 128), (8, 2, 64, 200, 16), (6, 3, 256, 130, 64)])
+def test_attend_decode_q4(hip, heads, kv, hd, L, W):
+    import oracle as O
+    g = torch.Generator(device="cuda").manual_seed(heads + L)
+    kfull = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+    vfull = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+    cos, sin = _tables(L, hd)
+    k4 = K.kv4_quantize(kfull)
+    v4 = K.kv4_quantize(vfull)
+    kw = torch.zeros(kv, W, hd, device="cuda", dtype=torch.float16)
+    vw = torch.zeros_like(kw)
+    ws = torch.empty(K.attend_workspace_bytes(heads, hd, L), device="cuda", dtype=torch.uint8)
+    grp = heads // kv
+    p0 = L // 2
+    last = torch.arange(max(0, p0 - W), p0, device="cuda")  # the window before the first step
+    kw.index_copy_(1, last % W, kfull[:, last])
+    vw.index_copy_(1, last % W, vfull[:, last])
+    for p in range(p0, p0 + 4):
+        case(heads=heads, kv=kv, hd=hd, L=L, W=W, pos=p)
+        qkv = (torch.randn((heads + 2 * kv) * hd, device="cuda", generator=g) * 2).half()
+        pos = torch.tensor([p], device="cuda", dtype=torch.int64)
+        out = K.attend_decode_q4(qkv, pos, cos, sin, heads, kv, kw, vw, k4, v4, ws)
+        q = _rope_ref(qkv[: heads * hd].reshape(1, heads, hd), cos[p][None, None, :], sin[p][None, None, :])
+        k = _rope_ref(qkv[heads * hd: (heads + kv) * hd].reshape(1, kv, hd), cos[p][None, None, :],
+                      sin[p][None, None, :])[0]
+        v = qkv[(heads + kv) * hd:].reshape(kv, hd)
+        # the append: fp16 ring slot p % W, and the codes of position p
+        assert torch.equal(kw[:, p % W], k) and torch.equal(vw[:, p % W], v)
+        kc, ks, kz = K.kv4_quantize(k.reshape(kv, 1, hd))
+        assert torch.equal(k4[0][:, p], kc[:, 0]) and torch.equal(k4[1][:, p], ks[:, 0]) and torch.equal(k4[2][:, p], kz[:, 0])
+        kfull[:, p], vfull[:, p] = k, v
+        # reference: window positions in fp16, older ones through the reference's dequant
+        kr = kfull[:, : p + 1].float().clone()
+        vr = vfull[:, : p + 1].float().clone()
+        old = p + 1 - W
+        if old > 0:
+            for src, dst in ((k4, kr), (v4, vr)):
+                cn, sn_, zn = (t[:, :old].cpu().numpy() for t in src)
+                deq = O.kv4_dequantize(cn.reshape(-1, hd // 32, 16), sn_.reshape(-1, hd // 32, 1),
+                                       zn.reshape(-1, hd // 32, 1))
+                dst[:, :old] = torch.from_numpy(O.bf16_bits_to_f32(deq).reshape(kv, old, hd)).cuda()
+        kk = kr.transpose(1, 2).repeat_interleave(grp, dim=0)
+        vv = vr.repeat_interleave(grp, dim=0)
+        sc = torch.matmul(q[0].float()[:, None, :], kk.contiguous())[:, 0, :] / math.sqrt(hd)
+        ref = torch.matmul(torch.softmax(sc, -1)[:, None, :], vv.contiguous())[:, 0, :]
+        err = (out.float() - ref).abs().max().item()
+        assert err <= 2e-3 * vfull.abs().max().item(), (p, err)

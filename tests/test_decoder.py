@@ -177,3 +177,40 @@ def test_decoder_graph_matches_eager(hip):
     t_graph = graphed.decode(6, use_graph=True)
     assert torch.equal(t_eager, t_graph)
     assert torch.equal(eager.k_cache, graphed.k_cache) and torch.equal(eager.v_cache, graphed.v_cache)
+
+
+def test_decoder_kv4_cache(hip):
+    """The 4-bit cache: while every position is inside the fp16 window the decode is the fp16
+    decoder's, bit for bit; the prompt's codes are the reference quantizer's codes of the
+    fp16 decoder's keys / values; past the window the logits stay near the fp16 decoder's and
+    graph replay equals eager decode."""
+    import dataclasses
+    import oracle as O
+    prompt = torch.randint(0, SMALL.vocab, (24,), generator=torch.Generator().manual_seed(4)).cuda()
+    full = SpectraDecoder(SMALL)
+    wide = SpectraDecoder(dataclasses.replace(SMALL, kv_bits=4, kv_window=64))
+    lf, lw = full.prefill(prompt), wide.prefill(prompt)
+    assert torch.equal(lf, lw)
+    assert torch.equal(full.decode(5, use_graph=False), wide.decode(5, use_graph=False))
+    # prompt codes = the reference quantizer on the fp16 cache rows
+    hd = SMALL.head_dim
+    for li in range(SMALL.layers):
+        for src, q4 in ((full.k_cache, wide.k4), (full.v_cache, wide.v4)):
+            rows = src[li][:, :24].reshape(-1, hd).cpu().numpy()
+            c, s, z = O.kv4_quantize(rows, "float16")
+            assert np.array_equal(q4[0][li][:, :24].reshape(-1, hd // 2).cpu().numpy(), c.reshape(-1, hd // 2))
+            assert np.array_equal(q4[1][li][:, :24].reshape(-1, hd // 32).cpu().numpy().view(np.uint16),
+                                  s.reshape(-1, hd // 32).view(np.uint16))
+            assert np.array_equal(q4[2][li][:, :24].reshape(-1, hd // 32).cpu().numpy(), z.reshape(-1, hd // 32))
+    # a window of 8: the first decode step already reads 16 of its 25 positions from the codes
+    narrow = dataclasses.replace(SMALL, kv_bits=4, kv_window=8)
+    q4, ref = SpectraDecoder(narrow), SpectraDecoder(SMALL)
+    q4.prefill(prompt), ref.prefill(prompt)
+    lq = q4.forward_tokens(q4.cur_id, q4.cur_pos, None).float()
+    lr = ref.forward_tokens(ref.cur_id, ref.cur_pos, None).float()
+    assert (lq - lr).abs().max().item() <= 0.1 * lr.abs().max().item()
+    eager, graphed = SpectraDecoder(narrow), SpectraDecoder(narrow)
+    eager.prefill(prompt), graphed.prefill(prompt)
+    assert torch.equal(eager.decode(6, use_graph=False), graphed.decode(6, use_graph=True))
+    for a, b in zip(eager.cache_tensors(), graphed.cache_tensors()):
+        assert torch.equal(a, b)

@@ -343,3 +343,41 @@ def test_outlier_selection_invariants():
     _, r2, _ = O.select_outlier_columns(w, "float32", None, 0.01, False)
     assert r2 == 0.01
     assert np.all(np.diff(idx) > 0)
+
+
+def test_kv4_oracle_matches_reference_vectors():
+    """The 4-bit KV quantizer restatement against vectors of the reference's own _quantize /
+    _dequantize (engine.py:624-672), fp16 and bf16 rows, special groups included."""
+    g = np.load(os.path.join(HERE, "golden", "kv4_quant.npz"))
+    for name in ("bf16_128", "fp16_128", "fp16_64", "bf16_96"):
+        dt = "bfloat16" if name.startswith("bf16") else "float16"
+        x = g[name + "_x"]
+        x = x.view(np.uint16) if dt == "bfloat16" else x
+        p, s, z = O.kv4_quantize(x, dt)
+        assert np.array_equal(p, g[name + "_packed"]), name
+        assert np.array_equal(s.view(np.uint16), g[name + "_scales"].view(np.uint16)), name
+        assert np.array_equal(z, g[name + "_zeros"]), name
+        assert np.array_equal(O.kv4_dequantize(p, s, z), g[name + "_deq"].view(np.uint16)), name
+
+
+def test_kv4_oracle_invariants():
+    """What the quantizer's definition fixes: codes and zero points in [0, 15]; every value
+    of a non-constant bf16 group reconstructed within one step (half a step of rounding,
+    and the zero point -- rounded in bf16 -- can shift the grid enough to clip the group's
+    extreme code by up to half a step more) plus the bf16 rounding of the result; a constant
+    bf16 group reconstructed exactly."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((50, 128)) * np.exp(rng.standard_normal((50, 1)))).astype(np.float32)
+    x[0, :32] = 0.75
+    x[1, 32:64] = -3.0
+    xb = O.f32_to_bf16_bits(x)
+    p, s, z = O.kv4_quantize(xb, "bfloat16")
+    q = np.stack([p & 15, p >> 4], -1).reshape(p.shape[0], p.shape[1], 32)
+    assert q.max() <= 15 and z.max() <= 15
+    deq = O.bf16_bits_to_f32(O.kv4_dequantize(p, s, z)).reshape(50, 4, 32)
+    xf = O.bf16_bits_to_f32(xb).reshape(50, 4, 32)
+    step = s.astype(np.float32)
+    err = np.abs(deq - xf)
+    assert np.all(err <= step * (1 + 1e-2) + np.abs(xf) * 2 ** -8 + 1e-30)
+    assert np.mean(err <= step / 2 * (1 + 1e-2) + np.abs(xf) * 2 ** -8) > 0.99  # clipping is rare
+    assert np.array_equal(deq[0, 0], xf[0, 0]) and np.array_equal(deq[1, 1], xf[1, 1])
