@@ -193,6 +193,8 @@ def main():
                     help="only run the dominant kernel's timing loop (for rocprofv3 runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run plain device copies of COPY_BYTES each (PMC traffic calibration)")
+    ap.add_argument("--profile-gemm", action="store_true",
+                    help="only run the cfg4 prefill GEMMs a few times (for rocprofv3 counter runs)")
     ap.add_argument("--decode-e2e", action="store_true",
                     help="only run the cfg5 end-to-end decode (for rocprofv3 runs); prints its JSON fields")
     args = ap.parse_args()
@@ -211,6 +213,9 @@ def main():
         return
     if args.decode_e2e:
         print(json.dumps(decode_e2e(dev)), flush=True)
+        return
+    if args.profile_gemm:
+        print(json.dumps(profile_gemm(dev)), flush=True)
         return
 
     # ---- cfg2 operands
@@ -380,6 +385,20 @@ def secondary(lib, dev, pool_gb: float) -> dict:
     out["cfg5_note"] = "113 GEMVs of one decode token (28 layers + lm_head) in one graph; attention/norms excluded"
     del chain, keep, layer, head
     out.update(decode_e2e(dev))
+    return out
+
+
+def profile_gemm(dev, iters: int = 3) -> dict:
+    """cfg4's two prefill GEMMs (M=2048, bf16), ``iters`` launches each after a warm-up."""
+    out = {}
+    for kk, nn in ((4096, 14336), (14336, 4096)):
+        q4 = synth_nf4(nn, kk, seed=40 + kk)
+        a = torch.randn(2048, kk, generator=torch.Generator().manual_seed(kk)).bfloat16().to(dev)
+        fn = lambda: K.batched_w4a16_gemm(a, q4.packed, q4.absmax, None, outlier_idx=q4.col, outlier_w=q4.val,
+                                          marlin_layout=True, **q4.kernel_kwargs())
+        t = _time_eager(fn, iters)
+        out[f"cfg4_gemm_k{kk}_n{nn}_us"] = round(t * 1e6, 1)
+        del q4, a
     return out
 
 

@@ -30,10 +30,18 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kBM = 256, kBK = 32;
 constexpr int kGemmWaves = 8;  // two per SIMD (four waves of 128 x 128 measured slower)
-constexpr int kRowH = 40;         // fp16 per LDS tile row: 32 + 8 of padding (80 bytes)
+constexpr int kRowH = 32;         // fp16 per LDS tile row (64 bytes, four 16-byte chunks, swizzled)
 constexpr int kPrepThreads = 256;
 constexpr int kGLut = 65536;      // lane-replicated nibble-pair LUT at LDS address 0
 constexpr int kWin = 4;           // outlier entries prefetched per weight row
+
+// 16-byte chunk c of tile row r sits at chunk c ^ tile_swz(r): with 64-byte rows, every
+// 8-lane (32 banks) or 16-lane (64 banks) phase of the tile stores (two or four lanes per
+// row) and of the MFMA fragment reads (one lane per row, 32 consecutive rows) touches
+// distinct banks.  The mask takes rows' bits 1..3 only, so rows 32 apart share it.
+__device__ __forceinline__ int tile_swz(int r) {
+  return (((r >> 1) ^ (r >> 2)) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1);
+}
 
 // ---------------------------------------------------------------------------
 // activation pre-pass
@@ -354,12 +362,13 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   // ---- register stage -> LDS buffer: activations as loaded, weights decoded ----
   auto store = [&](u32x4_t ga, u32x4_t gb, u32x4_t gc, u32x4_t gd, u32x4_t gw, uint16_t gs, uint8_t gz, int step,
                    int buf) __attribute__((always_inline)) {
-    u32x4_t* ad = (u32x4_t*)(As + (buf * kBM + ar) * kRowH + 8 * AU * ah);
-    ad[0] = ga;
-    ad[1] = gb;
+    uint16_t* arow_l = As + (buf * kBM + ar) * kRowH;
+    const int asw = tile_swz(ar);
+    *(u32x4_t*)(arow_l + 8 * ((AU * ah) ^ asw)) = ga;
+    *(u32x4_t*)(arow_l + 8 * ((AU * ah + 1) ^ asw)) = gb;
     if constexpr (AU == 4) {
-      ad[2] = gc;
-      ad[3] = gd;
+      *(u32x4_t*)(arow_l + 8 * ((AU * ah + 2) ^ asw)) = gc;
+      *(u32x4_t*)(arow_l + 8 * ((AU * ah + 3) ^ asw)) = gd;
     }
     const _Float16 sh = __builtin_bit_cast(_Float16, gs);
     const f16x2g_t s2 = {sh, sh};
@@ -377,19 +386,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
       d[b] = __builtin_bit_cast(uint32_t, c);
     }
     uint16_t* wrow_l = Ws + (buf * BN + wr) * kRowH;
-    if constexpr (BPT == 16) {
-      uint4* wd = (uint4*)(wrow_l + 2 * wb0);
-      wd[0] = make_uint4(d[0], d[1], d[2], d[3]);
-      wd[1] = make_uint4(d[4], d[5], d[6], d[7]);
-      wd[2] = make_uint4(d[8], d[9], d[10], d[11]);
-      wd[3] = make_uint4(d[12], d[13], d[14], d[15]);
-    } else if constexpr (BPT == 8) {
-      uint4* wd = (uint4*)(wrow_l + 2 * wb0);
-      wd[0] = make_uint4(d[0], d[1], d[2], d[3]);
-      wd[1] = make_uint4(d[4], d[5], d[6], d[7]);
-    } else {
-      *(uint4*)(wrow_l + 2 * wb0) = make_uint4(d[0], d[1], d[2], d[3]);
-    }
+    const int wsw = tile_swz(wr);
+    const int wc0 = wb0 / 4;  // first 16-byte chunk (8 fp16) of this thread's decoded run
+#pragma unroll
+    for (int u = 0; u < BPT / 4; ++u)
+      *(uint4*)(wrow_l + 8 * ((wc0 + u) ^ wsw)) = make_uint4(d[4 * u], d[4 * u + 1], d[4 * u + 2], d[4 * u + 3]);
     // outliers of this row inside the step: the queue head while it lies below the
     // step's end (ascending columns); the same thread wrote the decoded values above, so
     // program order suffices
@@ -398,7 +399,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
       while (qc[0] < khi) {
         const int kk = qc[0] - klo;
         const int jb = p.marlin ? (kk & 15) : (kk >> 1), h = p.marlin ? (kk >> 4) : (kk & 1);
-        if (kk >= 0 && jb >= wb0 && jb < wb0 + BPT) wrow_l[2 * jb + h] = qv[0];
+        if (kk >= 0 && jb >= wb0 && jb < wb0 + BPT) {
+          const int e = 2 * jb + h;  // fp16 index in the step's row
+          wrow_l[8 * ((e >> 3) ^ wsw) + (e & 7)] = qv[0];
+        }
 #pragma unroll
         for (int q = 0; q + 1 < kWin; ++q) {
           qc[q] = qc[q + 1];
@@ -426,14 +430,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   __syncthreads();
 
   const int arow = wm * 128 + (lane & 31), brow = wn * WN + (lane & 31), kq = 8 * (lane >> 5);
+  const int aswz = tile_swz(arow), bswz = tile_swz(brow);  // rows 32 apart share the mask
   auto mfma_step = [&](int buf) {
 #pragma unroll
     for (int s16 = 0; s16 < kBK; s16 += 16) {
       h8_t af[4], bf[NT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = *(const h8_t*)(As + (buf * kBM + arow + 32 * i) * kRowH + s16 + kq);
+      for (int i = 0; i < 4; ++i)
+        af[i] = *(const h8_t*)(As + (buf * kBM + arow + 32 * i) * kRowH + 8 * (((s16 + kq) >> 3) ^ aswz));
 #pragma unroll
-      for (int j = 0; j < NT; ++j) bf[j] = *(const h8_t*)(Ws + (buf * BN + brow + 32 * j) * kRowH + s16 + kq);
+      for (int j = 0; j < NT; ++j)
+        bf[j] = *(const h8_t*)(Ws + (buf * BN + brow + 32 * j) * kRowH + 8 * (((s16 + kq) >> 3) ^ bswz));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
