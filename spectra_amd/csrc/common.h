@@ -63,6 +63,27 @@ __device__ __forceinline__ float nf4_code_f32(int i) {
   return r;
 }
 
+__device__ __forceinline__ uint16_t nf4_f16_bits(int i) {
+  // fp16 roundings of the NF4 levels (compressor.py:22-27)
+  uint16_t r = 0xbc00;
+  r = (i == 1) ? 0xb992 : r;
+  r = (i == 2) ? 0xb833 : r;
+  r = (i == 3) ? 0xb652 : r;
+  r = (i == 4) ? 0xb48d : r;
+  r = (i == 5) ? 0xb1ea : r;
+  r = (i == 6) ? 0xadd4 : r;
+  r = (i == 7) ? 0x0000 : r;
+  r = (i == 8) ? 0x2d18 : r;
+  r = (i == 9) ? 0x3126 : r;
+  r = (i == 10) ? 0x33e0 : r;
+  r = (i == 11) ? 0x3568 : r;
+  r = (i == 12) ? 0x370d : r;
+  r = (i == 13) ? 0x3880 : r;
+  r = (i == 14) ? 0x39c9 : r;
+  r = (i == 15) ? 0x3c00 : r;
+  return r;
+}
+
 // ---------------------------------------------------------------------------
 // 16-bit float conversions (round-to-nearest-even)
 // ---------------------------------------------------------------------------
@@ -81,6 +102,30 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }
+// Nibble-pair LUT at LDS address 0: row v (a packed byte) holds the fp16 pair
+// (code[v & 15], code[v >> 4]) -- NF4 levels, or the integers 0..15 for Format A -- in 64
+// copies, so lane l reads its own copy at v * 256 + 4 l (one bank per lane).  Wave w of
+// nwaves fills the rows of high codes h = w, w + nwaves, ...: 16 rows of 256 B as four
+// wave-instructions of 1 KB (lane >> 4 picks the row, lane & 15 the 16-byte chunk:
+// conflict-free).  The high code is wave-uniform (scalar work) and the low code one of
+// four per lane, so the build reads no LDS and selects nothing per entry.
+template <int FMT>
+__device__ __forceinline__ void build_pair_lut(uint8_t* smem, int wave, int nwaves, int lane) {
+  auto code = [](int i) -> uint32_t { return FMT == SPECTRA_FMT_NF4 ? nf4_f16_bits(i) : f2h((float)i); };
+  uint32_t lo4[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) lo4[c] = code(4 * c + (lane >> 4));
+  uint4* lut = (uint4*)smem;
+  for (int h = wave; h < 16; h += nwaves) {
+    const uint32_t hb = code(h) << 16;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t e = lo4[c] | hb;
+      lut[(16 * h + 4 * c + (lane >> 4)) * 16 + (lane & 15)] = make_uint4(e, e, e, e);
+    }
+  }
+}
+
 // dtype-tagged load/store of one element
 __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
   if (dtype == SPECTRA_F16) return h2f(((const uint16_t*)p)[i]);

@@ -227,10 +227,6 @@ struct GemmParams {
   float* part;         // ksplit > 1: fp32 partials [ksplit][m][n]
 };
 
-__device__ __forceinline__ uint16_t gm_code_bits(int fmt, int i) {
-  return fmt == SPECTRA_FMT_NF4 ? f2h(nf4_code_f32(i)) : f2h((float)i);
-}
-
 template <int FMT, int BN, int NW>
 __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   constexpr int NTHR = 64 * NW;
@@ -244,7 +240,6 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   uint16_t* As = (uint16_t*)(smem + kGLut);       // [2][256][kRowH]
   uint16_t* Ws = As + 2 * kBM * kRowH;            // [2][BN][kRowH]
   int32_t* fx = (int32_t*)(Ws + 2 * BN * kRowH);  // [256] row exponents
-  uint16_t* codes = (uint16_t*)(fx + kBM);        // [8 waves][16]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * kBM;
@@ -338,24 +333,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
     if constexpr (FMT == SPECTRA_FMT_ASYM_G32) gz = zsrc[ks + step];
   };
 
-  // ---- nibble-pair LUT: 64 wave-instructions of 1 KB (lane l reads bank l) ----
-  if (lane < 16) codes[wave * 16 + lane] = gm_code_bits(FMT, lane);
-  {
-    uint4* lut = (uint4*)smem;
-    for (int i0 = wave; i0 < 64; i0 += 8 * NW) {
-      uint32_t e[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = i0 + NW * j;
-        e[j] = (uint32_t)codes[wave * 16 + 4 * (i & 3) + (lane >> 4)] | ((uint32_t)codes[wave * 16 + (i >> 2)] << 16);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = i0 + NW * j;
-        lut[(16 * (i >> 2) + 4 * (i & 3) + (lane >> 4)) * 16 + (lane & 15)] = make_uint4(e[j], e[j], e[j], e[j]);
-      }
-    }
-  }
+  // ---- nibble-pair LUT (from registers, no LDS reads) ----
+  build_pair_lut<FMT>(smem, wave, NW, lane);
   for (int r = tid; r < kBM; r += NTHR) fx[r] = p.fexp[min(m0 + r, p.m - 1)];
   const uint32_t lanebits = (uint32_t)lane << 2;
 
@@ -637,7 +616,7 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   p.ksplit = g.ksplit;
   p.ksteps = g.ksteps;
   p.part = g.ksplit > 1 ? (float*)((uint8_t*)fexp + align256((size_t)m * 4)) : nullptr;
-  const size_t lds = (size_t)kGLut + (size_t)2 * (kBM + BN) * kRowH * 2 + kBM * 4 + kGemmWaves * 16 * 2;
+  const size_t lds = (size_t)kGLut + (size_t)2 * (kBM + BN) * kRowH * 2 + kBM * 4;
   dim3 grid((unsigned)g.nt, (unsigned)g.mt, (unsigned)g.ksplit);
   const void* kern;
   if (w->format == SPECTRA_FMT_NF4)

@@ -11,7 +11,7 @@ static uint32_t align16(uint32_t v) { return (v + 15u) & ~15u; }
 
 struct GemvPlan {
   int mt, S, G, rpw, R, BD, grid, ocap;
-  uint32_t off_xp, off_xsc, off_part, off_codes, off_rp, off_bias, off_ss, off_res, off_oprod, lds_bytes;
+  uint32_t off_xp, off_xsc, off_part, off_rp, off_bias, off_ss, off_res, off_oprod, lds_bytes;
 };
 
 // returns false when the shape does not fit this kernel family
@@ -49,8 +49,6 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   off = align16(off + (uint32_t)(mt * (k / 32) * 4));
   pl->off_part = off;
   off = align16(off + (uint32_t)(R * S * mt * 4));
-  pl->off_codes = off;
-  off = align16(off + (uint32_t)(kMaxWaves * 16 * 2));
   pl->off_rp = off;
   off = align16(off + (uint32_t)((R + 1) * 4));
   pl->off_bias = off;
@@ -124,7 +122,7 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
   p.csr_nnz = csr ? (int)w->csr_nnz : 0;
   p.n_out = w->num_outliers; p.ow_dt = w->outlier_w_dtype; p.bias_dt = w->bias_dtype; p.act_dt = act_dtype;
   p.R = pl.R; p.S = pl.S; p.G = pl.G; p.ocap = pl.ocap;
-  p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_part = pl.off_part; p.off_codes = pl.off_codes;
+  p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_part = pl.off_part;
   p.off_rp = pl.off_rp; p.off_bias = pl.off_bias; p.off_oprod = pl.off_oprod;
   p.off_ss = pl.off_ss; p.off_res = pl.off_res;
   p.out_scale = w->hadamard_block ? (float)(1.0 / std::sqrt((double)w->hadamard_block)) : 1.0f;

@@ -20,8 +20,8 @@
 //    - nibble decode: a 256-entry LUT in LDS maps a packed byte to the fp16 pair
 //      (code[lo], code[hi]) -- NF4 levels for Format B, the integers 0..15 for Format A.
 //      It is replicated per lane (64 KB) so that lane l always reads bank l: the LDS
-//      address is (byte << 8) | (lane << 2), built by one v_perm_b32.  Each wave fills
-//      its share from a 16-entry table it wrote itself (no barrier, no select chains).
+//      address is (byte << 8) | (lane << 2), built by one v_perm_b32.  The waves fill it
+//      from registers (the high code of a row group is wave-uniform), with no LDS reads.
 //  * Math per packed byte: v_perm + ds_read_b32 + v_dot2_f32_f16.  Scales are applied once
 //    per 32 k: Format B acc * absmax * run_scale; Format A (acc - z * sum(x)) * s * run_scale.
 //  * Lane partials of all rows are reduced across the wave with a transposed halving
@@ -63,7 +63,7 @@ struct GemvParams {
   int okind, n_out, ow_dt, bias_dt, act_dt;
   int csr_nnz;
   int R, S, G, ocap;
-  uint32_t off_xp, off_xsc, off_part, off_codes, off_rp, off_bias, off_oprod, off_ss, off_res;
+  uint32_t off_xp, off_xsc, off_part, off_rp, off_bias, off_oprod, off_ss, off_res;
   float out_scale;  // 1/sqrt(hadamard_block) (1 without rotation)
   float inv_n_out;  // 1/n_out (dense outlier columns)
   // fusions (kernels with PRO != 0 serve one fp16 row)
@@ -77,27 +77,6 @@ struct GemvParams {
 constexpr int kProNone = 0;     // x as given
 constexpr int kProSiluMul = 1;  // x row = [g | u] (2K values): fp16(silu(g) * u)
 constexpr int kProRms = 2;      // x = h: h * w_norm, times rsqrt(mean(h^2) + eps) in the epilogue
-
-__device__ __forceinline__ uint16_t nf4_f16_bits(int i) {
-  // fp16 roundings of the NF4 levels (compressor.py:22-27)
-  uint16_t r = 0xbc00;
-  r = (i == 1) ? 0xb992 : r;
-  r = (i == 2) ? 0xb833 : r;
-  r = (i == 3) ? 0xb652 : r;
-  r = (i == 4) ? 0xb48d : r;
-  r = (i == 5) ? 0xb1ea : r;
-  r = (i == 6) ? 0xadd4 : r;
-  r = (i == 7) ? 0x0000 : r;
-  r = (i == 8) ? 0x2d18 : r;
-  r = (i == 9) ? 0x3126 : r;
-  r = (i == 10) ? 0x33e0 : r;
-  r = (i == 11) ? 0x3568 : r;
-  r = (i == 12) ? 0x370d : r;
-  r = (i == 13) ? 0x3880 : r;
-  r = (i == 14) ? 0x39c9 : r;
-  r = (i == 15) ? 0x3c00 : r;
-  return r;
-}
 
 __device__ __forceinline__ float pow2f(int e) {  // e in [-126, 127]
   return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
@@ -423,29 +402,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     res_raw = ((const uint16_t*)p.res)[mm < p.m ? (int64_t)mm * p.ldr + r0 + rr : 0];
   }
 
-  // ---------------- (3) nibble-pair LUT from a wave-private 16-entry code table ----------------
-  {
-    uint16_t* codes = (uint16_t*)(smem + p.off_codes) + wave * 16;
-    if (lane < 16) codes[lane] = FMT == SPECTRA_FMT_NF4 ? nf4_f16_bits(lane) : f2h((float)lane);
-    // 64 wave-instructions of 1 KB fill the 64 KB: instruction i writes rows
-    // v = 16 (i >> 2) + 4 (i & 3) + (lane >> 4), lane & 15 picking the 16-byte chunk (4
-    // consecutive rows, conflict-free).  All code reads of a batch are issued before the
-    // first store, so the batch waits for LDS once.
-    uint4* lut = (uint4*)smem;
-    for (int i0 = wave; i0 < 64; i0 += 8 * nwaves) {
-      uint32_t e[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = i0 + j * nwaves < 64 ? i0 + j * nwaves : 0;
-        e[j] = (uint32_t)codes[4 * (i & 3) + (lane >> 4)] | ((uint32_t)codes[i >> 2] << 16);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = i0 + j * nwaves;
-        if (i < 64) lut[(16 * (i >> 2) + 4 * (i & 3) + (lane >> 4)) * 16 + (lane & 15)] = make_uint4(e[j], e[j], e[j], e[j]);
-      }
-    }
-  }
+  // ---------------- (3) nibble-pair LUT (from registers, no LDS reads) ----------------
+  build_pair_lut<FMT>(smem, wave, nwaves, lane);
 
   // ---------------- (4) activation half-runs: FWHT, run scale, fp16 pairs -> LDS ----------------
   uint16_t* xp = (uint16_t*)(smem + p.off_xp);

@@ -32,27 +32,6 @@ typedef float sf4_t __attribute__((ext_vector_type(4)));
 constexpr int kSkPrepThreads = 256;
 constexpr int kSkLut = 65536;
 
-__device__ __forceinline__ uint16_t sk_nf4_bits(int i) {
-  // fp16 roundings of the NF4 levels (compressor.py:22-27)
-  uint16_t r = 0xbc00;
-  r = (i == 1) ? 0xb992 : r;
-  r = (i == 2) ? 0xb833 : r;
-  r = (i == 3) ? 0xb652 : r;
-  r = (i == 4) ? 0xb48d : r;
-  r = (i == 5) ? 0xb1ea : r;
-  r = (i == 6) ? 0xadd4 : r;
-  r = (i == 7) ? 0x0000 : r;
-  r = (i == 8) ? 0x2d18 : r;
-  r = (i == 9) ? 0x3126 : r;
-  r = (i == 10) ? 0x33e0 : r;
-  r = (i == 11) ? 0x3568 : r;
-  r = (i == 12) ? 0x370d : r;
-  r = (i == 13) ? 0x3880 : r;
-  r = (i == 14) ? 0x39c9 : r;
-  r = (i == 15) ? 0x3c00 : r;
-  return r;
-}
-
 // k (inside a 128-k chunk) of element e = 2 i + h of the 8 A/B values that lane group g
 // contributes to MFMA t of the chunk.  Lane group g0 loads chunk bytes [16 g0, 16 g0 + 16);
 // after the swap lane group g holds, in register slot t, dword d0 of group g0 with
@@ -166,7 +145,7 @@ struct SkinnyParams {
   void* out;
   int64_t ldo;
   int m, mp, n, k, nchunks, nrounds, csr_nnz, okind, bias_dt, act_dt, ecap;
-  uint32_t off_codes, off_rp, off_bias, off_xe, off_ve, off_sums;
+  uint32_t off_rp, off_bias, off_xe, off_ve, off_sums;
 };
 
 template <int T, int CPW>
@@ -186,7 +165,7 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
   // every argument the prologue needs, fetched in one round trip before the first load
   asm volatile("" ::"s"(p.packed), "s"(p.ldp), "s"(p.scales), "s"(p.lds32), "s"(p.xa), "s"(p.rowptr),
                "s"(p.bias), "s"(p.n), "s"(p.mp), "s"(p.nchunks), "s"(p.nrounds), "s"(p.okind), "s"(p.bias_dt),
-               "s"(p.csr_nnz), "s"(p.ccol), "s"(p.cval), "s"(p.off_codes));
+               "s"(p.csr_nnz), "s"(p.ccol), "s"(p.cval));
 
   // ---- (1) loads the tail needs first (wait counts are in issue order) ----
   // lanes 0/1: the workgroup's first / end CSR row pointer (packed bytes when no CSR)
@@ -263,23 +242,8 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
         ocv = *(big ? (const int4*)(p.ccol + gc) : (const int4*)p.packed);
         ovv = *(big ? (const uint2*)(p.cval + gc) : (const uint2*)p.packed);
       }
-      // ---- (4) nibble-pair LUT: 64 wave-instructions of 1 KB from a 16-entry table ----
-      uint16_t* codes = (uint16_t*)(smem + p.off_codes) + wave * 16;
-      if (lane < 16) codes[lane] = sk_nf4_bits(lane);
-      uint4* lut = (uint4*)smem;
-      for (int i0 = wave; i0 < 64; i0 += 8 * nw) {
-        uint32_t e[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int i = i0 + j * nw < 64 ? i0 + j * nw : 0;
-          e[j] = (uint32_t)codes[4 * (i & 3) + (lane >> 4)] | ((uint32_t)codes[i >> 2] << 16);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int i = i0 + j * nw;
-          if (i < 64) lut[(16 * (i >> 2) + 4 * (i & 3) + (lane >> 4)) * 16 + (lane & 15)] = make_uint4(e[j], e[j], e[j], e[j]);
-        }
-      }
+      // ---- (4) nibble-pair LUT (from registers, no LDS reads) ----
+      build_pair_lut<SPECTRA_FMT_NF4>(smem, wave, nw, lane);
       __syncthreads();  // LUT complete
     }
 
@@ -530,8 +494,7 @@ int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_
   p.off_xe = red_bytes;
   p.off_ve = (red_bytes + (uint32_t)ecap * (uint32_t)(2 * mp) + 15u) & ~15u;
   p.ecap = ecap;
-  p.off_codes = base;
-  p.off_rp = base + 8 * 32;
+  p.off_rp = base;
   p.off_bias = (p.off_rp + (uint32_t)(16 * pl.T + 1) * 4 + 15u) & ~15u;
   const uint32_t lds = p.off_bias + (uint32_t)(16 * pl.T) * 4;
   if (lds > 163840) return fail(SPECTRA_ERR_UNSUPPORTED, "small-batch LDS plan too large");
