@@ -109,20 +109,54 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 // wave-instructions of 1 KB (lane >> 4 picks the row, lane & 15 the 16-byte chunk:
 // conflict-free).  The high code is wave-uniform (scalar work) and the low code one of
 // four per lane, so the build reads no LDS and selects nothing per entry.
+// fp16 bits of the 16 codes, two per dword (code 2i in the low half): NF4 levels, and the
+// integers 0..15 (Format A)
+constexpr uint32_t kNf4CodePairs[8] = {0xb992bc00u, 0xb652b833u, 0xb1eab48du, 0x0000add4u,
+                                       0x31262d18u, 0x356833e0u, 0x3880370du, 0x3c0039c9u};
+constexpr uint32_t kIntCodePairs[8] = {0x3c000000u, 0x42004000u, 0x45004400u, 0x47004600u,
+                                       0x48804800u, 0x49804900u, 0x4a804a00u, 0x4b804b00u};
+
 template <int FMT>
 __device__ __forceinline__ void build_pair_lut(uint8_t* smem, int wave, int nwaves, int lane) {
-  auto code = [](int i) -> uint32_t { return FMT == SPECTRA_FMT_NF4 ? nf4_f16_bits(i) : f2h((float)i); };
+  const uint32_t* pairs = FMT == SPECTRA_FMT_NF4 ? kNf4CodePairs : kIntCodePairs;
+  // low code 4 c + j (j = lane >> 4): bytes 2j, 2j + 1 of the dword pair (2c, 2c + 1)
+  const uint32_t j2 = (uint32_t)(lane >> 4) * 2u;
+  const uint32_t sel = 0x0c0c0000u | ((j2 + 1u) << 8) | j2;
   uint32_t lo4[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) lo4[c] = code(4 * c + (lane >> 4));
+  for (int c = 0; c < 4; ++c) lo4[c] = __builtin_amdgcn_perm(pairs[2 * c + 1], pairs[2 * c], sel);
   uint4* lut = (uint4*)smem;
   for (int h = wave; h < 16; h += nwaves) {
-    const uint32_t hb = code(h) << 16;
+    // the high code (wave-uniform): code h sits in lo4[h >> 2] of lane 16 (h & 3)
+    const int hq = h >> 2;
+    const uint32_t src = hq == 0 ? lo4[0] : hq == 1 ? lo4[1] : hq == 2 ? lo4[2] : lo4[3];
+    const uint32_t hb = (uint32_t)__builtin_amdgcn_readlane((int)src, 16 * (h & 3)) << 16;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const uint32_t e = lo4[c] | hb;
       lut[(16 * h + 4 * c + (lane >> 4)) * 16 + (lane & 15)] = make_uint4(e, e, e, e);
     }
+  }
+}
+
+// Load through a wave-uniform base plus a 32-bit per-lane byte offset: the global_load
+// saddr form (base in SGPRs, offset in one VGPR), with no per-lane 64-bit address math.
+template <typename T>
+__device__ __forceinline__ T load_at(const void* base, uint32_t byte_off) {
+  typedef const __attribute__((address_space(1))) uint8_t* gbyte_t;
+  typedef const __attribute__((address_space(1))) T* gT_t;
+  gbyte_t b = (gbyte_t)base;  // global memory (the kernels take device pointers)
+  asm("" : "+s"(b));          // keep the base in SGPRs (no re-association into per-lane math)
+  // loaded as a plain integer vector of the same size (the HIP vector types have no
+  // constructor from a global-address-space reference)
+  if constexpr (sizeof(T) == 16) {
+    typedef uint32_t v4_t __attribute__((ext_vector_type(4)));
+    return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) v4_t*)(b + byte_off));
+  } else if constexpr (sizeof(T) == 8) {
+    typedef uint32_t v2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(T, *(const __attribute__((address_space(1))) v2_t*)(b + byte_off));
+  } else {
+    return *(gT_t)(b + byte_off);
   }
 }
 

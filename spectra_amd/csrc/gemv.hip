@@ -72,7 +72,7 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
     if (fit2 >= 256 && ocap > fit2) ocap = fit2;
   }
   pl->ocap = ocap;
-  off = align16(off + (uint32_t)(ocap * mt * 4));
+  off = align16(off + (uint32_t)((ocap > 0 ? ocap : 1) * mt * 4));  // at least one entry: the per-row reads index it
   pl->lds_bytes = off;
   return off <= 163840;
 }
@@ -92,6 +92,7 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
     return fail(SPECTRA_ERR_UNSUPPORTED, "shape not served by the GEMV family (use the GEMM family)");
   SPECTRA_REQUIRE(w->hadamard_block == 0 || w->hadamard_block <= 512, "GEMV serves hadamard_block <= 512");
   SPECTRA_REQUIRE(ptr_aligned(x, 16) && ldx % 8 == 0, "x must be 16-byte aligned with a row stride multiple of 8");
+  SPECTRA_REQUIRE((int64_t)m * ldx < (int64_t(1) << 30), "x rows must span fewer than 2^30 elements");
   SPECTRA_REQUIRE(ptr_aligned(w->packed, 16) && w->packed_stride % 16 == 0,
                   "packed weights must be 16-byte aligned with a row stride multiple of 16");
   if (csr)
@@ -122,6 +123,7 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
   p.csr_nnz = csr ? (int)w->csr_nnz : 0;
   p.n_out = w->num_outliers; p.ow_dt = w->outlier_w_dtype; p.bias_dt = w->bias_dtype; p.act_dt = act_dtype;
   p.R = pl.R; p.S = pl.S; p.G = pl.G; p.ocap = pl.ocap;
+  p.s_magic = (256 + pl.S - 1) / pl.S;
   p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_part = pl.off_part;
   p.off_rp = pl.off_rp; p.off_bias = pl.off_bias; p.off_oprod = pl.off_oprod;
   p.off_ss = pl.off_ss; p.off_res = pl.off_res;

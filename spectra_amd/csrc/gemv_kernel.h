@@ -63,6 +63,7 @@ struct GemvParams {
   int okind, n_out, ow_dt, bias_dt, act_dt;
   int csr_nnz;
   int R, S, G, ocap;
+  int s_magic;      // ceil(256 / S): wave / S == (wave * s_magic) >> 8 for wave < 8
   uint32_t off_xp, off_xsc, off_part, off_rp, off_bias, off_oprod, off_ss, off_res;
   float out_scale;  // 1/sqrt(hadamard_block) (1 without rotation)
   float inv_n_out;  // 1/n_out (dense outlier columns)
@@ -91,10 +92,10 @@ __device__ __forceinline__ int xp_pos(int k, int marlin) {
   return ((((q >> 6) * 4 + (j >> 2)) * 64 + (q & 63)) * 4 + (j & 3)) * 2 + half;
 }
 
-// Value of the partner lane across lane-logical bit KB of the reflected lane numbering
-// (see reflect_chunk): DPP quad permutes for bits 0 and 1, the half-row and row mirrors
-// for bits 2 and 3 (no LDS), ds_swizzle (32-lane mirror) for bit 4 and a cross-lane
-// permute (64-lane mirror) for bit 5.
+// Value of the partner lane across lane-logical bit KB of the reduction's lane numbering
+// lam = reflect_chunk(lane & 15, 4) | (lane & 48): DPP quad permutes for bits 0 and 1, the
+// half-row and row mirrors for bits 2 and 3, and the VALU row swaps v_permlane16_swap
+// (lane ^ 16) and v_permlane32_swap (lane ^ 32) for bits 4 and 5 -- no LDS traffic.
 template <int KB>
 __device__ __forceinline__ float lane_partner(float v, int lane) {
   const int iv = __builtin_bit_cast(int, v);
@@ -102,8 +103,13 @@ __device__ __forceinline__ float lane_partner(float v, int lane) {
   else if constexpr (KB == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
   else if constexpr (KB == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false));
   else if constexpr (KB == 3) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x140, 0xF, 0xF, false));
-  else if constexpr (KB == 4) return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(iv, 0x7C1F));
-  else return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((63 - lane) << 2, iv));
+  else if constexpr (KB == 4) {  // (v, v) -> rows [v0 v0 v2 v2] / [v1 v1 v3 v3]
+    const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)((lane & 16) ? r[0] : r[1]));
+  } else {  // (v, v) -> halves [lo lo] / [hi hi]
+    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)((lane & 32) ? r[0] : r[1]));
+  }
 }
 
 // Transposed halving reduction of N values per lane across the 64 lanes: at the step on
@@ -279,7 +285,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nwaves = BD >> 6;
-  const int s = wave % p.S, g = wave / p.S;
+  const int g = (wave * p.s_magic) >> 8, s = wave - g * p.S;  // wave / S, wave % S
   const int r0 = blockIdx.x * p.R;
   const int Rw = min(p.R, p.n - r0);
   const int K = p.k;
@@ -297,6 +303,10 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   uint4 xu[PRO == kProSiluMul ? XH : 1][2];   // the u half of a fused gate_up row
   uint4 nwv[PRO == kProRms ? XH : 1][2];      // RMSNorm weights of the half-run (fp16)
   int xm[XH], xq[XH], xcl[XH], xhf[XH];
+  const int bm = (1 << bL) - 1;
+  // block offsets of every slot (BD, hpr) are multiples of 2^bL, so the reflected chunk
+  // inside the block depends on the lane alone: computed once
+  const int rc = reflect_chunk(lane & bm, bL);
 #pragma unroll
   for (int i = 0; i < XH; ++i) {
     const int hd = tid + i * BD;
@@ -304,8 +314,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
 #pragma unroll
     for (int mm = 1; mm < MT; ++mm) m += hd >= mm * hpr ? 1 : 0;
     const int hrr = hd - m * hpr;
-    const int bm = (1 << bL) - 1;
-    const int cl = (hrr & ~bm) | reflect_chunk(hrr & bm, bL);
+    const int cl = (hrr & ~bm) | rc;
     xm[i] = m;
     xq[i] = cl >> 1;
     xcl[i] = cl & bm;  // the bits of the cross-lane stages (their signs)
@@ -314,23 +323,24 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     // padded rows (m >= p.m) and slots past the last half-run read row 0: finite values
     // whose results are never stored
     const bool ok = hd < MT * hpr && m < p.m;
-    const uint16_t* src = (const uint16_t*)p.x + (ok ? (int64_t)m * p.ldx + (int64_t)(cl >> 1) * 32 : 0);
+    // byte offset from the uniform base (the host keeps x within 2^31 bytes)
+    const uint32_t xo = ok ? (uint32_t)(m * p.ldx + (cl >> 1) * 32) * 2u : 0u;
     // waves with no half-run in this slot skip its loads (a wave-uniform branch; the
     // loads come before every other load, so later wait counts are unaffected)
     // (left undefined otherwise: those values are never read, and no copy or wait is
     // needed where the branch joins)
     if (i == 0 || wave * 64 + i * BD < MT * hpr) {
-      const int o0 = p.marlin ? 8 * hf : 16 * hf, o1 = p.marlin ? 16 + 8 * hf : 16 * hf + 8;
-      xr[i][0] = *(const uint4*)(src + o0);
-      xr[i][1] = *(const uint4*)(src + o1);
+      const uint32_t o0 = 2u * (p.marlin ? 8 * hf : 16 * hf), o1 = 2u * (p.marlin ? 16 + 8 * hf : 16 * hf + 8);
+      xr[i][0] = load_at<uint4>(p.x, xo + o0);
+      xr[i][1] = load_at<uint4>(p.x, xo + o1);
       if constexpr (PRO == kProSiluMul) {
-        xu[i][0] = *(const uint4*)(src + K + o0);
-        xu[i][1] = *(const uint4*)(src + K + o1);
+        xu[i][0] = load_at<uint4>(p.x, xo + 2u * K + o0);
+        xu[i][1] = load_at<uint4>(p.x, xo + 2u * K + o1);
       }
       if constexpr (PRO == kProRms) {
-        const uint16_t* nw = p.nw + (ok ? (int64_t)(cl >> 1) * 32 : 0);
-        nwv[i][0] = *(const uint4*)(nw + o0);
-        nwv[i][1] = *(const uint4*)(nw + o1);
+        const uint32_t no = ok ? (uint32_t)(cl >> 1) * 64u : 0u;
+        nwv[i][0] = load_at<uint4>(p.nw, no + o0);
+        nwv[i][1] = load_at<uint4>(p.nw, no + o1);
       }
     }
   }
@@ -342,7 +352,8 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   // values are read out of the lanes where they are needed, after the activation work.)
   int rpe = 0;
   if constexpr (FMT == SPECTRA_FMT_NF4)
-    rpe = *(p.okind == SPECTRA_OUTLIERS_CSR ? p.rowptr + r0 + (lane == 1 ? Rw : 0) : (const int32_t*)p.packed);
+    rpe = p.okind == SPECTRA_OUTLIERS_CSR ? load_at<int>(p.rowptr + r0, lane == 1 ? 4u * Rw : 0u)
+                                          : load_at<int>(p.packed, 0u);
 
   // ---------------- (2) the weight stream: every row of this wave, up front ----------------
   const int kb = s * 2048 + lane * 32;  // first k of this lane (one 32-run)
@@ -354,46 +365,51 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   uint8_t zq[RPW];
   bool wok[RPW];
   const int kk = kvalid ? kb : 0;
+  // Every address below is a wave-uniform row base (scalar arithmetic) plus one 32-bit
+  // per-lane byte offset shared by all rows: no per-lane 64-bit address math per load.
+  const uint32_t wo = (uint32_t)(kk >> 1);
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const int rl = g + i * p.G;
-    // the row is wave-uniform (its address is scalar arithmetic); only k is per lane
     const bool rok = rl < Rw;
     wok[i] = rok && kvalid;
     const int64_t row = r0 + (rok ? rl : 0);
-    wq[i] = *(const uint4*)(p.packed + row * p.ldp + (kk >> 1));
-    if (FMT == SPECTRA_FMT_ASYM_G32) zq[i] = p.zeros[row * p.ldz + (kk >> 5)];
+    wq[i] = load_at<uint4>(p.packed + row * p.ldp, wo);
+    if (FMT == SPECTRA_FMT_ASYM_G32) zq[i] = load_at<uint8_t>(p.zeros + row * p.ldz, (uint32_t)(kk >> 5));
   }
   // Scales after the weights.  With blocks of 64 or more, lanes 2j and 2j+1 share a
   // block: one load serves rows 2t (even lanes) and 2t+1 (odd lanes), and a DPP quad
   // broadcast hands each lane its row's value (in the stream).
   constexpr bool pair_sc = FMT == SPECTRA_FMT_NF4;  // the host serves NF4 blocks >= 64 only
-  const int64_t sk = kk >> p.gshift;
+  const uint32_t so = (uint32_t)(kk >> p.gshift) * 2u;
   if constexpr (pair_sc) {
+    const uint16_t* sbase = p.scales + (int64_t)r0 * p.lds;
+    const bool odd = lane & 1;
 #pragma unroll
     for (int t = 0; t < RP2; ++t) {
-      const int i = 2 * t + 1 < RPW ? 2 * t + (lane & 1) : 2 * t;
-      const int rl = g + i * p.G;
-      const int64_t row = r0 + (rl < Rw ? rl : 0);
-      sc2[t] = p.scales[row * p.lds + sk];
+      const int ie = 2 * t, io = 2 * t + 1 < RPW ? 2 * t + 1 : 2 * t;
+      const int rle = g + ie * p.G, rlo = g + io * p.G;
+      const uint32_t oe = __builtin_amdgcn_readfirstlane((uint32_t)((rle < Rw ? rle : 0) * p.lds) * 2u);
+      const uint32_t oo = __builtin_amdgcn_readfirstlane((uint32_t)((rlo < Rw ? rlo : 0) * p.lds) * 2u);
+      sc2[t] = load_at<uint16_t>(sbase, (odd ? oo : oe) + so);
     }
   } else {
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       const int rl = g + i * p.G;
       const int64_t row = r0 + (rl < Rw ? rl : 0);
-      sc[i] = p.scales[row * p.lds + sk];
+      sc[i] = load_at<uint16_t>(p.scales + row * p.lds, so);
     }
   }
 
   // ---------------- (2b) row pointers and bias: consumed after the stream ----------------
   int rp_v = 0;  // row pointers of this workgroup's rows, for the per-row phase
-  if (p.okind == SPECTRA_OUTLIERS_CSR) rp_v = p.rowptr[r0 + min(tid, Rw)];
+  if (p.okind == SPECTRA_OUTLIERS_CSR) rp_v = load_at<int>(p.rowptr + r0, 4u * (uint32_t)min(tid, Rw));
   uint32_t bias_raw = 0;
   if (p.bias != nullptr) {
-    const int64_t bi = r0 + (tid < Rw ? tid : 0);
-    if (p.bias_dt == SPECTRA_F32) bias_raw = ((const uint32_t*)p.bias)[bi];
-    else bias_raw = ((const uint16_t*)p.bias)[bi];
+    const uint32_t bi = (uint32_t)(tid < Rw ? tid : 0);
+    if (p.bias_dt == SPECTRA_F32) bias_raw = load_at<uint32_t>((const uint32_t*)p.bias + r0, 4u * bi);
+    else bias_raw = load_at<uint16_t>((const uint16_t*)p.bias + r0, 2u * bi);
   }
   // residual of output (row tid / Rw, column r0 + tid % Rw), read before any output is written
   uint16_t res_raw = 0;
@@ -506,14 +522,16 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
   uint2 ovv;
   int obase;  // el of this thread's first entry
   if constexpr (FMT == SPECTRA_FMT_NF4) {
-    const int g4 = (e0 & ~3) + 4 * tid;
-    // groups past this workgroup's entries (or the array end) re-read group 0, a cached
-    // line, so the stream carries no CSR bytes beyond the workgroup's own
+    const int g0 = e0 & ~3, g4 = g0 + 4 * tid;
+    // groups past this workgroup's entries (or the array end) re-read the first group (the
+    // workgroup's own, or the array's when that one is partial), a cached line, so the
+    // stream carries no CSR bytes beyond the workgroup's own
     // (arrays of fewer than 4 entries are never read this way: olim is 0 then)
     const bool big = has_o && p.csr_nnz >= 4;
-    const int gc = (big && g4 < e1 && g4 + 4 <= p.csr_nnz) ? g4 : 0;
-    ocv = *(big ? (const int4*)(p.ccol + gc) : (const int4*)p.packed);
-    ovv = *(big ? (const uint2*)(p.cval + gc) : (const uint2*)p.packed);
+    const bool ok4 = big && g4 < e1 && g4 + 4 <= p.csr_nnz;
+    const int gb = big && g0 + 4 <= p.csr_nnz ? g0 : 0;  // wave-uniform base group
+    ocv = big ? load_at<int4>(p.ccol + gb, ok4 ? 4u * (uint32_t)(g4 - gb) : 0u) : load_at<int4>(p.packed, 0u);
+    ovv = big ? load_at<uint2>(p.cval + gb, ok4 ? 2u * (uint32_t)(g4 - gb) : 0u) : load_at<uint2>(p.packed, 0u);
     obase = g4 - e0;
   } else {
     const int n_out = p.n_out > 0 ? p.n_out : 1;
@@ -523,8 +541,9 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
     int jj = ei - r * n_out;
     r = jj < 0 ? r - 1 : (jj >= n_out ? r + 1 : r);
     jj = ei - r * n_out;
-    ocv.x = *(has_o ? (const int*)(p.oidx + jj) : (const int*)p.packed);
-    ovv.x = *(has_o ? (const uint16_t*)p.ow + (int64_t)(r0 + r) * p.ldow + jj : (const uint16_t*)p.packed);
+    ocv.x = has_o ? load_at<int>(p.oidx, 8u * (uint32_t)jj) : load_at<int>(p.packed, 0u);
+    ovv.x = has_o ? load_at<uint16_t>((const uint16_t*)p.ow + (int64_t)r0 * p.ldow, 2u * (uint32_t)(r * p.ldow + jj))
+                  : load_at<uint16_t>(p.packed, 0u);
     obase = tid;
   }
 
@@ -601,7 +620,7 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
 
   // ---------------- (8) transposed halving reduction across the wave ----------------
   int idx = 0;
-  const int lam = reflect_chunk(lane, 6);
+  const int lam = reflect_chunk(lane & 15, 4) | (lane & 48);
   transposed_reduce<VP, 0>(vals, lane, lam, idx);
   // every lane now holds the total number idx (set by the low log2(VP) bits of lam); the
   // lanes with lam < VP write them
@@ -672,7 +691,20 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
       for (int m = 0; m < MT; ++m) {
         if (m >= p.m) break;
         float v = (gl < p.S && rv) ? part[(rr * p.S + gl) * MT + m] : 0.0f;
+        // staged entries gl, gl + 16, gl + 32, gl + 48 of the row: four reads issued together
+        // (in-bounds dummy index otherwise: the plan always holds one staged entry)
+        float o[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int el = lo + gl + 16 * u;
+          const bool st = el < hi && el < olim;
+          const float t = oprod[(st ? el : 0) * MT + m];
+          o[u] = st ? t : 0.0f;
+        }
+        v += (o[0] + o[1]) + (o[2] + o[3]);
+        // the rest: entries past the first 64 of the row, and any not staged in LDS
         for (int el = lo + gl; el < hi; el += 16) {
+          if (el < lo + 64 && el < olim) continue;
           if (el < olim) {
             v += oprod[el * MT + m];
           } else {  // beyond the staged entries: read the side tensor directly
