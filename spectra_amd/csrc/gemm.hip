@@ -33,7 +33,8 @@ constexpr int kGemmWaves = 8;  // two per SIMD (four waves of 128 x 128 measured
 constexpr int kRowH = 32;         // fp16 per LDS tile row (64 bytes, four 16-byte chunks, swizzled)
 constexpr int kPrepThreads = 256;
 constexpr int kGLut = 65536;      // lane-replicated nibble-pair LUT at LDS address 0
-constexpr int kWin = 4;           // outlier entries prefetched per weight row
+constexpr int kOGroup = 16;       // weight rows per outlier step list
+constexpr int kOListThreads = 256;
 
 // 16-byte chunk c of tile row r sits at chunk c ^ tile_swz(r): with 64-byte rows, every
 // 8-lane (32 banks) or 16-lane (64 banks) phase of the tile stores (two or four lanes per
@@ -225,6 +226,11 @@ struct GemmParams {
   int gshift, marlin, okind, n_out, ow_dt, bias_dt, act_dt;
   int ksplit, ksteps;  // K splits (blockIdx.z) and kBK-steps per split
   float* part;         // ksplit > 1: fp32 partials [ksplit][m][n]
+  // outlier step lists (gemm_outlier_lists_kernel): ostart[g][s] = first entry of row
+  // group g in K-step s (s = 0 .. K / kBK, the last = the group's end); oent = entries
+  const int32_t* ostart;
+  const uint32_t* oent;
+  int ogroups;
 };
 
 template <int FMT, int BN, int NW>
@@ -261,49 +267,40 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   const uint16_t* ssrc = p.scales + (int64_t)wrow * p.lds;
   const uint8_t* zsrc = FMT == SPECTRA_FMT_ASYM_G32 ? p.zeros + (int64_t)wrow * p.ldz : nullptr;
 
-  // ---- outlier window of this thread's row (CSR cursor, or the shared column list) ----
-  int cur = 0, cend = 0;
-  if (p.okind == SPECTRA_OUTLIERS_CSR) {
-    cur = p.rowptr[wrow];
-    cend = p.rowptr[wrow + 1];
-  } else if (p.okind == SPECTRA_OUTLIERS_COLUMNS) {
-    cend = p.n_out;
-  }
-  if (ks > 0 && p.okind != SPECTRA_OUTLIERS_NONE) {  // first entry at or past this split's K range
-    const int kfirst = ks * kBK;
-    int lo = cur, hi = cend;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      const int c = p.okind == SPECTRA_OUTLIERS_CSR ? p.ccol[mid] : (int)p.oidx[mid];
-      if (c < kfirst) lo = mid + 1;
-      else hi = mid;
-    }
-    cur = lo;
-  }
-  // the next kWin entries of the row in a register queue (q[0] = next); consuming one
-  // shifts the queue and loads the entry kWin further, which is read kWin entries later
-  int qc[kWin];
-  uint16_t qv[kWin];
-  int qe = cur + kWin;  // entry index of the next load
-  auto fetch = [&](int e, int& c, uint16_t& v) __attribute__((always_inline)) {
-    const bool ok = e < cend;
-    const int ei = ok ? e : 0;
-    if (p.okind == SPECTRA_OUTLIERS_CSR) {
-      c = ok ? p.ccol[ei] : 0x7fffffff;
-      v = p.cval[ei];
-    } else {
-      c = ok ? (int)p.oidx[ei] : 0x7fffffff;
-      v = f2h(load_elem(p.ow, (int64_t)wrow * p.ldow + ei, p.ow_dt));
-    }
+  // ---- outlier step lists: this wave decodes tile rows [wlo, wlo + 64 / TPR), one (TPR = 4)
+  //      or two (TPR = 2) groups of kOGroup; the lanes of half h of a two-group wave serve
+  //      group h.  Each step a lane reads one entry of its group's list for the step (two
+  //      steps ahead, like the tiles), and after the decode the lanes holding an entry
+  //      write its value over the decoded position (the code there is exactly 0).  The
+  //      group's start offsets are read one stage earlier still. ----
+  constexpr int OGW = 64 / TPR / kOGroup;  // groups per wave: 2 or 1
+  constexpr int OCAP = 64 / OGW;           // entries of a group one read covers: 32 or 64
+  const bool has_o = p.okind != SPECTRA_OUTLIERS_NONE;
+  const int wlo = 64 * wave / TPR;          // first tile row this wave decodes (wave-uniform)
+  const int oh = OGW == 2 ? lane >> 5 : 0;  // this lane's group inside the wave
+  const int oln = lane & (OCAP - 1);        // this lane's slot in the group's list
+  // (groups past the last row are clamped: those tile rows are never stored)
+  const int og = min((n0 + wlo) / kOGroup + oh, p.ogroups - 1);
+  const int KS = K / kBK;
+  const int32_t* ost = p.ostart + (has_o ? (int64_t)og * (KS + 1) : 0);
+  int oo0x = 0, oo0y = 0, oo1x = 0, oo1y = 0;  // (first, end) entry of the step a stage loads next
+  int oc0x = 0, oc0y = 0, oc1x = 0, oc1y = 0;  // ... of the step a stage holds
+  uint32_t oe0 = 0, oe1 = 0;                   // this lane's entry of that step
+  // (unconditional reads: without outliers the host points both arrays at a readable
+  // dummy and index 0 is read; past the split's end the index stays in bounds, unused)
+  auto ooffs = [&](int& ox, int& oy, int step) __attribute__((always_inline)) {
+    const int gi = has_o ? min(ks + step, KS - 1) : 0;
+    ox = ost[gi];
+    oy = ost[gi + 1];
   };
-#pragma unroll
-  for (int q = 0; q < kWin; ++q) {
-    qc[q] = 0x7fffffff;
-    qv[q] = 0;
-  }
-  if (p.okind != SPECTRA_OUTLIERS_NONE)
-#pragma unroll
-    for (int q = 0; q < kWin; ++q) fetch(cur + q, qc[q], qv[q]);
+  // the stage's entry for `step` (offsets read a stage earlier), then the offsets of step + 2
+  auto oload = [&](int& oox, int& ooy, int& ocx, int& ocy, uint32_t& oe, int step) __attribute__((always_inline)) {
+    ocx = oox;
+    ocy = ooy;
+    const int e = oox + oln;
+    oe = p.oent[has_o && e < ooy ? e : 0];
+    ooffs(oox, ooy, step + 2);
+  };
 
   // ---- global -> register staging, two steps ahead ----
   // (two named register stages; an array of them would be placed in scratch memory)
@@ -339,8 +336,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   const uint32_t lanebits = (uint32_t)lane << 2;
 
   // ---- register stage -> LDS buffer: activations as loaded, weights decoded ----
-  auto store = [&](u32x4_t ga, u32x4_t gb, u32x4_t gc, u32x4_t gd, u32x4_t gw, uint16_t gs, uint8_t gz, int step,
-                   int buf) __attribute__((always_inline)) {
+  auto store = [&](u32x4_t ga, u32x4_t gb, u32x4_t gc, u32x4_t gd, u32x4_t gw, uint16_t gs, uint8_t gz, int buf,
+                   int ocx, int ocy, uint32_t oe) __attribute__((always_inline)) {
     uint16_t* arow_l = As + (buf * kBM + ar) * kRowH;
     const int asw = tile_swz(ar);
     *(u32x4_t*)(arow_l + 8 * ((AU * ah) ^ asw)) = ga;
@@ -370,25 +367,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
 #pragma unroll
     for (int u = 0; u < BPT / 4; ++u)
       *(uint4*)(wrow_l + 8 * ((wc0 + u) ^ wsw)) = make_uint4(d[4 * u], d[4 * u + 1], d[4 * u + 2], d[4 * u + 3]);
-    // outliers of this row inside the step: the queue head while it lies below the
-    // step's end (ascending columns); the same thread wrote the decoded values above, so
-    // program order suffices
-    if (p.okind != SPECTRA_OUTLIERS_NONE) {
-      const int klo = (ks + step) * kBK, khi = klo + kBK;
-      while (qc[0] < khi) {
-        const int kk = qc[0] - klo;
-        const int jb = p.marlin ? (kk & 15) : (kk >> 1), h = p.marlin ? (kk >> 4) : (kk & 1);
-        if (kk >= 0 && jb >= wb0 && jb < wb0 + BPT) {
-          const int e = 2 * jb + h;  // fp16 index in the step's row
-          wrow_l[8 * ((e >> 3) ^ wsw) + (e & 7)] = qv[0];
-        }
-#pragma unroll
-        for (int q = 0; q + 1 < kWin; ++q) {
-          qc[q] = qc[q + 1];
-          qv[q] = qv[q + 1];
-        }
-        fetch(qe, qc[kWin - 1], qv[kWin - 1]);
-        ++qe;
+    // outliers of the step: every decode write of the wave precedes these (program order)
+    if (has_o) {
+      // the entry carries its fp16 index inside the group's tile rows (swizzle included)
+      uint16_t* grp_l = Ws + (buf * BN + wlo + kOGroup * oh) * kRowH;
+      auto put = [&](uint32_t v) __attribute__((always_inline)) { grp_l[v >> 16] = (uint16_t)v; };
+      if (ocx + oln < ocy) put(oe);
+      // a group with more entries in the step than one read covers (far beyond the
+      // format's ratios): the rest read directly, and no read left in flight after
+      if (__builtin_amdgcn_ballot_w64(ocy - ocx > OCAP) != 0) {
+        for (int e = ocx + OCAP + oln; e < ocy; e += OCAP) put(p.oent[e]);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
       }
     }
   };
@@ -401,11 +390,23 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  load(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 0);
-  if (nk > 1) load(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, 1);
-  __syncthreads();  // LUT and code tables
-  store(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 0, 0);
-  if (nk > 2) load(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 2);
+  // Every load is issued unconditionally (steps past the split re-read its last one), so
+  // the loads in flight are the same on every path and each wait covers exactly its stage.
+  auto load0 = [&](int step) __attribute__((always_inline)) {
+    load(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, min(step, nk - 1));
+    oload(oo0x, oo0y, oc0x, oc0y, oe0, step);
+  };
+  auto load1 = [&](int step) __attribute__((always_inline)) {
+    load(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, min(step, nk - 1));
+    oload(oo1x, oo1y, oc1x, oc1y, oe1, step);
+  };
+  ooffs(oo0x, oo0y, 0);
+  ooffs(oo1x, oo1y, 1);
+  load0(0);
+  load1(1);
+  __syncthreads();  // LUT
+  store(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 0, oc0x, oc0y, oe0);
+  load0(2);
   __syncthreads();
 
   const int arow = wm * 128 + (lane & 31), brow = wn * WN + (lane & 31), kq = 8 * (lane >> 5);
@@ -430,14 +431,13 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   // two steps per iteration so the register stages have static indices
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
-    store(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, kt + 1, 1);  // step kt+1 -> buffer 1 (buffer 1 free since the last barrier)
-    if (kt + 3 < nk) load(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, kt + 3);
+    // step kt+1 -> buffer 1 (buffer 1 free since the last barrier)
+    store(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, 1, oc1x, oc1y, oe1);
+    load1(kt + 3);
     mfma_step(0);                          // step kt from buffer 0
     __syncthreads();
-    if (kt + 2 < nk) {
-      store(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, kt + 2, 0);
-      if (kt + 4 < nk) load(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, kt + 4);
-    }
+    if (kt + 2 < nk) store(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 0, oc0x, oc0y, oe0);
+    load0(kt + 4);
     mfma_step(1);
     __syncthreads();
   }
@@ -504,27 +504,103 @@ __global__ void __launch_bounds__(kRedThreads) splitk_reduce_kernel(const float*
   }
 }
 
+// Outlier step lists for the GEMM, one workgroup per group of kOGroup weight rows: the
+// group's entries (CSR, or the outlier columns of every row) bucketed by K-step with a
+// counting sort in LDS.  ostart[g][s] = first entry of step s (s = 0 .. KS, the last = the
+// group's end), oent[e] = (fp16 index inside the group's 16 LDS tile rows, swizzle applied)
+// << 16 | fp16 value bits -- the tile rows of a group share their swizzle pattern modulo 16,
+// so the position is known here.  The order inside a step is arbitrary: each entry owns its
+// position in the tile.
+__global__ void __launch_bounds__(kOListThreads) gemm_outlier_lists_kernel(
+    int okind, const int32_t* __restrict__ rowptr, const int32_t* __restrict__ ccol,
+    const uint16_t* __restrict__ cval, const int64_t* __restrict__ oidx, const void* __restrict__ ow,
+    int64_t ldow, int ow_dt, int n_out, int n, int KS, int marlin, int32_t* __restrict__ ostart,
+    uint32_t* __restrict__ oent) {
+  extern __shared__ int32_t cnt[];  // [KS + 1]: counts, then cursors
+  __shared__ int32_t wtot[kOListThreads / 64];
+  const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const bool csr = okind == SPECTRA_OUTLIERS_CSR;
+  const int r0 = g * kOGroup, r1 = min(r0 + kOGroup, n);
+  const int base = csr ? rowptr[r0] : r0 * n_out;  // the group's first entry
+  for (int t = tid; t <= KS; t += kOListThreads) cnt[t] = 0;
+  __syncthreads();
+  for (int r = r0; r < r1; ++r) {
+    const int e0 = csr ? rowptr[r] : 0, e1 = csr ? rowptr[r + 1] : n_out;
+    for (int e = e0 + tid; e < e1; e += kOListThreads) {
+      const int c = csr ? ccol[e] : (int)oidx[e];
+      if ((unsigned)c < (unsigned)(KS * kBK)) atomicAdd(&cnt[c / kBK], 1);  // (columns outside K: dropped)
+    }
+  }
+  __syncthreads();
+  // exclusive scan of cnt[0, KS): thread t owns a run of `per` consecutive steps
+  const int per = (KS + kOListThreads - 1) / kOListThreads;
+  const int lo = min(tid * per, KS), hi = min(lo + per, KS);
+  int run = 0;
+  for (int t = lo; t < hi; ++t) run += cnt[t];
+  int inc = run;  // inclusive scan over the wave
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(inc, o, 64);
+    if (lane >= o) inc += v;
+  }
+  if (lane == 63) wtot[wv] = inc;
+  __syncthreads();
+  int pre = inc - run;
+  for (int w = 0; w < wv; ++w) pre += wtot[w];
+  int32_t* og = ostart + (int64_t)g * (KS + 1);
+  for (int t = lo; t < hi; ++t) {
+    const int c = cnt[t];
+    cnt[t] = pre;  // cursor
+    og[t] = base + pre;
+    pre += c;
+  }
+  if (tid == kOListThreads - 1) og[KS] = base + pre;  // the last thread's runs end at KS
+  __syncthreads();
+  for (int r = r0; r < r1; ++r) {
+    const int e0 = csr ? rowptr[r] : 0, e1 = csr ? rowptr[r + 1] : n_out;
+    for (int e = e0 + tid; e < e1; e += kOListThreads) {
+      const int c = csr ? ccol[e] : (int)oidx[e];
+      if ((unsigned)c >= (unsigned)(KS * kBK)) continue;
+      const uint32_t v = csr ? cval[e] : f2h(load_elem(ow, (int64_t)r * ldow + e, ow_dt));
+      const int pos = atomicAdd(&cnt[c / kBK], 1);
+      const int rr = r - r0, cs = c % kBK;
+      const int jb = marlin ? (cs & 15) : (cs >> 1), h = marlin ? (cs >> 4) : (cs & 1);
+      const int e2 = 2 * jb + h;  // fp16 index in the step's decoded row (packed-byte pair order)
+      const int off = rr * kRowH + 8 * ((e2 >> 3) ^ tile_swz(rr)) + (e2 & 7);
+      oent[base + pos] = ((uint32_t)off << 16) | v;
+    }
+  }
+}
+
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// tile plan: 256 x BN tiles (BN 256 when they fill the GPU), and K splits when even the
-// 128-wide tiles leave most CUs idle (each split >= 8 steps of 32; fp32 partials, a reduce)
+// tile plan: 256 x 256 tiles once there are at least 64 of them (twice the MFMA work per
+// step of the 128-wide tile, whose fixed per-step work weighs double), 256 x 128 below that,
+// and K splits while the tiles fill fewer than 256 CUs (each split >= 8 steps of 32; fp32
+// partials, a fixed-order reduce)
 struct GemmPlan {
   int BN, mt, nt, ksplit, ksteps;
 };
 static GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
   GemmPlan g;
   g.mt = (int)((m + kBM - 1) / kBM);
-  const bool wide = (int64_t)g.mt * ((n + 255) / 256) >= 256;
+  const bool wide = (int64_t)g.mt * ((n + 255) / 256) >= 64;
   g.BN = wide ? 256 : 128;
   g.nt = (int)((n + g.BN - 1) / g.BN);
   const int tiles = g.mt * g.nt;
   const int steps = (int)(k / kBK);
-  int ks = tiles < 128 && n % 4 == 0 ? 256 / tiles : 1;
+  int ks = tiles < 256 && n % 4 == 0 ? 256 / tiles : 1;
   ks = ks > 8 ? 8 : ks;
   while (ks > 1 && steps / ks < 8) --ks;
   g.ksteps = (steps + ks - 1) / ks;
   g.ksplit = (steps + g.ksteps - 1) / g.ksteps;
   return g;
+}
+
+// entries the outlier step lists hold (0: none)
+static int64_t outlier_entries(const spectra_qweight_t* w) {
+  if (w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0) return w->csr_nnz;
+  if (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS && w->num_outliers > 0) return w->n * (int64_t)w->num_outliers;
+  return 0;
 }
 
 // skinny.hip: the small-batch MFMA family (2 <= m <= 16)
@@ -540,8 +616,12 @@ extern "C" size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64
   (void)act_dtype;
   if (w == nullptr || m <= 0) return 0;
   const GemmPlan g = plan_gemm(m, w->n, w->k);
-  const size_t gemm = align256((size_t)m * (size_t)w->k * 2) + align256((size_t)m * 4) +
-                      (g.ksplit > 1 ? align256((size_t)g.ksplit * m * w->n * 4) : 0);
+  size_t gemm = align256((size_t)m * (size_t)w->k * 2) + align256((size_t)m * 4) +
+                (g.ksplit > 1 ? align256((size_t)g.ksplit * m * w->n * 4) : 0);
+  const int64_t nent = outlier_entries(w);
+  if (nent > 0)  // outlier step lists
+    gemm += align256((size_t)((w->n + kOGroup - 1) / kOGroup) * (size_t)(w->k / kBK + 1) * 4) +
+            align256((size_t)nent * 4);
   const size_t small = skinny_workspace(w, m);
   return gemm > small ? gemm : small;
 }
@@ -616,6 +696,28 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   p.ksplit = g.ksplit;
   p.ksteps = g.ksteps;
   p.part = g.ksplit > 1 ? (float*)((uint8_t*)fexp + align256((size_t)m * 4)) : nullptr;
+  // outlier step lists (after the partials in the workspace), built for this call
+  const int64_t nent = outlier_entries(w);
+  const int KS = (int)(w->k / kBK);
+  p.ogroups = (int)((w->n + kOGroup - 1) / kOGroup);
+  if (nent > 0) {
+    if (nent >= (int64_t(1) << 31)) return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family serves < 2^31 outlier entries");
+    uint8_t* lists = (uint8_t*)fexp + align256((size_t)m * 4) +
+                     (g.ksplit > 1 ? align256((size_t)g.ksplit * m * w->n * 4) : 0);
+    int32_t* ostart = (int32_t*)lists;
+    uint32_t* oent = (uint32_t*)(lists + align256((size_t)p.ogroups * (size_t)(KS + 1) * 4));
+    p.ostart = ostart;
+    p.oent = oent;
+    hipLaunchKernelGGL(gemm_outlier_lists_kernel, dim3((unsigned)p.ogroups), dim3(kOListThreads),
+                       (size_t)(KS + 1) * 4, s, p.okind, w->csr_rowptr, w->csr_col, w->csr_val, w->outlier_idx,
+                       w->outlier_w, w->outlier_w_stride, w->outlier_w_dtype, (int)w->num_outliers, (int)w->n, KS,
+                       p.marlin, ostart, oent);
+    SPECTRA_HIP_CHECK(hipGetLastError());
+  } else {
+    p.okind = SPECTRA_OUTLIERS_NONE;
+    p.ostart = (const int32_t*)a16;  // readable dummies: the kernel reads index 0 and 1 only
+    p.oent = (const uint32_t*)a16;
+  }
   const size_t lds = (size_t)kGLut + (size_t)2 * (kBM + BN) * kRowH * 2 + kBM * 4;
   dim3 grid((unsigned)g.nt, (unsigned)g.mt, (unsigned)g.ksplit);
   const void* kern;

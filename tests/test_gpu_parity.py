@@ -445,11 +445,16 @@ def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
         print(f"{name} m={m}: max-abs {err:.3e} rel-L2 {rel:.3e}", flush=True)
 
 
-def test_prefill_gemm_against_torch_fp32(hip):
-    """cfg4 shape class (K=4096 -> N=14336, M=512 here): fp32 torch reference on the
-    GPU built from the bit-exact dequant and FWHT kernels, plus oracle rows."""
+@pytest.mark.parametrize("m,k,n", [
+    (512, 4096, 14336),   # 256-wide tiles, K split in two
+    (2048, 14336, 4096),  # cfg4's second GEMM at full size: 256-wide tiles, K split in two
+    (512, 8192, 3072),    # 128-wide tiles, K split in four
+])
+def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
+    """cfg4 shape class: fp32 torch reference on the GPU built from the bit-exact dequant
+    and FWHT kernels (0.5% CSR outliers, bf16 activations)."""
+    case(m=m, k=k, n=n)
     g = torch.Generator().manual_seed(4)
-    m, k, n = 512, 4096, 14336
     w = (torch.randn(n, k, generator=g) * 0.02).half()
     nnz = int(round(0.005 * n * k))
     pos = torch.randperm(n * k, generator=g)[:nnz]
