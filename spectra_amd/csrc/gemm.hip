@@ -6,17 +6,20 @@
 //    fp16 rounding.  The row is stored in packed-byte pair order: position 2 b + h holds
 //    the element that nibble h of packed byte b multiplies, so a decoded byte (an fp16
 //    code pair) and the activations it meets sit at the same positions.
-// 2. gemm_kernel<FMT, BN>: a 256 x BN output tile per workgroup, K step 32, 8 waves of
-//    128 x BN/4 (v_mfma_f32_32x32x16_f16, fp32 accumulators; two waves per SIMD so one
-//    wave's decode and copies overlap the other's MFMAs).  Each step one thread
-//    decodes half (BN = 256) or a quarter (BN = 128) of one weight row's 16-byte run through the
-//    lane-replicated nibble-pair LUT, applies the block scale (Format A: (q - z) * s) with
-//    one fp16 rounding, and writes the row into LDS; CSR outliers / outlier columns of
-//    the run overwrite their positions there (the quantized code there is exactly 0).
-//    Activation and weight tiles are double-buffered in LDS with one barrier per step;
-//    global loads run two steps ahead, so the next step's decode and the copies overlap
-//    this step's MFMAs.  The epilogue undoes the row scale, adds the bias in fp32 and
-//    rounds once.
+// 2. gemm_outlier_lists_kernel (when the weight has outliers): each group of 16 weight rows'
+//    CSR entries / outlier columns bucketed by K-step, with each entry's position in the
+//    decoded LDS tile precomputed.
+// 3. gemm_kernel<FMT, BN>: a 256 x BN output tile per workgroup, K step 32, 8 waves of
+//    128 x BN/4 (v_mfma_f32_32x32x16_f16, fp32 accumulators, two waves per SIMD).  Each step
+//    one thread decodes half (BN = 256) or a quarter (BN = 128) of one weight row's 16-byte
+//    run through the lane-replicated nibble-pair LUT, applies the block scale (Format A:
+//    (q - z) * s) with one fp16 rounding, and writes the row into LDS; the lanes holding one
+//    of the step's outlier entries then write its value over its position (the quantized
+//    code there is exactly 0).  Activation and weight tiles are double-buffered in LDS with
+//    one barrier per step; global loads (tiles, outlier entries) run two steps ahead, and
+//    each half-step interleaves the MFMAs of one step with the decode, tile writes and
+//    loads of the next (scheduling groups), so the matrix pipe is fed while the wave
+//    decodes.  The epilogue undoes the row scale, adds the bias in fp32 and rounds once.
 #include <cmath>
 
 #include "common.h"
@@ -335,6 +338,22 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
   for (int r = tid; r < kBM; r += NTHR) fx[r] = p.fexp[min(m0 + r, p.m - 1)];
   const uint32_t lanebits = (uint32_t)lane << 2;
 
+  auto outl = [&](int buf, int ocx, int ocy, uint32_t oe) __attribute__((always_inline)) {
+    // outliers of the step: every decode write of the wave precedes these (program order)
+    if (has_o) {
+      // the entry carries its fp16 index inside the group's tile rows (swizzle included)
+      uint16_t* grp_l = Ws + (buf * BN + wlo + kOGroup * oh) * kRowH;
+      auto put = [&](uint32_t v) __attribute__((always_inline)) { grp_l[v >> 16] = (uint16_t)v; };
+      if (ocx + oln < ocy) put(oe);
+      // a group with more entries in the step than one read covers (far beyond the
+      // format's ratios): the rest read directly, and no read left in flight after
+      if (__builtin_amdgcn_ballot_w64(ocy - ocx > OCAP) != 0) {
+        for (int e = ocx + OCAP + oln; e < ocy; e += OCAP) put(p.oent[e]);
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+      }
+    }
+  };
+
   // ---- register stage -> LDS buffer: activations as loaded, weights decoded ----
   auto store = [&](u32x4_t ga, u32x4_t gb, u32x4_t gc, u32x4_t gd, u32x4_t gw, uint16_t gs, uint8_t gz, int buf,
                    int ocx, int ocy, uint32_t oe) __attribute__((always_inline)) {
@@ -367,19 +386,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
 #pragma unroll
     for (int u = 0; u < BPT / 4; ++u)
       *(uint4*)(wrow_l + 8 * ((wc0 + u) ^ wsw)) = make_uint4(d[4 * u], d[4 * u + 1], d[4 * u + 2], d[4 * u + 3]);
-    // outliers of the step: every decode write of the wave precedes these (program order)
-    if (has_o) {
-      // the entry carries its fp16 index inside the group's tile rows (swizzle included)
-      uint16_t* grp_l = Ws + (buf * BN + wlo + kOGroup * oh) * kRowH;
-      auto put = [&](uint32_t v) __attribute__((always_inline)) { grp_l[v >> 16] = (uint16_t)v; };
-      if (ocx + oln < ocy) put(oe);
-      // a group with more entries in the step than one read covers (far beyond the
-      // format's ratios): the rest read directly, and no read left in flight after
-      if (__builtin_amdgcn_ballot_w64(ocy - ocx > OCAP) != 0) {
-        for (int e = ocx + OCAP + oln; e < ocy; e += OCAP) put(p.oent[e]);
-        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-      }
-    }
+    outl(buf, ocx, ocy, oe);
   };
 
   f16v_t acc[4][NT];
@@ -428,17 +435,81 @@ __global__ void __launch_bounds__(64 * NW) gemm_kernel(const GemmParams p) {
     }
   };
 
+  // One half-step: the MFMAs of the step in buffer mbuf, interleaved with the decode and
+  // tile writes of the next step (into the other buffer) and the loads of the stage.
+  auto half = [&](int mbuf, u32x4_t ga, u32x4_t gb, u32x4_t gc, u32x4_t gd, u32x4_t gw, uint16_t gs, uint8_t gz,
+                  int ocx, int ocy, uint32_t oe, int lstage, int lstep) __attribute__((always_inline)) {
+    const int buf = 1 - mbuf;
+    h8_t af[2][4], bf[2][NT];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[s2][i] = *(const h8_t*)(As + (mbuf * kBM + arow + 32 * i) * kRowH + 8 * (((16 * s2 + kq) >> 3) ^ aswz));
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        bf[s2][j] = *(const h8_t*)(Ws + (mbuf * BN + brow + 32 * j) * kRowH + 8 * (((16 * s2 + kq) >> 3) ^ bswz));
+    }
+    // decode of the next step
+    const _Float16 sh = __builtin_bit_cast(_Float16, gs);
+    const f16x2g_t sc2 = {sh, sh};
+    uint32_t d[BPT];
+#pragma unroll
+    for (int b = 0; b < BPT; ++b) {
+      const uint32_t addr = __builtin_amdgcn_perm(gw[b >> 2], lanebits, 0x0c0c0000u | ((4u + (b & 3)) << 8));
+      f16x2g_t c = __builtin_bit_cast(f16x2g_t, *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr);
+      if constexpr (FMT == SPECTRA_FMT_ASYM_G32) {
+        const _Float16 zh = (_Float16)(-(float)gz);
+        const f16x2g_t z2 = {zh, zh};
+        c = c + z2;
+      }
+      c = c * sc2;
+      d[b] = __builtin_bit_cast(uint32_t, c);
+    }
+    uint16_t* arow_l = As + (buf * kBM + ar) * kRowH;
+    const int asw = tile_swz(ar);
+    *(u32x4_t*)(arow_l + 8 * ((AU * ah) ^ asw)) = ga;
+    *(u32x4_t*)(arow_l + 8 * ((AU * ah + 1) ^ asw)) = gb;
+    if constexpr (AU == 4) {
+      *(u32x4_t*)(arow_l + 8 * ((AU * ah + 2) ^ asw)) = gc;
+      *(u32x4_t*)(arow_l + 8 * ((AU * ah + 3) ^ asw)) = gd;
+    }
+    uint16_t* wrow_l = Ws + (buf * BN + wr) * kRowH;
+    const int wsw = tile_swz(wr);
+    const int wc0 = wb0 / 4;
+#pragma unroll
+    for (int u = 0; u < BPT / 4; ++u)
+      *(uint4*)(wrow_l + 8 * ((wc0 + u) ^ wsw)) = make_uint4(d[4 * u], d[4 * u + 1], d[4 * u + 2], d[4 * u + 3]);
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[s2][i], bf[s2][j], acc[i][j], 0, 0, 0);
+    if (lstage == 0) load0(lstep);
+    else load1(lstep);
+    // Interleave: the first k16's fragments, then per MFMA one LDS op (fragment / LUT read
+    // or tile write), two VALU (decode) and one global load, so the MFMA pipe is fed while
+    // this wave's decode and copies run (measured best of the patterns tried).
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // LDS reads
+#pragma unroll
+    for (int q = 0; q < 2 * 4 * NT; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x080, 1, 0);  // LDS
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+    }
+    outl(buf, ocx, ocy, oe);
+  };
+
   // two steps per iteration so the register stages have static indices
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
-    // step kt+1 -> buffer 1 (buffer 1 free since the last barrier)
-    store(sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, 1, oc1x, oc1y, oe1);
-    load1(kt + 3);
-    mfma_step(0);                          // step kt from buffer 0
+    // MFMAs of step kt (buffer 0) with step kt+1 -> buffer 1; then step kt+1 with kt+2 ->
+    // buffer 0 (past the end: unread)
+    half(0, sa1a, sa1b, sa1c, sa1d, sw1, ss1, sz1, oc1x, oc1y, oe1, 1, kt + 3);
     __syncthreads();
-    if (kt + 2 < nk) store(sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, 0, oc0x, oc0y, oe0);
-    load0(kt + 4);
-    mfma_step(1);
+    half(1, sa0a, sa0b, sa0c, sa0d, sw0, ss0, sz0, oc0x, oc0y, oe0, 0, kt + 4);
     __syncthreads();
   }
   if (kt < nk) mfma_step(0);  // odd step count: the last step sits in buffer 0
