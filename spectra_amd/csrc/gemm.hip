@@ -588,19 +588,38 @@ __global__ void __launch_bounds__(kOListThreads) gemm_outlier_lists_kernel(
     int64_t ldow, int ow_dt, int n_out, int n, int KS, int marlin, int32_t* __restrict__ ostart,
     uint32_t* __restrict__ oent) {
   extern __shared__ int32_t cnt[];  // [KS + 1]: counts, then cursors
+  __shared__ int32_t rp[kOGroup + 1];
   __shared__ int32_t wtot[kOListThreads / 64];
   const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const bool csr = okind == SPECTRA_OUTLIERS_CSR;
-  const int r0 = g * kOGroup, r1 = min(r0 + kOGroup, n);
-  const int base = csr ? rowptr[r0] : r0 * n_out;  // the group's first entry
+  const int r0 = g * kOGroup, nr = min(kOGroup, n - r0);
+  // the group's entries are [rp[0], rp[nr]), row r's [rp[r], rp[r + 1]) (the outlier columns
+  // of every row for Format A: n_out per row)
+  if (tid <= nr) rp[tid] = csr ? rowptr[r0 + tid] : (r0 + tid) * n_out;
   for (int t = tid; t <= KS; t += kOListThreads) cnt[t] = 0;
   __syncthreads();
-  for (int r = r0; r < r1; ++r) {
-    const int e0 = csr ? rowptr[r] : 0, e1 = csr ? rowptr[r + 1] : n_out;
-    for (int e = e0 + tid; e < e1; e += kOListThreads) {
-      const int c = csr ? ccol[e] : (int)oidx[e];
-      if ((unsigned)c < (unsigned)(KS * kBK)) atomicAdd(&cnt[c / kBK], 1);  // (columns outside K: dropped)
+  const int base = rp[0], total = rp[nr] - base;
+  // entry el of the group: its row, column and fp16 value (entries in parallel, no per-row chain)
+  auto entry = [&](int el, int& r, int& c, uint32_t& v) __attribute__((always_inline)) {
+    if (csr) {
+      const int e = base + el;
+      r = 0;
+#pragma unroll
+      for (int q = 1; q < kOGroup; ++q) r += (q < nr && rp[q] <= e) ? 1 : 0;
+      c = ccol[e];
+      v = cval[e];
+    } else {
+      r = el / n_out;
+      const int jj = el - r * n_out;
+      c = (int)oidx[jj];
+      v = f2h(load_elem(ow, (int64_t)(r0 + r) * ldow + jj, ow_dt));
     }
+  };
+  for (int el = tid; el < total; el += kOListThreads) {
+    int r, c;
+    uint32_t v;
+    entry(el, r, c, v);
+    if ((unsigned)c < (unsigned)(KS * kBK)) atomicAdd(&cnt[c / kBK], 1);  // (columns outside K: dropped)
   }
   __syncthreads();
   // exclusive scan of cnt[0, KS): thread t owns a run of `per` consecutive steps
@@ -626,19 +645,17 @@ __global__ void __launch_bounds__(kOListThreads) gemm_outlier_lists_kernel(
   }
   if (tid == kOListThreads - 1) og[KS] = base + pre;  // the last thread's runs end at KS
   __syncthreads();
-  for (int r = r0; r < r1; ++r) {
-    const int e0 = csr ? rowptr[r] : 0, e1 = csr ? rowptr[r + 1] : n_out;
-    for (int e = e0 + tid; e < e1; e += kOListThreads) {
-      const int c = csr ? ccol[e] : (int)oidx[e];
-      if ((unsigned)c >= (unsigned)(KS * kBK)) continue;
-      const uint32_t v = csr ? cval[e] : f2h(load_elem(ow, (int64_t)r * ldow + e, ow_dt));
-      const int pos = atomicAdd(&cnt[c / kBK], 1);
-      const int rr = r - r0, cs = c % kBK;
-      const int jb = marlin ? (cs & 15) : (cs >> 1), h = marlin ? (cs >> 4) : (cs & 1);
-      const int e2 = 2 * jb + h;  // fp16 index in the step's decoded row (packed-byte pair order)
-      const int off = rr * kRowH + 8 * ((e2 >> 3) ^ tile_swz(rr)) + (e2 & 7);
-      oent[base + pos] = ((uint32_t)off << 16) | v;
-    }
+  for (int el = tid; el < total; el += kOListThreads) {
+    int r, c;
+    uint32_t v;
+    entry(el, r, c, v);
+    if ((unsigned)c >= (unsigned)(KS * kBK)) continue;
+    const int pos = atomicAdd(&cnt[c / kBK], 1);
+    const int cs = c % kBK;
+    const int jb = marlin ? (cs & 15) : (cs >> 1), h = marlin ? (cs >> 4) : (cs & 1);
+    const int e2 = 2 * jb + h;  // fp16 index in the step's decoded row (packed-byte pair order)
+    const int off = r * kRowH + 8 * ((e2 >> 3) ^ tile_swz(r)) + (e2 & 7);
+    oent[base + pos] = ((uint32_t)off << 16) | v;
   }
 }
 
