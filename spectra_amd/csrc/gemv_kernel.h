@@ -37,7 +37,8 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kRpwMax = 11;  // rows per wave held in registers (<= 128 VGPRs: two 8-wave workgroups per CU)
 constexpr int kLutBytes = 65536;
-constexpr int kMaxWaves = 8;
+constexpr int kMaxWaves = 16;  // waves per workgroup: 8 (two per SIMD) or 16 (four per SIMD)
+constexpr int kRpwWide = 6;    // rows per wave of the 16-wave kernels (<= 128 VGPRs)
 
 struct GemvParams {
   const uint8_t* packed;
@@ -276,8 +277,8 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-template <int FMT, int MT, int RPW, bool BF, int PRO = kProNone>
-__global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
+template <int FMT, int MT, int RPW, bool BF, int PRO = kProNone, int LB = 512>
+__global__ void __launch_bounds__(LB) gemv_kernel(const GemvParams p) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int XH = 2 * MT;  // 16-element half-runs of activations per thread (at most)
   const int tid = threadIdx.x;
@@ -740,9 +741,10 @@ __global__ void __launch_bounds__(512) gemv_kernel(const GemvParams p) {
 // ---------------------------------------------------------------------------
 typedef void (*gemv_fn)(const GemvParams);
 
-gemv_fn gemv_pick_f16(int fmt, int mt, int rpw);
-gemv_fn gemv_pick_bf16(int fmt, int mt, int rpw);
-gemv_fn gemv_pick_f16_pro(int pro, int rpw);  // one fp16 row, NF4, fused prologue
+// wide: the 16-wave kernels (one activation row, rpw <= kRpwWide)
+gemv_fn gemv_pick_f16(int fmt, int mt, int rpw, bool wide);
+gemv_fn gemv_pick_bf16(int fmt, int mt, int rpw, bool wide);
+gemv_fn gemv_pick_f16_pro(int pro, int rpw, bool wide);  // one fp16 row, NF4, fused prologue
 
 
 template <int FMT, int MT, bool BF>
@@ -794,8 +796,22 @@ gemv_fn pick_rpw4(int rpw) {
   }
 }
 
+// 16-wave kernels (launch bound 1024: four waves per SIMD)
+template <int FMT, bool BF, int PRO>
+gemv_fn pick_wide(int rpw) {
+  switch (rpw) {
+    case 1: return gemv_kernel<FMT, 1, 1, BF, PRO, 1024>;
+    case 2: return gemv_kernel<FMT, 1, 2, BF, PRO, 1024>;
+    case 3: return gemv_kernel<FMT, 1, 3, BF, PRO, 1024>;
+    case 4: return gemv_kernel<FMT, 1, 4, BF, PRO, 1024>;
+    case 5: return gemv_kernel<FMT, 1, 5, BF, PRO, 1024>;
+    default: return gemv_kernel<FMT, 1, 6, BF, PRO, 1024>;
+  }
+}
+
 template <int FMT, bool BF>
-gemv_fn pick_kernel(int mt, int rpw) {
+gemv_fn pick_kernel(int mt, int rpw, bool wide) {
+  if (wide) return pick_wide<FMT, BF, kProNone>(rpw);
   if (mt == 1) return pick_rpw<FMT, 1, BF>(rpw);
   if (mt == 2) return pick_rpw<FMT, 2, BF>(rpw);
   return pick_rpw4<FMT, BF>(rpw);
