@@ -295,7 +295,25 @@ __global__ void __launch_bounds__(LB) gemv_kernel(const GemvParams p) {
   asm volatile("" ::"s"(p.x), "s"(p.ldx), "s"(p.packed), "s"(p.ldp), "s"(p.scales), "s"(p.lds), "s"(p.m),
                "s"(p.gshift), "s"(p.log_had), "s"(p.marlin), "s"(p.zeros), "s"(p.ldz), "s"(p.rowptr), "s"(p.okind), "s"(p.bias), "s"(p.bias_dt));
 
-  // ---------------- (1) activation runs and CSR row pointers: raw bits, issued first ----------------
+  // One workgroup per CU (the 16-wave kernels): the outlier entries are loaded ahead of the
+  // weights and their products formed right after barrier 1, while the weights are still
+  // in flight.  Several workgroups per CU (8 waves): each would wait a round trip for its
+  // row pointers before its weights, so there they are loaded behind the weights and the
+  // products formed after the stream.
+  constexpr bool kEarlyOutl = LB > 512;
+  // this workgroup's CSR entries [e0, e1): scalar (constant-cache) loads, issued first so
+  // that their latency overlaps the activation address arithmetic
+  const bool has_o = p.okind != SPECTRA_OUTLIERS_NONE;
+  int e0 = 0, e1 = 0;
+  if constexpr (FMT == SPECTRA_FMT_NF4 && kEarlyOutl) {
+    if (p.okind == SPECTRA_OUTLIERS_CSR) {
+      const __attribute__((address_space(4))) int32_t* rpc = (const __attribute__((address_space(4))) int32_t*)p.rowptr;
+      e0 = rpc[r0];
+      e1 = rpc[r0 + Rw];
+    }
+  }
+
+  // ---------------- (1) activation runs: raw bits, issued first ----------------
   // half-run hr = tid + i * BD of the MT x (K / 16) half-runs; inside a Hadamard block of
   // 2^bL lanes the lane holds logical chunk reflect_chunk (bit 0 = which half of its run)
   const int hpr = K >> 4;  // half-runs per activation row
@@ -346,15 +364,64 @@ __global__ void __launch_bounds__(LB) gemv_kernel(const GemvParams p) {
     }
   }
 
-  // CSR row pointers, issued before the weights: the outlier loads need e0 before the
-  // stream has arrived (the wait counts are in issue order)
-  // (one unconditional load per wave: lane 0 reads the first, lane 1 the last row
-  // pointer; without CSR it reads the packed tensor and the value is unused.  The
-  // values are read out of the lanes where they are needed, after the activation work.)
+  // row pointers through the vector path (lane 0 the first, lane 1 the last), issued before
+  // the weights (the 8-wave kernels)
   int rpe = 0;
-  if constexpr (FMT == SPECTRA_FMT_NF4)
+  if constexpr (FMT == SPECTRA_FMT_NF4 && !kEarlyOutl)
     rpe = p.okind == SPECTRA_OUTLIERS_CSR ? load_at<int>(p.rowptr + r0, lane == 1 ? 4u * Rw : 0u)
                                           : load_at<int>(p.packed, 0u);
+  int olim = 0;
+  int4 ocv;
+  uint2 ovv;
+  int obase = 0;  // el of this thread's first entry
+  // ---------------- (1b) outlier entries of this workgroup ----------------
+  // Raw loaded words only (extracted where they are used, so nothing here waits for
+  // them), one unconditional load pair per thread (the wait counts never branch):
+  //  * Format B, CSR: four consecutive entries from the 4-aligned entry below e0 (a
+  //    dwordx4 of columns, a dwordx2 of fp16 values; entry e is el = e - e0).  The
+  //    entries of a partial last group of the array are read in the per-row phase.
+  //  * Format A, dense columns: entry el = tid, row el / n_out, column el % n_out (the
+  //    low dword of the int64 index, the 16-bit weight).
+  // Without outliers the loads read the first bytes of the packed tensor.  Entries
+  // el < olim have their products staged in LDS; the rest (beyond the LDS share, or in a
+  // partial last CSR group) are read from the side tensors per row.
+  auto load_outliers = [&]() __attribute__((always_inline)) {
+  if constexpr (FMT == SPECTRA_FMT_NF4 && !kEarlyOutl) {
+    e0 = has_o ? __builtin_amdgcn_readlane(rpe, 0) : 0;
+    e1 = has_o ? __builtin_amdgcn_readlane(rpe, 1) : 0;
+  }
+  olim = FMT == SPECTRA_FMT_NF4 ? min(p.ocap, (p.csr_nnz & ~3) - e0) : p.ocap;
+  if constexpr (FMT == SPECTRA_FMT_NF4) {
+    const int g0 = e0 & ~3, g4 = g0 + 4 * tid;
+    // groups past this workgroup's entries (or the array end) re-read the first group (the
+    // workgroup's own, or the array's when that one is partial), a cached line, so the
+    // stream carries no CSR bytes beyond the workgroup's own
+    // (arrays of fewer than 4 entries are never read this way: olim is 0 then)
+    const bool big = has_o && p.csr_nnz >= 4;
+    const bool ok4 = big && g4 < e1 && g4 + 4 <= p.csr_nnz;
+    const int gb = big && g0 + 4 <= p.csr_nnz ? g0 : 0;  // wave-uniform base group
+    // one load each, from a wave-uniform base (selected in scalar registers)
+    const void* cbase = big ? (const void*)(p.ccol + gb) : (const void*)p.packed;
+    const void* vbase = big ? (const void*)(p.cval + gb) : (const void*)p.packed;
+    const uint32_t eo = ok4 ? (uint32_t)(g4 - gb) : 0u;
+    ocv = load_at<int4>(cbase, 4u * eo);
+    ovv = load_at<uint2>(vbase, 2u * eo);
+    obase = g4 - e0;
+  } else {
+    const int n_out = p.n_out > 0 ? p.n_out : 1;
+    // (row, column) of entry tid: float reciprocal, exact after one correction
+    const int ei = tid < Rw * n_out ? tid : 0;
+    int r = (int)((float)ei * p.inv_n_out);
+    int jj = ei - r * n_out;
+    r = jj < 0 ? r - 1 : (jj >= n_out ? r + 1 : r);
+    jj = ei - r * n_out;
+    ocv.x = has_o ? load_at<int>(p.oidx, 8u * (uint32_t)jj) : load_at<int>(p.packed, 0u);
+    ovv.x = has_o ? load_at<uint16_t>((const uint16_t*)p.ow + (int64_t)r0 * p.ldow, 2u * (uint32_t)(r * p.ldow + jj))
+                  : load_at<uint16_t>(p.packed, 0u);
+    obase = tid;
+  }
+  };
+  if constexpr (kEarlyOutl) load_outliers();
 
   // ---------------- (2) the weight stream: every row of this wave, up front ----------------
   const int kb = s * 2048 + lane * 32;  // first k of this lane (one 32-run)
@@ -501,52 +568,7 @@ __global__ void __launch_bounds__(LB) gemv_kernel(const GemvParams p) {
     }
   }
 
-  // ---------------- (5) outlier entries of this workgroup (consumed after the stream) ----------------
-  // Raw loaded words only (extracted where they are used, so nothing here waits for
-  // them), one unconditional load pair per thread (the wait counts never branch):
-  //  * Format B, CSR: four consecutive entries from the 4-aligned entry below e0 (a
-  //    dwordx4 of columns, a dwordx2 of fp16 values; entry e is el = e - e0).  The
-  //    entries of a partial last group of the array are read in the per-row phase.
-  //  * Format A, dense columns: entry el = tid, row el / n_out, column el % n_out (the
-  //    low dword of the int64 index, the 16-bit weight).
-  // Without outliers the loads read the first bytes of the packed tensor.
-  const bool has_o = p.okind != SPECTRA_OUTLIERS_NONE;
-  int e0 = 0, e1 = 0;
-  if constexpr (FMT == SPECTRA_FMT_NF4) {
-    e0 = has_o ? __builtin_amdgcn_readlane(rpe, 0) : 0;
-    e1 = has_o ? __builtin_amdgcn_readlane(rpe, 1) : 0;
-  }
-  // entries el < olim have their products staged in LDS; the rest (beyond the LDS share,
-  // or in a partial last CSR group) are read from the side tensors per row
-  const int olim = FMT == SPECTRA_FMT_NF4 ? min(p.ocap, (p.csr_nnz & ~3) - e0) : p.ocap;
-  int4 ocv;
-  uint2 ovv;
-  int obase;  // el of this thread's first entry
-  if constexpr (FMT == SPECTRA_FMT_NF4) {
-    const int g0 = e0 & ~3, g4 = g0 + 4 * tid;
-    // groups past this workgroup's entries (or the array end) re-read the first group (the
-    // workgroup's own, or the array's when that one is partial), a cached line, so the
-    // stream carries no CSR bytes beyond the workgroup's own
-    // (arrays of fewer than 4 entries are never read this way: olim is 0 then)
-    const bool big = has_o && p.csr_nnz >= 4;
-    const bool ok4 = big && g4 < e1 && g4 + 4 <= p.csr_nnz;
-    const int gb = big && g0 + 4 <= p.csr_nnz ? g0 : 0;  // wave-uniform base group
-    ocv = big ? load_at<int4>(p.ccol + gb, ok4 ? 4u * (uint32_t)(g4 - gb) : 0u) : load_at<int4>(p.packed, 0u);
-    ovv = big ? load_at<uint2>(p.cval + gb, ok4 ? 2u * (uint32_t)(g4 - gb) : 0u) : load_at<uint2>(p.packed, 0u);
-    obase = g4 - e0;
-  } else {
-    const int n_out = p.n_out > 0 ? p.n_out : 1;
-    // (row, column) of entry tid: float reciprocal, exact after one correction
-    const int ei = tid < Rw * n_out ? tid : 0;
-    int r = (int)((float)ei * p.inv_n_out);
-    int jj = ei - r * n_out;
-    r = jj < 0 ? r - 1 : (jj >= n_out ? r + 1 : r);
-    jj = ei - r * n_out;
-    ocv.x = has_o ? load_at<int>(p.oidx, 8u * (uint32_t)jj) : load_at<int>(p.packed, 0u);
-    ovv.x = has_o ? load_at<uint16_t>((const uint16_t*)p.ow + (int64_t)r0 * p.ldow, 2u * (uint32_t)(r * p.ldow + jj))
-                  : load_at<uint16_t>(p.packed, 0u);
-    obase = tid;
-  }
+  if constexpr (!kEarlyOutl) load_outliers();
 
   if constexpr (PRO == kProRms) {  // per-wave sums of h^2, fixed order
     for (int off = 32; off >= 1; off >>= 1) ssq += __shfl_xor(ssq, off, 64);
@@ -576,6 +598,32 @@ __global__ void __launch_bounds__(LB) gemv_kernel(const GemvParams p) {
         xsum[m] += h2f((uint16_t)xpair[m][q]) + h2f((uint16_t)(xpair[m][q] >> 16));
     }
   }
+
+  // ---------------- (6b) outlier products, in the same scaled fp16 activation basis ----------------
+  // (before the stream in the 16-wave kernels, after it in the others)
+  float* oprod = (float*)(smem + p.off_oprod);
+  auto outlier_products = [&]() __attribute__((always_inline)) {
+  {
+    const int cnt = !has_o ? 0 : (FMT == SPECTRA_FMT_NF4 ? e1 - e0 : Rw * p.n_out);
+    const int odt = FMT == SPECTRA_FMT_NF4 ? SPECTRA_F16 : p.ow_dt;
+    constexpr int NE = FMT == SPECTRA_FMT_NF4 ? 4 : 1;
+    const int cols[4] = {ocv.x, ocv.y, ocv.z, ocv.w};
+    const uint32_t vals4[4] = {ovv.x & 0xffffu, ovv.x >> 16, ovv.y & 0xffffu, ovv.y >> 16};
+#pragma unroll
+    for (int u = 0; u < NE; ++u) {
+      const int el = obase + u;  // workgroup-local entry index
+      if (el >= 0 && el < cnt && el < olim) {
+        const int col = cols[u];
+        const int pos = xp_pos(col, p.marlin);
+        const float ov = to_f32_16((uint16_t)vals4[u], odt);
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+          oprod[el * MT + m] = ov * (h2f(xp[m * XS + pos]) * xsc[m * qpr + (col >> 5)]);
+      }
+    }
+  }
+  };
+  if constexpr (kEarlyOutl) outlier_products();
 
   // ---------------- (7) the stream: LUT decode + dot2 per packed byte ----------------
   constexpr int V = RPW * MT;
@@ -632,27 +680,7 @@ __global__ void __launch_bounds__(LB) gemv_kernel(const GemvParams p) {
     if (rl < Rw) part[(rl * p.S + s) * MT + m] = vals[0];
   }
 
-  // ---------------- (9) outlier products, in the same scaled fp16 activation basis ----------------
-  float* oprod = (float*)(smem + p.off_oprod);
-  {
-    const int cnt = !has_o ? 0 : (FMT == SPECTRA_FMT_NF4 ? e1 - e0 : Rw * p.n_out);
-    const int odt = FMT == SPECTRA_FMT_NF4 ? SPECTRA_F16 : p.ow_dt;
-    constexpr int NE = FMT == SPECTRA_FMT_NF4 ? 4 : 1;
-    const int cols[4] = {ocv.x, ocv.y, ocv.z, ocv.w};
-    const uint32_t vals4[4] = {ovv.x & 0xffffu, ovv.x >> 16, ovv.y & 0xffffu, ovv.y >> 16};
-#pragma unroll
-    for (int u = 0; u < NE; ++u) {
-      const int el = obase + u;  // workgroup-local entry index
-      if (el >= 0 && el < cnt && el < olim) {
-        const int col = cols[u];
-        const int pos = xp_pos(col, p.marlin);
-        const float ov = to_f32_16((uint16_t)vals4[u], odt);
-#pragma unroll
-        for (int m = 0; m < MT; ++m)
-          oprod[el * MT + m] = ov * (h2f(xp[m * XS + pos]) * xsc[m * qpr + (col >> 5)]);
-      }
-    }
-  }
+  if constexpr (!kEarlyOutl) outlier_products();
   int32_t* rps = (int32_t*)(smem + p.off_rp);
   if (p.okind == SPECTRA_OUTLIERS_CSR && tid <= Rw) rps[tid] = rp_v;
   float* bl = (float*)(smem + p.off_bias);
