@@ -59,6 +59,62 @@ __device__ __forceinline__ int tile_swz(int r) {
 // written in packed-byte pair order.
 constexpr int kPrepMaxU = 16;  // K <= 256 * 8 * 16 = 32768
 
+// Value of lane (lane ^ LB) for LB = 1 .. 32, on the VALU: DPP quad permutes (1, 2), a
+// half-row mirror then a quad reversal (4), a row rotation by 8 (8), and the row swaps
+// v_permlane16_swap / v_permlane32_swap (16, 32).
+template <int LB>
+__device__ __forceinline__ float lane_xor(float v, int lane) {
+  const int iv = __builtin_bit_cast(int, v);
+  if constexpr (LB == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+  else if constexpr (LB == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+  else if constexpr (LB == 4) {
+    const int t = __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false);  // l -> 7 - l inside 8 lanes
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, false));  // then quad reversed
+  } else if constexpr (LB == 8) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false));
+  else if constexpr (LB == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)((lane & 16) ? r[0] : r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)((lane & 32) ? r[0] : r[1]));
+  }
+}
+
+// Butterfly across lanes at distance LB: v += c * partner with c = +1 on the low side and
+// -1 on the high side, leaving u + v low and -(u - v) high (the product by +-1 is exact
+// and the fma rounds once, as the reference's add / subtract does).  Partners share their
+// sign before every stage, and the lane's final sign (-1)^(high sides taken) rides on
+// the output scale.
+// (distances 1, 2, 8: one v_fmac_f32_dpp per value, eight per block behind the two wait
+// states a DPP source needs after its VALU write)
+#define SPECTRA_PFLY(CTRL, A)                                                          \
+  asm volatile("s_nop 1\n"                                                            \
+               "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), \
+                 "+v"(A[6]), "+v"(A[7])                                                 \
+               : "v"(c))
+
+template <int LB, int U>
+__device__ __forceinline__ void prep_fly(float (&v)[U][8], float c, int lane) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if constexpr (LB == 1) SPECTRA_PFLY("quad_perm:[1,0,3,2]", v[u]);
+    else if constexpr (LB == 2) SPECTRA_PFLY("quad_perm:[2,3,0,1]", v[u]);
+    else if constexpr (LB == 8) SPECTRA_PFLY("row_ror:8", v[u]);
+    else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = __builtin_fmaf(lane_xor<LB>(v[u][e], lane), c, v[u][e]);
+    }
+  }
+}
+
 template <int kPrepU>
 __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __restrict__ a, int64_t lda, int dt,
                                                                   int k, int log_had, float div, int marlin, int vec,
@@ -108,20 +164,16 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
           }
     }
   }
-#pragma unroll
-  for (int lh = 3; lh < 9; ++lh) {
-    if (lh < log_had) {
-      const int lb = 1 << (lh - 3);
-      const bool hi = (tid & lb) != 0;
-#pragma unroll
-      for (int u = 0; u < kPrepU; ++u)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float o = __shfl_xor(v[u][e], lb, 64);
-          v[u][e] = hi ? o - v[u][e] : v[u][e] + o;
-        }
-    }
-  }
+  // stages h = 8 .. 256 across the lanes of a block (lane bit lh - 3)
+  const int lane = tid & 63;
+  float sgn = 1.0f;
+  auto side = [&](int lb) { const bool hi = (tid & lb) != 0; if (hi) sgn = -sgn; return hi ? -1.0f : 1.0f; };
+  if (log_had > 3) prep_fly<1>(v, side(1), lane);
+  if (log_had > 4) prep_fly<2>(v, side(2), lane);
+  if (log_had > 5) prep_fly<4>(v, side(4), lane);
+  if (log_had > 6) prep_fly<8>(v, side(8), lane);
+  if (log_had > 7) prep_fly<16>(v, side(16), lane);
+  if (log_had > 8) prep_fly<32>(v, side(32), lane);
   if (log_had > 9) {  // 1024-blocks: the stage across waves through LDS
 #pragma unroll
     for (int u = 0; u < kPrepU; ++u)
@@ -133,34 +185,33 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
     for (int u = 0; u < kPrepU; ++u) {
       const int c = tid + u * kPrepThreads;
       if (c < n8) {
-        const bool hi = (c & 64) != 0;  // element bit 9 = chunk bit 6
+        const float cc = (c & 64) != 0 ? -1.0f : 1.0f;  // element bit 9 = chunk bit 6 (same for every u)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float o = fs[8 * (c ^ 64) + e];
-          v[u][e] = hi ? o - v[u][e] : v[u][e] + o;
-        }
+        for (int e = 0; e < 8; ++e) v[u][e] = __builtin_fmaf(fs[8 * (c ^ 64) + e], cc, v[u][e]);
       }
     }
     __syncthreads();
+    if (tid & 64) sgn = -sgn;  // every chunk of this thread has the same bit 6 (256 | 64)
   }
+  // the normalisation by sqrt(block) (compressor.py:40-41) rides on the output scale below
   float mx = 0.0f;
 #pragma unroll
   for (int u = 0; u < kPrepU; ++u)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (log_had > 0) v[u][e] = v[u][e] / div;  // compressor.py:40-41
-      mx = fmaxf(mx, fabsf(v[u][e]));
-    }
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[u][e]));
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
   if ((tid & 63) == 0) wmax[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  if (log_had > 0) mx = mx / div;  // the normalised row's max |x_rot|
   const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
   const int eb = (int)(bits >> 23);
   const int E = eb == 0 ? -126 : eb - 127;
   int F = bits == 0 ? 0 : 14 - E;  // max |x_rot| * 2^F in [2^14, 2^15): exact scaling, no overflow
   F = F < -126 ? -126 : (F > 126 ? 126 : F);
-  const float f = __builtin_bit_cast(float, (uint32_t)(F + 127) << 23);
+  const float f2 = __builtin_bit_cast(float, (uint32_t)(F + 127) << 23);
+  // output scale: 2^F / sqrt(block) (one rounding), with the lane's butterfly sign
+  const float f = sgn * (log_had > 0 ? f2 / div : f2);
   uint16_t* xs = (uint16_t*)fs;
   if (marlin) {  // natural order into LDS, then pairs (k, k + 16) of each 32-run
 #pragma unroll
