@@ -160,6 +160,65 @@ __device__ __forceinline__ T load_at(const void* base, uint32_t byte_off) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// cross-lane Walsh-Hadamard butterflies (activation prep of the GEMM and small-batch families)
+// ---------------------------------------------------------------------------
+// Value of lane (lane ^ LB) for LB = 1 .. 32, on the VALU: DPP quad permutes (1, 2), a
+// half-row mirror then a quad reversal (4), a row rotation by 8 (8), and the row swaps
+// v_permlane16_swap / v_permlane32_swap (16, 32).
+template <int LB>
+__device__ __forceinline__ float lane_xor(float v, int lane) {
+  const int iv = __builtin_bit_cast(int, v);
+  if constexpr (LB == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0xB1, 0xF, 0xF, false));
+  else if constexpr (LB == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x4E, 0xF, 0xF, false));
+  else if constexpr (LB == 4) {
+    const int t = __builtin_amdgcn_mov_dpp(iv, 0x141, 0xF, 0xF, false);  // l -> 7 - l inside 8 lanes
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(t, 0x1B, 0xF, 0xF, false));  // then quad reversed
+  } else if constexpr (LB == 8) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(iv, 0x128, 0xF, 0xF, false));
+  else if constexpr (LB == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)((lane & 16) ? r[0] : r[1]));
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(iv, iv, false, false);
+    return __builtin_bit_cast(float, (int)((lane & 32) ? r[0] : r[1]));
+  }
+}
+
+// Butterfly across lanes at distance LB: v += c * partner with c = +1 on the low side and
+// -1 on the high side, leaving u + v low and -(u - v) high (the product by +-1 is exact
+// and the fma rounds once, as the reference's add / subtract does).  Partners share their
+// sign before every stage, and the lane's final sign (-1)^(high sides taken) rides on
+// the output scale.
+// (distances 1, 2, 8: one v_fmac_f32_dpp per value, eight per block behind the two wait
+// states a DPP source needs after its VALU write)
+#define SPECTRA_PFLY(CTRL, A)                                                          \
+  asm volatile("s_nop 1\n"                                                            \
+               "v_fmac_f32_dpp %0, %0, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %1, %1, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %2, %2, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %3, %3, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %4, %4, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %5, %5, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %6, %6, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               "v_fmac_f32_dpp %7, %7, %8 " CTRL " row_mask:0xf bank_mask:0xf\n"      \
+               : "+v"(A[0]), "+v"(A[1]), "+v"(A[2]), "+v"(A[3]), "+v"(A[4]), "+v"(A[5]), \
+                 "+v"(A[6]), "+v"(A[7])                                                 \
+               : "v"(c))
+
+template <int LB, int U>
+__device__ __forceinline__ void prep_fly(float (&v)[U][8], float c, int lane) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if constexpr (LB == 1) SPECTRA_PFLY("quad_perm:[1,0,3,2]", v[u]);
+    else if constexpr (LB == 2) SPECTRA_PFLY("quad_perm:[2,3,0,1]", v[u]);
+    else if constexpr (LB == 8) SPECTRA_PFLY("row_ror:8", v[u]);
+    else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = __builtin_fmaf(lane_xor<LB>(v[u][e], lane), c, v[u][e]);
+    }
+  }
+}
+
 // dtype-tagged load/store of one element
 __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dtype) {
   if (dtype == SPECTRA_F16) return h2f(((const uint16_t*)p)[i]);

@@ -127,6 +127,108 @@ __global__ void __launch_bounds__(kSkPrepThreads) skinny_prep_kernel(const void*
   if (sg == 0 && tid == 0) fexp[m] = F;
 }
 
+// The same pre-pass for Hadamard blocks of at most 512: one workgroup of 256 threads per
+// 2048-element segment, thread t owning elements 8 t .. 8 t + 7.  The FWHT runs on register
+// bits (h = 1, 2, 4) and across the lanes of a block (h = 8 .. 256: v_fmac_f32_dpp
+// butterflies, the lane's sign and 1 / sqrt(b) riding on the output scale), with no
+// barrier per stage; the scaled fp16 values pass through LDS once to reach the MFMA
+// operand order.  Same scale bound, layout and outputs as skinny_prep_kernel.
+constexpr int kSkSegFast = 8 * kSkPrepThreads;
+
+__global__ void __launch_bounds__(kSkPrepThreads) skinny_prep_fast_kernel(
+    const void* __restrict__ x, int64_t ldx, int dt, int k, int log_had, float div, int mp, int marlin, int want_xk,
+    uint4* __restrict__ xa, uint16_t* __restrict__ xk, int32_t* __restrict__ fexp) {
+  __shared__ __align__(16) uint16_t xs[kSkSegFast];
+  __shared__ float wmax[kSkPrepThreads / 64];
+  const int sg = blockIdx.x, m = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int k0 = sg * kSkSegFast;
+  const int len = min(kSkSegFast, k - k0);
+  const uint16_t* row = (const uint16_t*)x + (int64_t)m * ldx;
+  // this thread's 8 elements (K % 128 == 0 and the host checked the alignment)
+  float v[1][8];
+  {
+    uint4 q = make_uint4(0u, 0u, 0u, 0u);
+    if (8 * tid < len) q = *(const uint4*)(row + k0 + 8 * tid);
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[0][2 * e] = to_f32_16((uint16_t)(w4[e] & 0xffffu), dt);
+      v[0][2 * e + 1] = to_f32_16((uint16_t)(w4[e] >> 16), dt);
+    }
+  }
+  // row max |x| (the whole row: every segment computes the same bound)
+  float mx = 0.0f;
+  for (int i = tid * 8; i < k; i += kSkPrepThreads * 8) {
+    const uint4 q = *(const uint4*)(row + i);
+    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      mx = fmaxf(mx, fabsf(to_f32_16((uint16_t)(u[j] & 0xffffu), dt)));
+      mx = fmaxf(mx, fabsf(to_f32_16((uint16_t)(u[j] >> 16), dt)));
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if (lane == 0) wmax[tid >> 6] = mx;
+  // compressor.py:34-39: stages h = 1, 2, 4 on register bits, then across lanes
+#pragma unroll
+  for (int lh = 0; lh < 3; ++lh) {
+    if (lh < log_had) {
+      const int h = 1 << lh;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if ((e & h) == 0) {
+          const float x0 = v[0][e], x1 = v[0][e | h];
+          v[0][e] = x0 + x1;
+          v[0][e | h] = x0 - x1;
+        }
+    }
+  }
+  float sgn = 1.0f;
+  auto side = [&](int lb) { const bool hi = (tid & lb) != 0; if (hi) sgn = -sgn; return hi ? -1.0f : 1.0f; };
+  if (log_had > 3) prep_fly<1>(v, side(1), lane);
+  if (log_had > 4) prep_fly<2>(v, side(2), lane);
+  if (log_had > 5) prep_fly<4>(v, side(4), lane);
+  if (log_had > 6) prep_fly<8>(v, side(8), lane);
+  if (log_had > 7) prep_fly<16>(v, side(16), lane);
+  if (log_had > 8) prep_fly<32>(v, side(32), lane);
+  __syncthreads();
+  mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  if (log_had > 0) {
+    mx = mx * div;  // sqrt(b) max|x| bounds the rotated row before the division
+    mx = mx * 1.0009765625f;
+  }
+  const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
+  const int eb = (int)(bits >> 23);
+  const int E = eb == 0 ? -126 : eb - 127;
+  int F = bits == 0 ? 0 : 14 - E;
+  F = F < -126 ? -126 : (F > 126 ? 126 : F);
+  const float f2 = __builtin_bit_cast(float, (uint32_t)(F + 127) << 23);
+  // (sum) / sqrt(b) (compressor.py:40-41) times 2^F, in one scale with the lane's sign
+  const float fo = sgn * (log_had > 0 ? f2 / div : f2);
+  {
+    uint32_t d[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d[e] = (uint32_t)f2h(v[0][2 * e] * fo) | ((uint32_t)f2h(v[0][2 * e + 1] * fo) << 16);
+    *(uint4*)(xs + 8 * tid) = make_uint4(d[0], d[1], d[2], d[3]);
+  }
+  __syncthreads();
+  // A-operand units of this segment: (chunk c, MFMA t, lane group g) -> 8 fp16 at [c][t][g][mp][8]
+  const int units = (len >> 7) * 16, c0 = k0 >> 7;
+  for (int u = tid; u < units; u += kSkPrepThreads) {
+    const int c = u >> 4, t = (u >> 2) & 3, g = u & 3;
+    uint32_t d[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      d[i] = (uint32_t)xs[c * 128 + sk_chunk_k(t, g, 2 * i, marlin)] |
+             ((uint32_t)xs[c * 128 + sk_chunk_k(t, g, 2 * i + 1, marlin)] << 16);
+    xa[(int64_t)((c0 + c) * 16 + (u & 15)) * mp + m] = make_uint4(d[0], d[1], d[2], d[3]);
+  }
+  if (want_xk)
+    for (int i = tid; i < len; i += kSkPrepThreads) xk[(int64_t)(k0 + i) * mp + m] = xs[i];
+  if (sg == 0 && tid == 0) fexp[m] = F;
+}
+
 // ---------------------------------------------------------------------------
 // MFMA stream
 // ---------------------------------------------------------------------------
@@ -458,11 +560,19 @@ int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_
   const float div = had > 1 ? (float)std::sqrt((double)had) : 1.0f;
   const int seg = had > kSkSeg ? had : kSkSeg;
   const int nseg = (int)((w->k + seg - 1) / seg);
-  int st = ensure_lds_limit((const void*)skinny_prep_kernel);
-  if (st != SPECTRA_OK) return st;
-  hipLaunchKernelGGL(skinny_prep_kernel, dim3((unsigned)nseg, (unsigned)m), dim3(kSkPrepThreads), (size_t)seg * 4,
-                     stream, x, ldx, act_dtype, (int)w->k, seg, log_had, div, mp, w->marlin_layout ? 1 : 0,
-                     csr ? 1 : 0, xa, xk, fexp);
+  int st;
+  if (log_had <= 9) {  // blocks up to 512: register / DPP butterflies
+    const int nsegf = (int)((w->k + kSkSegFast - 1) / kSkSegFast);
+    hipLaunchKernelGGL(skinny_prep_fast_kernel, dim3((unsigned)nsegf, (unsigned)m), dim3(kSkPrepThreads), 0, stream,
+                       x, ldx, act_dtype, (int)w->k, log_had, div, mp, w->marlin_layout ? 1 : 0, csr ? 1 : 0, xa,
+                       xk, fexp);
+  } else {
+    st = ensure_lds_limit((const void*)skinny_prep_kernel);
+    if (st != SPECTRA_OK) return st;
+    hipLaunchKernelGGL(skinny_prep_kernel, dim3((unsigned)nseg, (unsigned)m), dim3(kSkPrepThreads), (size_t)seg * 4,
+                       stream, x, ldx, act_dtype, (int)w->k, seg, log_had, div, mp, w->marlin_layout ? 1 : 0,
+                       csr ? 1 : 0, xa, xk, fexp);
+  }
   SPECTRA_HIP_CHECK(hipGetLastError());
 
   SkinnyParams p;
