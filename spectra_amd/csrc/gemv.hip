@@ -16,7 +16,7 @@ struct GemvPlan {
 };
 
 // returns false when the shape does not fit this kernel family
-static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, GemvPlan* pl, int rpw_cap = kRpwMax) {
+static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, GemvPlan* pl, int rpw2) {
   const int mt = m <= 1 ? 1 : (m <= 2 ? 2 : 4);
   if (m > 4 || k > 16384 || k % 32) return false;
   const int S = (int)((k + 2047) / 2048);
@@ -26,14 +26,15 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   if (G > want) G = (int)want;
   if (G < 1) G = 1;
   int rpw = (int)((want + G - 1) / G);
-  const int rpw_max = mt == 4 ? 8 : rpw_cap;
+  const int rpw_max = mt == 4 ? 8 : kRpwMax;
   bool wide = false;
   if (rpw > rpw_max && mt == 1) {
     // more rows than one resident workgroup per CU holds: size for two per CU (LDS <= 80 KB
-    // below; the one-row kernels stay within 128 VGPRs), so that one workgroup's set-up
-    // overlaps the other's stream
+    // below, at most rpw2 rows per wave: the kernels built for 128 VGPRs), so that one
+    // workgroup's set-up overlaps the other's stream
     const int64_t want2 = (n + 511) / 512;
     rpw = (int)((want2 + G - 1) / G);
+    if (rpw > rpw2) rpw = rpw2;
   } else if (mt == 1) {
     // one workgroup per CU: 16 waves (four per SIMD) hide the phases' latencies better
     // (measured: down_proj 7.84 -> 7.35 us); with two per CU the 8-wave plan stays ahead
@@ -100,9 +101,8 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
   GemvPlan pl;
   const bool csr = outliers && w->outlier_kind == SPECTRA_OUTLIERS_CSR;
   const int pro = fu ? fu->prologue : SPECTRA_PROLOGUE_NONE;
-  // the fused-RMSNorm kernels hold the norm weights through the stream issue: 9 rows per
-  // wave keep them within 128 VGPRs (two resident workgroups per CU)
-  if (!plan_gemv(w->n, w->k, m, outliers, csr, &pl, pro == SPECTRA_PROLOGUE_RMSNORM ? 9 : kRpwMax))
+  const int kpro = pro == SPECTRA_PROLOGUE_RMSNORM ? kProRms : pro == SPECTRA_PROLOGUE_SILU_MUL ? kProSiluMul : kProNone;
+  if (!plan_gemv(w->n, w->k, m, outliers, csr, &pl, gemv_rpw_two_per_cu(w->format, kpro)))
     return fail(SPECTRA_ERR_UNSUPPORTED, "shape not served by the GEMV family (use the GEMM family)");
   SPECTRA_REQUIRE(w->hadamard_block == 0 || w->hadamard_block <= 512, "GEMV serves hadamard_block <= 512");
   SPECTRA_REQUIRE(ptr_aligned(x, 16) && ldx % 8 == 0, "x must be 16-byte aligned with a row stride multiple of 8");

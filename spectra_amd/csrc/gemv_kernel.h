@@ -80,6 +80,14 @@ constexpr int kProNone = 0;     // x as given
 constexpr int kProSiluMul = 1;  // x row = [g | u] (2K values): fp16(silu(g) * u)
 constexpr int kProRms = 2;      // x = h: h * w_norm, times rsqrt(mean(h^2) + eps) in the epilogue
 
+// Rows per wave of the one-row 8-wave kernels when two workgroups share a CU (large N):
+// four waves per SIMD leave 128 VGPRs per wave, and these are the largest row counts that
+// compile within that without spilling (the fused prologues and Format A's zero points
+// hold more registers per row).  Those kernels are built for four waves per SIMD.
+constexpr int gemv_rpw_two_per_cu(int fmt, int pro) {
+  return fmt != SPECTRA_FMT_NF4 ? 8 : pro == kProRms ? 8 : pro == kProSiluMul ? 9 : kRpwMax;
+}
+
 __device__ __forceinline__ float pow2f(int e) {  // e in [-126, 127]
   return __builtin_bit_cast(float, (uint32_t)(e + 127) << 23);
 }
@@ -277,8 +285,11 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// One-row 8-wave kernels run two workgroups per CU in the large-N plans: four waves per
+// SIMD, i.e. at most 128 VGPRs (one more and the second workgroup no longer fits).
 template <int FMT, int MT, int RPW, bool BF, int PRO = kProNone, int LB = 512>
-__global__ void __launch_bounds__(LB) gemv_kernel(const GemvParams p) {
+__global__ void __launch_bounds__(LB, (MT == 1 && LB == 512 && RPW <= gemv_rpw_two_per_cu(FMT, PRO) ? 4 : 1))
+    gemv_kernel(const GemvParams p) {
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int XH = 2 * MT;  // 16-element half-runs of activations per thread (at most)
   const int tid = threadIdx.x;
