@@ -98,18 +98,22 @@ def gemv_bytes(q: C.NF4Weight, m: int = 1) -> int:
 
 class Launcher:
     """Pre-bound linear call (descriptor, x, out[, workspace]) -> one ctypes call each.
-    m <= GEMV_MAX_M uses the GEMV family, larger m the MFMA GEMM."""
+    m = 1 uses the GEMV family, 2 <= m <= GEMV_MAX_M the dispatching entry
+    (spectra_w4a16_linear: GEMV or small-batch family by shape), larger m the GEMM entry."""
 
     def __init__(self, lib, ops: K.QWeightOperands, x: torch.Tensor, out: torch.Tensor):
         m = x.shape[0]
         self.ops = ops
-        if m <= K.GEMV_MAX_M:
+        if m == 1:
             self.name, self.fn = "spectra_w4a16_gemv", lib.spectra_w4a16_gemv
             self.args = (ctypes.byref(ops.desc), x.data_ptr(), x.stride(0), m, L.F16, out.data_ptr(), out.stride(0))
         else:
             ws = lib.spectra_w4a16_gemm_workspace(ctypes.byref(ops.desc), m, L.F16)
-            self.ws = torch.empty(int(ws), dtype=torch.uint8, device=x.device)
-            self.name, self.fn = "spectra_w4a16_gemm", lib.spectra_w4a16_gemm
+            self.ws = torch.empty(max(int(ws), 256), dtype=torch.uint8, device=x.device)
+            if m <= K.GEMV_MAX_M:
+                self.name, self.fn = "spectra_w4a16_linear", lib.spectra_w4a16_linear
+            else:
+                self.name, self.fn = "spectra_w4a16_gemm", lib.spectra_w4a16_gemm
             self.args = (ctypes.byref(ops.desc), x.data_ptr(), x.stride(0), m, L.F16, out.data_ptr(), out.stride(0),
                          self.ws.data_ptr(), self.ws.numel())
 

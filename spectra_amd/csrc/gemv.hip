@@ -94,6 +94,16 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
 
 static bool ptr_aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// workgroups of the plan for m activation rows (0 when the family does not serve the shape);
+// the descriptor is already validated
+int gemv_plan_grid(const spectra_qweight_t* w, int m) {
+  const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
+  const bool outliers = w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS || csr;
+  GemvPlan pl;
+  if (!plan_gemv(w->n, w->k, m, outliers, csr, &pl, gemv_rpw_two_per_cu(w->format, kProNone))) return 0;
+  return pl.grid;
+}
+
 int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, int act_dtype, void* out,
                 int64_t ldo, hipStream_t stream, const spectra_gemv_fusion_t* fu) {
   const bool outliers = w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS ||

@@ -524,8 +524,9 @@ static bool plan_skinny(int64_t n, int64_t k, SkinnyPlan* pl) {
 
 // Returns SPECTRA_ERR_UNSUPPORTED (and launches nothing) when the operands are not
 // served by this family: the caller then uses the prefill GEMM.
-int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m, int act_dtype, void* out,
-                  int64_t ldo, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+// SPECTRA_OK when this family serves the operands (the descriptor already validated),
+// SPECTRA_ERR_UNSUPPORTED with the reason otherwise
+int skinny_supported(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m) {
   if (m < 2 || m > 16) return fail(SPECTRA_ERR_UNSUPPORTED, "small-batch family serves 2 <= m <= 16");
   if (w->format != SPECTRA_FMT_NF4 || w->group_size != 64)
     return fail(SPECTRA_ERR_UNSUPPORTED, "small-batch family serves NF4 with blocks of 64");
@@ -544,6 +545,16 @@ int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_
     return fail(SPECTRA_ERR_UNSUPPORTED, "small-batch family needs 16-byte aligned activation rows");
   SkinnyPlan pl;
   if (!plan_skinny(w->n, w->k, &pl)) return fail(SPECTRA_ERR_UNSUPPORTED, "no small-batch plan for this shape");
+  return SPECTRA_OK;
+}
+
+int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m, int act_dtype, void* out,
+                  int64_t ldo, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const int sup = skinny_supported(w, x, ldx, m);
+  if (sup != SPECTRA_OK) return sup;
+  SkinnyPlan pl;
+  plan_skinny(w->n, w->k, &pl);
+  const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
   const size_t need = skinny_workspace(w, m);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(SPECTRA_ERR_WORKSPACE, "workspace missing or smaller than spectra_w4a16_gemm_workspace()");

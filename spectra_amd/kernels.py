@@ -151,6 +151,8 @@ def _run_linear(ops: QWeightOperands, x2: torch.Tensor, out2: torch.Tensor, fami
     m, k = x2.shape
     adt = _DT[x2.dtype]
     stream = _stream(x2.device)
+    if family == "linear" and m == 1:
+        family = "gemv"  # one row: the GEMV family, no workspace
     if family == "gemv":
         st = lib.spectra_w4a16_gemv(ops.ptr(), x2.data_ptr(), x2.stride(0), m, adt, out2.data_ptr(),
                                     out2.stride(0), stream)
@@ -208,7 +210,7 @@ def fused_w4a16_gemv_hdsq(x: torch.Tensor, packed_w: torch.Tensor, scales: torch
         raise ValueError(f"out must be [B={B}, N={N}], got {tuple(out.shape)}")
     target = out if (out.dtype == x2.dtype and out.stride(1) == 1) else torch.empty((B, N), device=x.device,
                                                                                       dtype=x2.dtype)
-    _run_linear(ops, x2, target, "gemv" if B <= GEMV_MAX_M else "gemm")
+    _run_linear(ops, x2, target, "linear" if B <= GEMV_MAX_M else "gemm")
     if target is not out:
         out.copy_(target)
     return out.squeeze(0) if orig_1d else out
