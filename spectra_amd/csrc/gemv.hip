@@ -28,7 +28,8 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   int rpw = (int)((want + G - 1) / G);
   const int rpw_max = mt == 4 ? 8 : kRpwMax;
   bool wide = false;
-  if (rpw > rpw_max && mt == 1) {
+  const bool two = rpw > rpw_max && mt == 1;
+  if (two) {
     // more rows than one resident workgroup per CU holds: size for two per CU (LDS <= 80 KB
     // below, at most rpw2 rows per wave: the kernels built for 128 VGPRs), so that one
     // workgroup's set-up overlaps the other's stream
@@ -49,7 +50,10 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
     }
   }
   rpw = rpw < 1 ? 1 : (rpw > rpw_max ? rpw_max : rpw);
-  const int R = G * rpw;
+  // exactly the rows that spread N over the CUs (one workgroup per CU, or two in the large-N
+  // plan): the last row of some waves then stays empty, and every CU streams
+  const int64_t per_wg = two ? (n + 511) / 512 : want;
+  const int R = (int64_t)G * rpw > per_wg ? (int)per_wg : G * rpw;
   const int BD = 64 * S * G;
   // each thread stages at most mt 32-element activation runs
   const int64_t runs = (int64_t)mt * (k / 32);

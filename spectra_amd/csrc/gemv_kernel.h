@@ -645,6 +645,14 @@ __global__ void __launch_bounds__(LB, (MT == 1 && LB == 512 && RPW <= gemv_rpw_t
   const uint32_t lanebits = (uint32_t)lane << 2;  // this lane's LUT copy: conflict-free reads
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
+    // the plan may leave the last row of some waves empty (R < G x RPW): the 16-wave kernels
+    // skip its decode (a wave-uniform branch; in the 8-wave kernels with more rows the branch
+    // costs spills, so there the row is decoded and zeroed)
+    if (LB > 512 && i == RPW - 1 && g + i * p.G >= Rw) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) vals[i * MT + m] = 0.0f;
+      continue;
+    }
     float acc[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
