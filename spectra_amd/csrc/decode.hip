@@ -27,13 +27,25 @@ namespace spectra {
 constexpr int kDecThreads = 256;
 constexpr int kSpanMax = 64;  // positions per attention workgroup (one per lane of wave 0)
 
+// Butterflies across the wave through DPP and the permlane swaps (lane_xor), no LDS round
+// trips; the same partners and order as a __shfl_xor butterfly, so the same results.
 __device__ __forceinline__ float wave_sum(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  const int lane = __lane_id();
+  v += lane_xor<32>(v, lane);
+  v += lane_xor<16>(v, lane);
+  v += lane_xor<8>(v, lane);
+  v += lane_xor<4>(v, lane);
+  v += lane_xor<2>(v, lane);
+  return v + lane_xor<1>(v, lane);
 }
 __device__ __forceinline__ float wave_max(float v) {
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  const int lane = __lane_id();
+  v = fmaxf(v, lane_xor<32>(v, lane));
+  v = fmaxf(v, lane_xor<16>(v, lane));
+  v = fmaxf(v, lane_xor<8>(v, lane));
+  v = fmaxf(v, lane_xor<4>(v, lane));
+  v = fmaxf(v, lane_xor<2>(v, lane));
+  return fmaxf(v, lane_xor<1>(v, lane));
 }
 
 // One workgroup per row.  Rows of hidden % 8 == 0 (<= 8192) are read as 16-byte chunks, all
@@ -153,9 +165,27 @@ __global__ void rope_append_kernel(const uint16_t* __restrict__ qkv, int64_t ldq
 // ends with the group's total.
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int off = 1; off < W; off <<= 1) v += __shfl_xor(v, off, 64);
+  const int lane = __lane_id();
+  if constexpr (W > 1) v += lane_xor<1>(v, lane);
+  if constexpr (W > 2) v += lane_xor<2>(v, lane);
+  if constexpr (W > 4) v += lane_xor<4>(v, lane);
+  if constexpr (W > 8) v += lane_xor<8>(v, lane);
+  if constexpr (W > 16) v += lane_xor<16>(v, lane);
+  if constexpr (W > 32) v += lane_xor<32>(v, lane);
   return v;
+}
+
+// Sum over the lanes of a wave that are W, 2W, ... apart (W a power of two < 64): every
+// lane ends with the total of its residue class mod W.
+template <int W>
+__device__ __forceinline__ float stride_sum(float v) {
+  const int lane = __lane_id();
+  if constexpr (W <= 1) v += lane_xor<1>(v, lane);
+  if constexpr (W <= 2) v += lane_xor<2>(v, lane);
+  if constexpr (W <= 4) v += lane_xor<4>(v, lane);
+  if constexpr (W <= 8) v += lane_xor<8>(v, lane);
+  if constexpr (W <= 16) v += lane_xor<16>(v, lane);
+  return v + lane_xor<32>(v, lane);
 }
 
 __device__ __forceinline__ void unpack8(const uint4& u, float (&f)[8]) {
@@ -273,9 +303,22 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
   __shared__ float sc[G][kSpanMax];        // scores, then exponentials
   __shared__ float wsum[4][G][HD];         // V sums of the four waves
   const int kh = blockIdx.x, sp = blockIdx.y, nspan = gridDim.y, tid = threadIdx.x;
+  const int t0 = sp * kSpanMax;
+  const int dg = tid % DG, pr = tid / DG;
+  // fp16 cache: the span's K / V rows first, at addresses independent of the position (rows
+  // clamped into the cache; those past the position are masked below), so they are in
+  // flight while the position arrives (a scalar load)
+  uint4 kr[NP], vr[NP];
+  if constexpr (!Q4) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int64_t t = min(t0 + pr + i * PPW, lmax - 1);
+      kr[i] = *(const uint4*)(kvc.k + ((int64_t)kh * lmax + t) * HD + dg * 8);
+      vr[i] = *(const uint4*)(kvc.v + ((int64_t)kh * lmax + t) * HD + dg * 8);
+    }
+  }
   int64_t pos = *pos_p;
   pos = pos < 0 ? 0 : (pos >= lmax ? lmax - 1 : pos);
-  const int t0 = sp * kSpanMax;
   const int n = (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform
   float* pbase = part + ((int64_t)kh * G * nspan + sp) * (HD + 2);  // head j: + j * nspan * (HD + 2)
   if (n <= 0) {  // span past the position: an empty piece for the merge
@@ -283,9 +326,9 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
       pbase[(int64_t)tid * nspan * (HD + 2) + HD] = -INFINITY;
       pbase[(int64_t)tid * nspan * (HD + 2) + HD + 1] = 0.0f;
     }
+    if constexpr (!Q4) __builtin_amdgcn_s_waitcnt(0x0f70);  // the span's loads land before the wave ends
     return;
   }
-  const int dg = tid % DG, pr = tid / DG;
   const bool upper = dg * 8 >= H2;
   const int pdg = upper ? dg - H2 / 8 : dg + H2 / 8;  // partner chunk
   const int tnew = (int)(pos - t0);                   // < 64 when this span holds pos
@@ -320,14 +363,19 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
   auto row16 = [&](const uint16_t* base, int64_t t) __attribute__((always_inline)) {
     return base + ((int64_t)kh * W + (Q4 ? t % W : t)) * HD + dg * 8;
   };
-  uint4 kr[NP], vr[NP];
   uint32_t inwin = 0;  // Q4: bit i = pass i's position is in the fp16 window
 #pragma unroll
   for (int i = 0; i < NP; ++i) {
     const int tl = pr + i * PPW;
+    if constexpr (!Q4) {
+      // rows past the position hold whatever the cache held: their scores are masked, and
+      // their values are zeroed so that a zero weight cannot meet a NaN
+      if (tl >= n) vr[i] = make_uint4(0, 0, 0, 0);
+      continue;
+    }
     const int64_t t = t0 + (tl < n ? tl : 0);  // past the end: re-read the first (in bounds)
-    if (!Q4 || t > pos - W) {
-      if (Q4) inwin |= 1u << i;
+    if (t > pos - W) {
+      inwin |= 1u << i;
       kr[i] = *(const uint4*)row16(kvc.k, t);
       vr[i] = *(const uint4*)row16(kvc.v, t);
     } else {
@@ -430,12 +478,7 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
 #pragma unroll
   for (int j = 0; j < G; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float a = acc[j][e];
-#pragma unroll
-      for (int off = DG; off < 64; off <<= 1) a += __shfl_xor(a, off, 64);
-      acc[j][e] = a;
-    }
+    for (int e = 0; e < 8; ++e) acc[j][e] = stride_sum<DG>(acc[j][e]);
   if (lane < DG) {
 #pragma unroll
     for (int j = 0; j < G; ++j)

@@ -85,7 +85,7 @@ def _tables(L, hd):
 
 
 @pytest.mark.parametrize("heads,kv,hd,L", [(24, 8, 128, 768), (4, 4, 64, 1000), (8, 2, 256, 130), (6, 3, 64, 64),
-                                           (32, 4, 128, 300), (12, 2, 64, 200)])
+                                           (32, 4, 128, 300), (12, 2, 64, 200), (24, 8, 128, 1100)])
 @pytest.mark.parametrize("rope", [True, False])
 def test_attend_decode(hip, heads, kv, hd, L, rope):
     g = torch.Generator(device="cuda").manual_seed(heads * L + rope)
@@ -94,7 +94,7 @@ def test_attend_decode(hip, heads, kv, hd, L, rope):
     cos, sin = _tables(L, hd) if rope else (None, None)
     ws = torch.full((K.attend_workspace_bytes(heads, hd, L),), 255, device="cuda", dtype=torch.uint8)  # reused
     grp = heads // kv
-    for p in sorted({0, 1, 62, 63, 64, 65, L // 2, L - 2, L - 1}):
+    for p in sorted({0, 1, 62, 63, 64, 65, 511, 512, 513, L // 2, L - 2, L - 1}):
         if p >= L:
             continue
         case(heads=heads, kv=kv, hd=hd, L=L, rope=rope, pos=p)
@@ -118,6 +118,28 @@ def test_attend_decode(hip, heads, kv, hd, L, rope):
         ref = torch.matmul(torch.softmax(sc, -1)[:, None, :], vv.contiguous())[:, 0, :]
         err = (out.float() - ref).abs().max().item()
         assert err <= 2e-3 * vc.abs().max().item(), (p, err)
+
+
+@pytest.mark.parametrize("L", [600, 1100])
+def test_attend_decode_ignores_rows_past_position(hip, L):
+    """Cache rows past the position may hold anything (here NaN): the output and the rows
+    up to the position are those of a cache with finite values there."""
+    heads, kv, hd, p = 24, 8, 128, 300
+    g = torch.Generator(device="cuda").manual_seed(L)
+    kc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+    vc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+    cos, sin = _tables(L, hd)
+    qkv = (torch.randn((heads + 2 * kv) * hd, device="cuda", generator=g) * 2).half()
+    pos = torch.tensor([p], device="cuda", dtype=torch.int64)
+    ws = torch.zeros((K.attend_workspace_bytes(heads, hd, L),), device="cuda", dtype=torch.uint8)
+    kf, vf = kc.clone(), vc.clone()
+    ref = K.attend_decode(qkv, pos, cos, sin, heads, kv, kf, vf, ws)
+    kc[:, p + 1:, :] = float("nan")
+    vc[:, p + 1:, :] = float("nan")
+    out = K.attend_decode(qkv, pos, cos, sin, heads, kv, kc, vc, ws)
+    assert torch.isfinite(out).all()
+    assert torch.equal(out, ref)
+    assert torch.equal(kc[:, : p + 1], kf[:, : p + 1]) and torch.equal(vc[:, : p + 1], vf[:, : p + 1])
 
 
 @pytest.mark.parametrize("rows,inter", [(1, 8192), (7, 300)])
