@@ -184,6 +184,27 @@ __device__ __forceinline__ float lane_xor(float v, int lane) {
   }
 }
 
+// All-reductions across the wave through lane_xor (no LDS round trips): partners 32, 16,
+// ..., 1, the order of a __shfl_xor butterfly, so the same result in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  const int lane = __lane_id();
+  v += lane_xor<32>(v, lane);
+  v += lane_xor<16>(v, lane);
+  v += lane_xor<8>(v, lane);
+  v += lane_xor<4>(v, lane);
+  v += lane_xor<2>(v, lane);
+  return v + lane_xor<1>(v, lane);
+}
+__device__ __forceinline__ float wave_max(float v) {
+  const int lane = __lane_id();
+  v = fmaxf(v, lane_xor<32>(v, lane));
+  v = fmaxf(v, lane_xor<16>(v, lane));
+  v = fmaxf(v, lane_xor<8>(v, lane));
+  v = fmaxf(v, lane_xor<4>(v, lane));
+  v = fmaxf(v, lane_xor<2>(v, lane));
+  return fmaxf(v, lane_xor<1>(v, lane));
+}
+
 // Butterfly across lanes at distance LB: v += c * partner with c = +1 on the low side and
 // -1 on the high side, leaving u + v low and -(u - v) high (the product by +-1 is exact
 // and the fma rounds once, as the reference's add / subtract does).  Partners share their

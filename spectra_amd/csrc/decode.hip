@@ -27,26 +27,6 @@ namespace spectra {
 constexpr int kDecThreads = 256;
 constexpr int kSpanMax = 64;  // positions per attention workgroup (one per lane of wave 0)
 
-// Butterflies across the wave through DPP and the permlane swaps (lane_xor), no LDS round
-// trips; the same partners and order as a __shfl_xor butterfly, so the same results.
-__device__ __forceinline__ float wave_sum(float v) {
-  const int lane = __lane_id();
-  v += lane_xor<32>(v, lane);
-  v += lane_xor<16>(v, lane);
-  v += lane_xor<8>(v, lane);
-  v += lane_xor<4>(v, lane);
-  v += lane_xor<2>(v, lane);
-  return v + lane_xor<1>(v, lane);
-}
-__device__ __forceinline__ float wave_max(float v) {
-  const int lane = __lane_id();
-  v = fmaxf(v, lane_xor<32>(v, lane));
-  v = fmaxf(v, lane_xor<16>(v, lane));
-  v = fmaxf(v, lane_xor<8>(v, lane));
-  v = fmaxf(v, lane_xor<4>(v, lane));
-  v = fmaxf(v, lane_xor<2>(v, lane));
-  return fmaxf(v, lane_xor<1>(v, lane));
-}
 
 // One workgroup per row.  Rows of hidden % 8 == 0 (<= 8192) are read as 16-byte chunks, all
 // issued before the first use (every chunk of the row is in flight at once); other rows take
@@ -629,14 +609,22 @@ __global__ void __launch_bounds__(kArgThreads) greedy_kernel(const uint16_t* __r
       besti = i;
     }
   }
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float ov = __shfl_xor(best, off, 64);
-    const int oi = __shfl_xor(besti, off, 64);
+  // across the wave: DPP / permlane butterflies (partners 32, 16, ..., 1), value and index
+  // moved as bits
+  const int lane = tid & 63;
+  auto take = [&](float ov, float oib) __attribute__((always_inline)) {
+    const int oi = __builtin_bit_cast(int, oib);
     if (arg_better(ov, oi, best, besti)) {
       best = ov;
       besti = oi;
     }
-  }
+  };
+  take(lane_xor<32>(best, lane), lane_xor<32>(__builtin_bit_cast(float, besti), lane));
+  take(lane_xor<16>(best, lane), lane_xor<16>(__builtin_bit_cast(float, besti), lane));
+  take(lane_xor<8>(best, lane), lane_xor<8>(__builtin_bit_cast(float, besti), lane));
+  take(lane_xor<4>(best, lane), lane_xor<4>(__builtin_bit_cast(float, besti), lane));
+  take(lane_xor<2>(best, lane), lane_xor<2>(__builtin_bit_cast(float, besti), lane));
+  take(lane_xor<1>(best, lane), lane_xor<1>(__builtin_bit_cast(float, besti), lane));
   if ((tid & 63) == 0) {
     bv[tid >> 6] = best;
     bi[tid >> 6] = besti;

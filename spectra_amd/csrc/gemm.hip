@@ -143,7 +143,7 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
   for (int u = 0; u < kPrepU; ++u)
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(v[u][e]));
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = wave_max(mx);
   if ((tid & 63) == 0) wmax[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));

@@ -582,7 +582,7 @@ __global__ void __launch_bounds__(LB, (MT == 1 && LB == 512 && RPW <= gemv_rpw_t
   if constexpr (!kEarlyOutl) load_outliers();
 
   if constexpr (PRO == kProRms) {  // per-wave sums of h^2, fixed order
-    for (int off = 32; off >= 1; off >>= 1) ssq += __shfl_xor(ssq, off, 64);
+    ssq = wave_sum(ssq);
     if (lane == 0) ((float*)(smem + p.off_ss))[wave] = ssq;
   }
 

@@ -76,7 +76,7 @@ __global__ void __launch_bounds__(kSkPrepThreads) skinny_prep_kernel(const void*
     }
   }
   for (int i = tid; i < len; i += kSkPrepThreads) fs[i] = to_f32_16(row[k0 + i], dt);
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = wave_max(mx);
   if ((tid & 63) == 0) wmax[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
@@ -168,7 +168,7 @@ __global__ void __launch_bounds__(kSkPrepThreads) skinny_prep_fast_kernel(
       mx = fmaxf(mx, fabsf(to_f32_16((uint16_t)(u[j] >> 16), dt)));
     }
   }
-  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  mx = wave_max(mx);
   if (lane == 0) wmax[tid >> 6] = mx;
   // compressor.py:34-39: stages h = 1, 2, 4 on register bits, then across lanes
 #pragma unroll
