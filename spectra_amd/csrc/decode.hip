@@ -577,38 +577,39 @@ __global__ void __launch_bounds__(kArgThreads) greedy_kernel(const uint16_t* __r
   __shared__ float bv[kArgThreads / 64];
   __shared__ int bi[kArgThreads / 64];
   const int tid = threadIdx.x;
+  // A thread visits its indices in increasing order, so inside the thread "better" is a
+  // strict > (the first of equal maxima stays) or a first NaN; the scan starts from the
+  // thread's first element.  Across threads arg_better applies the full rule.
   float best = -INFINITY;
   int besti = 0x7fffffff;
+  bool first = true;
+  auto visit = [&](float f, int i) __attribute__((always_inline)) {
+    const bool take = first || f > best || (f != f && best == best);
+    best = take ? f : best;
+    besti = take ? i : besti;
+    first = false;
+  };
+  constexpr int Q = 16;  // chunks of 8 in flight per thread: 131072 logits per round trip
   const int nch = n >> 3;
-  for (int c0 = 0; c0 < nch; c0 += 4 * kArgThreads) {  // 4 chunks of 8 in flight per thread
-    uint4 u[4];
+  for (int c0 = 0; c0 < nch; c0 += Q * kArgThreads) {
+    uint4 u[Q];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < Q; ++q) {
       const int ch = c0 + tid + q * kArgThreads;
       u[q] = ((const uint4*)logits)[ch < nch ? ch : 0];
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < Q; ++q) {
       const int ch = c0 + tid + q * kArgThreads;
       if (ch < nch) {
         float f[8];
         unpack8(u[q], f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (arg_better(f[e], 8 * ch + e, best, besti)) {
-            best = f[e];
-            besti = 8 * ch + e;
-          }
+        for (int e = 0; e < 8; ++e) visit(f[e], 8 * ch + e);
       }
     }
   }
-  for (int i = (nch << 3) + tid; i < n; i += kArgThreads) {  // tail
-    const float f = h2f(logits[i]);
-    if (arg_better(f, i, best, besti)) {
-      best = f;
-      besti = i;
-    }
-  }
+  for (int i = (nch << 3) + tid; i < n; i += kArgThreads) visit(h2f(logits[i]), i);  // tail
   // across the wave: DPP / permlane butterflies (partners 32, 16, ..., 1), value and index
   // moved as bits
   const int lane = tid & 63;

@@ -171,6 +171,44 @@ def test_greedy_next(hip, n):
     assert int(pos) == 4 and int(hist[4]) == n // 3 and int((hist == -1).sum()) == 9
 
 
+def _argmax_rule(x: torch.Tensor) -> int:
+    """torch.argmax's rule, stated on the host: the first NaN, else the first maximum."""
+    v = x.float().cpu()
+    nan = torch.nonzero(torch.isnan(v))
+    if nan.numel():
+        return int(nan[0])
+    return int(torch.nonzero(v == v.max())[0])
+
+
+@pytest.mark.parametrize("n", [128256, 300001, 4097])
+def test_greedy_next_ties_infinities_nans(hip, n):
+    """Equal maxima across scan rounds and threads, all -inf, one finite value among -inf,
+    NaNs (several), and the tail past the last 8-value chunk."""
+    case(n=n)
+    token = torch.zeros(1, dtype=torch.int64, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(n + 1)
+    cases = []
+    x = torch.full((n,), 2.0, device="cuda", dtype=torch.float16)
+    cases.append(x.clone())  # all equal: index 0
+    cases.append(torch.full((n,), float("-inf"), device="cuda", dtype=torch.float16))  # all -inf
+    x = torch.full((n,), float("-inf"), device="cuda", dtype=torch.float16)
+    x[n - 2] = -3.0
+    cases.append(x)  # one finite value
+    x = torch.randn(n, device="cuda", generator=gen).half()
+    x[n - 1] = 50.0
+    x[7] = 50.0
+    x[n // 2 + 3] = 50.0
+    cases.append(x)  # ties far apart (other rounds, other threads, the tail)
+    x = torch.randn(n, device="cuda", generator=gen).half()
+    x[n - 1] = float("nan")
+    x[n // 3 + 5] = float("nan")
+    x[2] = 60.0
+    cases.append(x)  # NaNs: the first NaN
+    for x in cases:
+        K.greedy_next(x, token)
+        assert int(token) == _argmax_rule(x)
+
+
 # ---------------------------------------------------------------------------
 # the GEMV with fused RMSNorm / SiLU-mul prologues and residual epilogue
 # ---------------------------------------------------------------------------
