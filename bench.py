@@ -204,7 +204,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the multi-GPU sharding is design-only (DESIGN.md)", file=sys.stderr)
+              "sharding across GPUs is not built: each GPU would run these kernels at its shard's shape",
+              file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py: no GPU", file=sys.stderr)
