@@ -479,6 +479,46 @@ def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     check_y(y, y_t, torch.bfloat16)
 
 
+@pytest.mark.parametrize("m", [2, 4])
+def test_linear_dispatch_with_and_without_workspace(hip, m):
+    """spectra_w4a16_linear on a wide layer (N=16384, K=3072: the 2-4-row GEMV plan needs more
+    than one workgroup per CU): with the workspace the rows go to the small-batch family,
+    with none (or one too small) they stay on the GEMV; both against the fp32 reference."""
+    import ctypes
+    from spectra_amd import _lib as L
+    case(m=m)
+    n, k = 16384, 3072
+    g = torch.Generator().manual_seed(m)
+    w = (torch.randn(n, k, generator=g) * 0.02).half()
+    nnz = int(round(0.005 * n * k))
+    pos = torch.randperm(n * k, generator=g)[:nnz]
+    mask = torch.zeros(n * k, dtype=torch.bool)
+    mask[pos] = True
+    w.view(-1)[pos] = (torch.randn(nnz, generator=g) * 0.2).half()
+    q = C.quantize_nf4(w.cuda(), 64, 0, mask.view(n, k).cuda(), True)
+    q.hadamard_block = 128
+    col, val = q.outliers()
+    ops = K.QWeightOperands(q.packed, q.absmax, None, k, marlin_layout=True, outlier_idx=col, outlier_w=val,
+                            **q.kernel_kwargs())
+    x = torch.randn(m, k, generator=g).half().cuda()
+    w_eff = K.w4_dequant(q.packed, q.absmax, None, out_dtype=torch.float32, codebook="nf4", marlin_layout=True,
+                         outlier_idx=q.col, outlier_w=q.val, outlier_rowptr=q.rowptr)
+    y_t = (K.fwht_rows(x, 128, out_dtype=torch.float32) @ w_eff.T).double().cpu().numpy()
+    lib = L.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    need = int(lib.spectra_w4a16_gemm_workspace(ctypes.byref(ops.desc), m, L.F16))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    outs = []
+    for wptr, wbytes in ((ws.data_ptr(), need), (None, 0), (ws.data_ptr(), need - 256)):
+        y = torch.full((m, n), float("nan"), dtype=torch.float16, device="cuda")
+        st = lib.spectra_w4a16_linear(ctypes.byref(ops.desc), x.data_ptr(), k, m, L.F16, y.data_ptr(), n, wptr,
+                                      wbytes, stream)
+        assert st == L.OK, lib.spectra_last_error()
+        check_y(y, y_t, torch.float16)
+        outs.append(y)
+    assert torch.equal(outs[1], outs[2])  # both stayed on the GEMV
+
+
 # ---------------------------------------------------------------------------
 # engineering properties
 # ---------------------------------------------------------------------------
