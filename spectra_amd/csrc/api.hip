@@ -77,6 +77,26 @@ int ensure_lds_limit(const void* kernel, bool dyn_at_zero) {
   return SPECTRA_OK;
 }
 
+int device_cu_count() {
+  static std::mutex mu;
+  static std::vector<std::pair<int, int>> known;  // (device, CUs)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  for (const auto& d : known)
+    if (d.first == dev) return d.second;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+    (void)hipGetLastError();
+    cus = 256;
+  }
+  known.emplace_back(dev, cus);
+  return cus;
+}
+
 }  // namespace spectra
 
 // gemv.hip / gemm.hip

@@ -38,6 +38,10 @@ int validate_qweight(const spectra_qweight_t* w);
 // dyn_at_zero: the kernel addresses dynamic LDS from address 0 (fails if it has static LDS).
 int ensure_lds_limit(const void* kernel, bool dyn_at_zero = false);
 inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+// Compute units of the current device (hipDeviceAttributeMultiprocessorCount, queried once
+// per device): the launch plans size their grids to it.  Falls back to 256 (MI355X) if the
+// query fails.
+int device_cu_count();
 
 // ---------------------------------------------------------------------------
 // NF4 codebook (compressor.py:22-27): fp32 literals and their fp16 roundings

@@ -4,6 +4,7 @@
 #include <cmath>
 
 #include "gemv_kernel.h"
+#include "gemv_stream.h"
 
 namespace spectra {
 
@@ -98,9 +99,124 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
 
 static bool ptr_aligned(const void* p, int a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// ---------------------------------------------------------------------------
+// stream kernel plan (one activation row, NF4, K a multiple of 1024)
+// ---------------------------------------------------------------------------
+struct StreamPlan {
+  int W, P, RG, NS, R, grid, ocap, pmagic, cpr;
+  uint32_t off_xp, off_xsc, off_part, off_rp, off_bias, off_res, off_ss, off_sc, off_op, lds_bytes;
+};
+
+// R = ceil(N / CUs) rows per workgroup (one workgroup per CU); W waves with 2W a multiple
+// of P = K / 1024, the most waves among those that give the fewest slots per lane
+static bool plan_stream(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block, int ncu, StreamPlan* pl) {
+  if (k % 1024 != 0 || k > 16384 || ncu <= 0) return false;
+  if ((k / block) % 8 != 0 || (lda * 2) % 16 != 0) return false;  // absmax rows in whole 16-byte chunks
+  const int P = (int)(k / 1024);
+  const int64_t R = (n + ncu - 1) / ncu;
+  int bestW = 0, bestNS = 1 << 30;
+  for (int W = 16; W >= 4; --W) {
+    if ((2 * W) % P != 0 || 64 * W < k / 16) continue;  // one activation half-run per thread
+    const int RG = 2 * W / P;
+    const int NS = (int)((R + RG - 1) / RG);
+    if (NS < bestNS) {
+      bestNS = NS;
+      bestW = W;
+    }
+  }
+  if (bestW == 0 || bestNS > kStreamMaxSlots) return false;
+  // 32-bit per-lane byte offsets from the workgroup's first row
+  if (R * ldp >= (int64_t(1) << 31) || R * lda * 2 >= (int64_t(1) << 31)) return false;
+  pl->W = bestW;
+  pl->P = P;
+  pl->RG = 2 * bestW / P;
+  pl->NS = bestNS;
+  pl->R = (int)R;
+  pl->grid = (int)((n + R - 1) / R);
+  pl->pmagic = (65536 + P - 1) / P;
+  pl->cpr = (int)(k / block / 8);
+  if (R * pl->cpr > 64 * bestW) return false;  // one absmax chunk per thread
+  uint32_t off = kLutBytes;
+  pl->off_xp = off;
+  off = align16(off + (uint32_t)(k * 2));
+  pl->off_xsc = off;
+  off = align16(off + (uint32_t)(k / 32 * 4));
+  pl->off_part = off;
+  off = align16(off + (uint32_t)(R * P * 4));
+  pl->off_rp = off;
+  off = align16(off + (uint32_t)((R + 1) * 4));
+  pl->off_bias = off;
+  off = align16(off + (uint32_t)(R * 4));
+  pl->off_res = off;
+  off = align16(off + (uint32_t)(R * 2));
+  pl->off_ss = off;
+  off = align16(off + (uint32_t)(kMaxWaves * 4));
+  pl->off_sc = off;
+  off = align16(off + (uint32_t)(R * pl->cpr * 16));
+  pl->off_op = off;
+  if (off + 4 > 163840) return false;
+  int ocap = kStreamOutlierLoads * 64 * bestW;
+  const int fit = (int)((163840 - off) / 4u);
+  if (ocap > fit) ocap = fit;
+  pl->ocap = ocap;
+  pl->lds_bytes = align16(off + (uint32_t)(ocap * 4));
+  return pl->lds_bytes <= 163840;
+}
+
+static int stream_launch(const spectra_qweight_t* w, const StreamPlan& pl, const void* x, int act_dtype, void* out,
+                         hipStream_t stream, const spectra_gemv_fusion_t* fu, int kpro) {
+  StreamParams p;
+  p.packed = w->packed; p.ldp = w->packed_stride;
+  p.absmax = w->scales; p.lda = w->scales_stride;
+  const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
+  p.rowptr = csr ? w->csr_rowptr : nullptr;
+  p.ccol = csr ? w->csr_col : nullptr;
+  p.cval = csr ? w->csr_val : nullptr;
+  p.csr = csr ? 1 : 0;
+  p.csr_nnz = csr ? (int)w->csr_nnz : 0;
+  p.bias = w->bias; p.bias_dt = w->bias_dtype;
+  p.x = x; p.out = out;
+  p.nw = fu ? fu->norm_weight : nullptr;
+  p.res = fu ? fu->residual : nullptr;
+  p.eps = fu ? fu->eps : 0.0f;
+  p.out_scale = w->hadamard_block ? (float)(1.0 / std::sqrt((double)w->hadamard_block)) : 1.0f;
+  p.n = (int)w->n; p.k = (int)w->k;
+  p.W = pl.W; p.R = pl.R; p.P = pl.P; p.RG = pl.RG; p.pmagic = pl.pmagic;
+  int gs = 0;
+  while ((1 << gs) < w->group_size) ++gs;
+  p.gshift = gs;
+  p.log_had = 0;
+  while (p.log_had < 30 && (1 << p.log_had) < w->hadamard_block) ++p.log_had;
+  p.marlin = w->marlin_layout ? 1 : 0;
+  p.ocap = pl.ocap;
+  p.cpr = pl.cpr;
+  p.cmagic = (65536 + pl.cpr - 1) / pl.cpr;
+  p.off_sc = pl.off_sc;
+  p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_part = pl.off_part; p.off_rp = pl.off_rp;
+  p.off_bias = pl.off_bias; p.off_res = pl.off_res; p.off_ss = pl.off_ss; p.off_op = pl.off_op;
+  gemv_stream_fn fn = act_dtype == SPECTRA_BF16 ? gemv_stream_pick_bf16(pl.NS) : gemv_stream_pick_f16(pl.NS, kpro);
+  const int st = ensure_lds_limit((const void*)fn, true);
+  if (st != SPECTRA_OK) return st;
+  hipLaunchKernelGGL(fn, dim3(pl.grid), dim3(64 * pl.W), pl.lds_bytes, stream, p);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
+// the stream kernel serves one row of NF4 activations with CSR outliers or none, K a
+// multiple of 1024 up to 16384, and at most kStreamMaxSlots rows per lane
+static bool stream_serves(const spectra_qweight_t* w, int m, StreamPlan* pl) {
+  if (m != 1 || w->format != SPECTRA_FMT_NF4 || w->group_size < 32) return false;
+  if (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS) return false;
+  if (w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz >= (int64_t(1) << 29)) return false;
+  if (!ptr_aligned(w->scales, 16)) return false;
+  return plan_stream(w->n, w->k, w->packed_stride, w->scales_stride, w->group_size, device_cu_count(), pl);
+}
+
 // workgroups of the plan for m activation rows (0 when the family does not serve the shape);
 // the descriptor is already validated
 int gemv_plan_grid(const spectra_qweight_t* w, int m) {
+  StreamPlan sp;
+  if (stream_serves(w, m, &sp)) return sp.grid;
   const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
   const bool outliers = w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS || csr;
   GemvPlan pl;
@@ -128,6 +244,8 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
                     "CSR columns must be 16-byte and values 8-byte aligned (nnz < 2^31)");
   // the kernels pair each format with its own outlier kind and scale scheme: Format B
   // (NF4, blocks >= 64, CSR outliers), Format A (groups of 32, dense outlier columns)
+  StreamPlan sp;
+  if (stream_serves(w, m, &sp)) return stream_launch(w, sp, x, act_dtype, out, stream, fu, kpro);
   if (w->format == SPECTRA_FMT_NF4 && w->group_size < 64)
     return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMV family needs an NF4 block of at least 64");
   if (outliers && (w->format == SPECTRA_FMT_NF4) != csr)
