@@ -156,6 +156,22 @@ int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, int64_t ldx,
                          size_t workspace_bytes, spectra_stream_t stream);
 
 /*
+ * spectra_w4a16_linear without a workspace argument and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * workspace is a file-scope device array of SPECTRA_NOALLOC_SCRATCH_BYTES, one copy per GPU,
+ * held until the process ends; its address is looked up on the first call on each device.
+ * Calls whose workspace (spectra_w4a16_gemm_workspace) exceeds it return
+ * SPECTRA_ERR_WORKSPACE before launching anything (m <= 16 on every Llama-3.2-3B shape fits).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ * two threads) race and give undefined results.  No part of the array needs to start at
+ * zero (every kernel writes what it reads), so nothing is cleared between calls.
+ */
+#define SPECTRA_NOALLOC_SCRATCH_BYTES (8u << 20)
+int spectra_w4a16_linear_noalloc(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m,
+                                 int32_t act_dtype, void* out, int64_t ldo, spectra_stream_t stream);
+
+/*
  * Materialise W_eff [N, K] in out_dtype (F16/BF16/F32), bit-exact:
  *   Format A: round((q - z) * s in fp32), then outlier columns := round(outlier_w)
  *   Format B: round(fp32(NF4[q]) * fp32(absmax)), then CSR positions := round(val)

@@ -60,6 +60,8 @@ SIGNATURES = {
                                      c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
     "spectra_w4a16_linear": (c_int32, [ctypes.POINTER(QWeight), c_void_p, c_int64, c_int64, c_int32,
                                        c_void_p, c_int64, c_void_p, c_size_t, c_void_p]),
+    "spectra_w4a16_linear_noalloc": (c_int32, [ctypes.POINTER(QWeight), c_void_p, c_int64, c_int64, c_int32,
+                                               c_void_p, c_int64, c_void_p]),
     "spectra_w4_dequant": (c_int32, [ctypes.POINTER(QWeight), c_void_p, c_int64, c_int32, c_void_p]),
     "spectra_quantize_group32": (c_int32, [c_void_p, c_int64, c_int32, c_int64, c_int64, c_int32, c_void_p,
                                            c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -111,6 +111,59 @@ extern "C" const char* spectra_version(void) { return "spectra_hip 0.1.0 gfx950"
 
 extern "C" const char* spectra_last_error(void) { return spectra::g_last_error.c_str(); }
 
+// ---------------------------------------------------------------------------
+// no-allocation variant of spectra_w4a16_linear: its workspace is this file-scope array
+// ---------------------------------------------------------------------------
+namespace spectra {
+
+// Scratch of the no-allocation entry point: one copy per GPU the library runs on, held until
+// the process ends.  In host code the name is only a handle: its device address on each GPU
+// comes from hipGetSymbolAddress (scratch_ptr), and only that address is passed to kernels.
+static __device__ __align__(256) uint8_t scratch[SPECTRA_NOALLOC_SCRATCH_BYTES];
+
+// Device address of `scratch` on the current device, looked up once per device (with that
+// device current) and kept; nullptr (and a message) when the lookup fails.
+static void* scratch_ptr() {
+  static std::mutex mu;
+  static std::vector<std::pair<int, void*>> known;  // (device, address)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    set_error("hipGetDevice failed");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  for (const auto& d : known)
+    if (d.first == dev) return d.second;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || ptr == nullptr) {
+    (void)hipGetLastError();
+    set_error(std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    return nullptr;
+  }
+  known.emplace_back(dev, ptr);
+  return ptr;
+}
+
+}  // namespace spectra
+
+extern "C" int spectra_w4a16_linear_noalloc(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m,
+                                            int32_t act_dtype, void* out, int64_t ldo, spectra_stream_t stream) {
+  int st = spectra::validate_qweight(w);
+  if (st != SPECTRA_OK) return st;
+  SPECTRA_REQUIRE(m >= 1, "m must be >= 1");
+  const size_t need = m >= 2 ? spectra_w4a16_gemm_workspace(w, m, act_dtype) : 0;
+  if (need > (size_t)SPECTRA_NOALLOC_SCRATCH_BYTES)
+    return spectra::fail(SPECTRA_ERR_WORKSPACE,
+                         "this call needs " + std::to_string(need) + " bytes of workspace, more than the " +
+                             std::to_string((size_t)SPECTRA_NOALLOC_SCRATCH_BYTES) +
+                             "-byte scratch of spectra_w4a16_linear_noalloc; use spectra_w4a16_linear with a workspace");
+  void* ws = spectra::scratch_ptr();
+  if (ws == nullptr) return SPECTRA_ERR_HIP;
+  return spectra_w4a16_linear(w, x, ldx, m, act_dtype, out, ldo, ws, (size_t)SPECTRA_NOALLOC_SCRATCH_BYTES, stream);
+}
+
 extern "C" int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m,
                                     int32_t act_dtype, void* out, int64_t ldo, void* workspace,
                                     size_t workspace_bytes, spectra_stream_t stream) {
