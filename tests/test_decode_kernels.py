@@ -244,7 +244,8 @@ def _check(y, ref):
     assert float((yv - ref).norm() / ref.norm()) <= 1e-3
 
 
-@pytest.mark.parametrize("n,k,had", [(640, 3072, 128), (16384, 3072, 128), (5000, 3072, 0), (512, 1024, 64)])
+@pytest.mark.parametrize("n,k,had", [(640, 3072, 128), (16384, 3072, 128), (5000, 3072, 0), (512, 1024, 64),
+                                     (128256, 3072, 128)])  # the decoder's tied lm_head
 def test_gemv_rmsnorm_prologue(hip, n, k, had):
     case(n=n, k=k, had=had)
     ops, w_eff = _nf4_ops(n, k, had, seed=n + k)

@@ -166,6 +166,51 @@ def test_decoder_against_fp32_reference(hip):
         assert int(dec.cur_pos) == prompt.numel() + step + 1
 
 
+def _greedy_consistent(ours: int, lr: torch.Tensor, tol: float) -> None:
+    """Our greedy token must be the reference's argmax, unless the reference's top two are
+    closer than the logit tolerance allows to resolve (then ours must be within it of the max)."""
+    top = torch.topk(lr.reshape(-1), 2).values
+    if float(top[0] - top[1]) > 2 * tol:
+        assert ours == int(torch.argmax(lr)), (ours, int(torch.argmax(lr)), float(top[0] - top[1]))
+    else:
+        assert float(lr.reshape(-1)[ours]) >= float(top[0]) - 2 * tol
+
+
+def test_decoder_llama32_3b_shape_against_fp32_reference(hip):
+    """BASELINE configs[4] at full size (engine.py:1801-1860, :1124-1168): 28 layers, hidden 3072,
+    24 / 8 heads, intermediate 8192, vocab 128256, random init (seed 0), every linear NF4 +
+    FWHT-128 + 0.5% CSR outliers, tied quantized embedding / lm_head (the fused-RMSNorm GEMV at
+    N=128256, K=3072); a 512-token prompt, then 8 graph-replayed greedy steps, against the fp32
+    restatement.  Greedy tokens equal (on a near-tie: within the logit tolerance of the
+    reference's maximum, the reference then following our token); logits within 2e-2 of the
+    logit scale.  The bar is 2e-2, not the single-layer 1e-2: every linear is held to 1e-3
+    relative L2 (fp16 rotated activations and fp16 outputs, as in any fp16 implementation), and
+    over 28 layers of a random-init residual stream those roundings compound -- measured
+    0.16-0.3% of the logit scale after one layer, 0.5% after four, 0.8-1.3% after 28."""
+    cfg = DecoderConfig(max_seq=640)
+    dec = SpectraDecoder(cfg)
+    ref = RefDecoder(dec)
+    prompt = torch.randint(0, cfg.vocab, (512,), generator=torch.Generator().manual_seed(5)).cuda()
+
+    def check(stage, lg, lr):
+        scale = lr.abs().max().item()
+        err = (lg - lr).abs().max().item()
+        print(f"{stage}: max |dlogit| {err:.4e}, logit scale {scale:.4e} ({err / scale:.2e})", flush=True)
+        assert err <= 2e-2 * scale
+        _greedy_consistent(int(dec.cur_id), lr, 2e-2 * scale)
+
+    case(stage="prefill", T=prompt.numel(), layers=cfg.layers, vocab=cfg.vocab)
+    check("prefill", dec.prefill(prompt).float(), ref.forward(prompt, 0))
+    dec.capture_decode()
+    for step in range(8):
+        case(stage="decode", step=step)
+        tok = int(dec.cur_id)
+        dec.graph.replay()
+        check(f"step {step}", dec.graph_logits.float(),
+              ref.forward(torch.tensor([tok], device="cuda"), prompt.numel() + step))
+        assert int(dec.cur_pos) == prompt.numel() + step + 1
+
+
 def test_decoder_graph_matches_eager(hip):
     """The captured decode step replays the eager computation bit for bit."""
     prompt = torch.randint(0, SMALL.vocab, (5,), generator=torch.Generator().manual_seed(2)).cuda()

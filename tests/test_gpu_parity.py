@@ -454,6 +454,7 @@ def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
 
 @pytest.mark.parametrize("m,k,n", [
     (512, 4096, 14336),   # 256-wide tiles, K split in two
+    (2048, 4096, 14336),  # cfg4's first GEMM at full size: 448 tiles of 256 x 256, no K split
     (2048, 14336, 4096),  # cfg4's second GEMM at full size: 256-wide tiles, K split in two
     (512, 8192, 3072),    # 128-wide tiles, K split in four
 ])
