@@ -70,7 +70,7 @@ typedef struct spectra_qweight {
   int64_t n, k;
   int32_t format;         /* spectra_format_t */
   int32_t group_size;     /* 32 (Format A) or the NF4 block size (64) */
-  int32_t hadamard_block; /* 0, or a power of two in [8, 512] dividing k */
+  int32_t hadamard_block; /* 0, or a power of two in [2, 1024] dividing k (GEMV: <= 512) */
   int32_t marlin_layout;  /* 1: byte j of a 32-run = q[j] | q[j+16]<<4; 0: q[2j] | q[2j+1]<<4 */
   const uint8_t* packed;  int64_t packed_stride;  /* uint8 [N, K/2] */
   const uint16_t* scales; int64_t scales_stride;  /* fp16 [N, K/group] (absmax for NF4) */

@@ -106,6 +106,8 @@ class SpectraError(RuntimeError):
 def load(path: str = LIB_PATH) -> ctypes.CDLL:
     """Load the library once; raise (never fall back) when it is unavailable."""
     global _lib
+    if _lib is not None:  # loaded: no lock on the per-call path
+        return _lib
     with _lock:
         if _lib is not None:
             return _lib

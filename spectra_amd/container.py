@@ -34,6 +34,8 @@ from typing import Any, Dict, Iterator, Optional, Tuple, Union
 import numpy as np
 import torch
 
+from .kernels import validate_outliers
+
 __all__ = ["MAGIC", "FORMAT_A", "nf4_type", "TrdcWriter", "TrdcReader", "FormatAWeight", "norm_vector_for",
            "prescan_norm_vectors", "stream_checkpoint", "compress_checkpoint", "nf4_concat", "select_csr_outliers"]
 
@@ -260,17 +262,20 @@ class TrdcReader:
                 wdt = _DTYPES.get(meta.get("outlier_w_dtype", "float16"), torch.float16)
                 idx = mv(idx)
                 ow = mv(self._tensor(w_b, wdt, (n, -1)))
+                validate_outliers(n, k, idx=idx, ow=ow)
             return FormatAWeight(packed, scales, zeros, idx, ow, k, bool(meta.get("marlin_layout", False)))
         if ttype.startswith("nf4_"):
             from .compressor import NF4Weight
             n, k = meta["shape"]
             blk = meta["block"]
             p_b, a_b, r_b, c_b, v_b = self._parts(meta, ["packed_len", "absmax_len", "rowptr_len", "col_len", "val_len"])
+            rowptr = mv(self._tensor(r_b, torch.int32, (n + 1,)))
+            col = mv(self._tensor(c_b, torch.int32, (-1,)))
+            val = mv(self._tensor(v_b, torch.float16, (-1,)))
+            validate_outliers(n, k, rowptr=rowptr, col=col, val=val)
             return NF4Weight(mv(self._tensor(p_b, torch.uint8, (n, k // 2))),
                              mv(self._tensor(a_b, torch.float16, (n, k // blk))),
-                             mv(self._tensor(r_b, torch.int32, (n + 1,))),
-                             mv(self._tensor(c_b, torch.int32, (-1,))),
-                             mv(self._tensor(v_b, torch.float16, (-1,))),
+                             rowptr, col, val,
                              k, blk, int(meta["hadamard_block"]), bool(meta.get("marlin_layout", True)))
         if "lossless" in ttype:
             (raw,) = self._parts(meta, ["total_len"])

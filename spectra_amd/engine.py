@@ -22,17 +22,26 @@ from .kernels import (GEMV_MAX_M, QWeightOperands, attend_decode, attend_decode_
 __all__ = ["SpectraFusedLinear", "SpectraFusedEmbedding", "DecoderConfig", "SpectraDecoder"]
 
 
+def _block(group_size: Optional[int], codebook: str) -> int:
+    """The quantization block: as given, else the codebook's own (32 for Format A, 64 for NF4)."""
+    if group_size is not None:
+        return int(group_size)
+    return 32 if codebook == "asym" else 64
+
+
 class SpectraFusedLinear(nn.Module):
     """Drop-in quantized linear: packed 4-bit weights, scales, zeros and outliers
     (engine.py:35-88); rows <= GEMV_MAX_M go to the GEMV family, larger batches to
     the MFMA GEMM (engine.py:94-124)."""
 
-    def __init__(self, in_features: int, out_features: int, group_size: int = 32, has_bias: bool = False,
-                 enable_hdsq: bool = True, marlin_layout: bool = False, *, codebook: str = "asym",
-                 hadamard_block: int = 0):
+    def __init__(self, in_features: int, out_features: int, group_size: Optional[int] = None,
+                 has_bias: bool = False, enable_hdsq: bool = True, marlin_layout: bool = False, *,
+                 codebook: str = "asym", hadamard_block: int = 0):
         super().__init__()
         self.in_features = in_features
         self.out_features = out_features
+        # None: the codebook's own block (32 for Format A as engine.py:42, 64 for NF4); an
+        # explicit value is used as given
         self.group_size = group_size
         self.enable_hdsq = enable_hdsq
         self.marlin_layout = marlin_layout
@@ -77,10 +86,10 @@ class SpectraFusedLinear(nn.Module):
     def _operands(self) -> QWeightOperands:
         if self._ops is None:
             use_o = self.enable_hdsq and self.outlier_idx is not None and self.outlier_weight is not None
-            gs = self.group_size if self.codebook == "asym" else (self.group_size if self.group_size != 32 else 64)
             self._ops = QWeightOperands(
                 self.packed_weight, self.scales, self.zeros, self.in_features, codebook=self.codebook,
-                group_size=gs, hadamard_block=self.hadamard_block, marlin_layout=self.marlin_layout,
+                group_size=_block(self.group_size, self.codebook), hadamard_block=self.hadamard_block,
+                marlin_layout=self.marlin_layout,
                 outlier_idx=self.outlier_idx if use_o else None, outlier_w=self.outlier_weight if use_o else None,
                 outlier_rowptr=self.outlier_rowptr if use_o else None, bias=self.bias)
         return self._ops
@@ -89,6 +98,9 @@ class SpectraFusedLinear(nn.Module):
         self._ops = None
         return super()._apply(fn, *args, **kwargs)
 
+    # outside any torch.compile trace, as the reference marks it (engine.py:90): the library
+    # call is opaque to the compiler
+    @torch.compiler.disable
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         total_tokens = x.numel() // self.in_features
         if total_tokens == 0:
@@ -112,8 +124,8 @@ class SpectraFusedEmbedding(nn.Module):
     through keyword-only arguments.  Zero points may be given packed (two per byte,
     engine.py:177-183) or unpacked."""
 
-    def __init__(self, num_embeddings: int, embedding_dim: int, group_size: int = 32, marlin_layout: bool = False,
-                 *, codebook: str = "asym"):
+    def __init__(self, num_embeddings: int, embedding_dim: int, group_size: Optional[int] = None,
+                 marlin_layout: bool = False, *, codebook: str = "asym"):
         super().__init__()
         self.num_embeddings = num_embeddings
         self.embedding_dim = embedding_dim
@@ -143,7 +155,7 @@ class SpectraFusedEmbedding(nn.Module):
     def operands(self) -> QWeightOperands:
         if self._ops is None:
             zeros = self.zeros
-            gs = self.group_size if self.codebook == "asym" else (self.group_size if self.group_size != 32 else 64)
+            gs = _block(self.group_size, self.codebook)
             if self.codebook == "asym" and zeros is not None and zeros.shape[1] < self.scales.shape[1]:
                 from .compressor import unpack_zeros  # engine.py:177-183: two zero points per byte
                 zeros = unpack_zeros(zeros, self.embedding_dim)

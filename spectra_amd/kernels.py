@@ -18,6 +18,8 @@ computes on the host and there is no fallback path.
 from __future__ import annotations
 
 import ctypes
+import weakref
+from collections import OrderedDict
 from typing import List, Optional, Tuple
 
 import torch
@@ -27,7 +29,7 @@ from . import _lib as L
 __all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_dequant", "fwht_rows",
            "QWeightOperands", "GEMV_MAX_M", "w4_embedding", "rmsnorm", "rope_append", "attend_decode",
            "attend_workspace_bytes", "silu_mul", "greedy_next", "w4a16_gemv_fused", "kv4_quantize",
-           "kv4_dequantize", "attend_decode_q4"]
+           "kv4_dequantize", "attend_decode_q4", "validate_outliers"]
 
 GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
 
@@ -59,6 +61,35 @@ def _rows(t: torch.Tensor, name: str, align: int = 1) -> Tuple[torch.Tensor, int
     return t, t.stride(0)
 
 
+def validate_outliers(n: int, k: int, *, rowptr: Optional[torch.Tensor] = None, col: Optional[torch.Tensor] = None,
+                      val: Optional[torch.Tensor] = None, idx: Optional[torch.Tensor] = None,
+                      ow: Optional[torch.Tensor] = None) -> None:
+    """Raise ValueError unless the outlier side tensors index inside W[N, K]: CSR ``rowptr``
+    [N+1] starting at 0, never decreasing and ending at nnz, ``col`` in [0, K) and ``val`` of
+    nnz entries; dense ``idx`` in [0, K) with ``ow`` [N, n_out].  The kernels use these
+    values as addresses, so a corrupt side tensor would read out of bounds.  Works on any
+    device; one host read of the result."""
+    if rowptr is not None:
+        nnz = 0 if col is None else col.numel()
+        if rowptr.dim() != 1 or rowptr.numel() != n + 1:
+            raise ValueError(f"CSR rowptr must have N+1={n + 1} entries, got {tuple(rowptr.shape)}")
+        if val is None or val.numel() != nnz:
+            raise ValueError(f"CSR col and val must both have nnz entries ({nnz} vs {None if val is None else val.numel()})")
+        rp = rowptr.to(torch.int64)
+        ok = (rp[0] == 0) & (rp[-1] == nnz) & torch.all(rp[1:] >= rp[:-1])
+        if nnz:
+            c = col.to(torch.int64)
+            ok = ok & torch.all((c >= 0) & (c < k))
+        if not bool(ok):
+            raise ValueError("corrupt CSR outliers: rowptr must start at 0, never decrease and end at nnz, "
+                             f"and every column must lie in [0, K={k})")
+    if idx is not None:
+        if ow is not None and (ow.dim() != 2 or ow.shape[0] != n or ow.shape[1] != idx.numel()):
+            raise ValueError(f"outlier_w must be [N, n_out] = [{n}, {idx.numel()}], got {tuple(ow.shape)}")
+        if idx.numel() and not bool(torch.all((idx >= 0) & (idx < k))):
+            raise ValueError(f"outlier column indices must lie in [0, K={k})")
+
+
 class QWeightOperands:
     """Validated device operands of one quantized weight + its C descriptor.
 
@@ -70,7 +101,11 @@ class QWeightOperands:
                  codebook: str = "asym", group_size: Optional[int] = None, hadamard_block: int = 0,
                  marlin_layout: bool = False, outlier_idx: Optional[torch.Tensor] = None,
                  outlier_w: Optional[torch.Tensor] = None, outlier_rowptr: Optional[torch.Tensor] = None,
-                 bias: Optional[torch.Tensor] = None, packed_align: int = 16):
+                 bias: Optional[torch.Tensor] = None, packed_align: int = 16, hold_inputs: bool = True):
+        # hold_inputs=False: keep only the tensors made here (conversions, copies); the caller's
+        # own tensors must then outlive every use of the descriptor (the functional API's
+        # cache drops an entry as soon as one of them is freed)
+        inputs = {id(t) for t in (packed, scales, zeros, outlier_idx, outlier_w, outlier_rowptr, bias) if t is not None}
         if not packed.is_cuda:
             raise ValueError("packed weights must be on the GPU")
         dev = packed.device
@@ -88,6 +123,9 @@ class QWeightOperands:
         keep: List[torch.Tensor] = []
         packed, ldp = _rows(packed, "packed_w", packed_align)
         keep.append(packed)
+        for t, what in ((scales, "scales"), (zeros, "zeros"), (bias, "bias")):
+            if t is not None and t.device != dev:
+                raise ValueError(f"{what} is on {t.device}, the packed weights on {dev}")
         if scales.dtype != torch.float16:
             raise ValueError(f"scales must be float16, got {scales.dtype}")
         if scales.shape[0] != n or scales.shape[1] < k // gs:
@@ -118,14 +156,14 @@ class QWeightOperands:
             val = outlier_w.to(device=dev).contiguous()
             if rp.numel() != n + 1 or col.numel() != val.numel():
                 raise ValueError("CSR shapes: rowptr [N+1], col and val [nnz]")
+            validate_outliers(n, k, rowptr=rp, col=col, val=val)
             keep += [rp, col, val]
             w.outlier_kind = L.OUTLIERS_CSR
             w.csr_rowptr, w.csr_col, w.csr_val, w.csr_nnz = rp.data_ptr(), col.data_ptr(), val.data_ptr(), col.numel()
         elif outlier_idx is not None and outlier_w is not None:
             idx = outlier_idx.to(device=dev, dtype=torch.int64).contiguous()
-            ow = outlier_w
-            if ow.dim() != 2 or ow.shape[0] != n or ow.shape[1] != idx.numel():
-                raise ValueError(f"outlier_w must be [N, n_out], got {tuple(ow.shape)}")
+            ow = outlier_w.to(device=dev)
+            validate_outliers(n, k, idx=idx, ow=ow)
             odt = _dtype_code(ow, (torch.float16, torch.bfloat16), "outlier_w")
             ow, ldow = _rows(ow, "outlier_w")
             keep += [idx, ow]
@@ -139,11 +177,51 @@ class QWeightOperands:
             w.bias, w.bias_dtype = b.data_ptr(), _dtype_code(b, _DT.keys(), "bias")
             keep.append(b)
         self.desc = w
-        self.keep = keep
+        self.keep = keep if hold_inputs else [t for t in keep if id(t) not in inputs]
         self.n, self.k, self.device = n, k, dev
 
     def ptr(self):
         return ctypes.byref(self.desc)
+
+
+class _OperandCache:
+    """Descriptors of the functional API, keyed by the identity, address, shape, strides, dtype
+    and version (in-place writes bump it) of every operand tensor: a weight passed again is
+    neither rebuilt nor re-validated.  An entry holds no reference to the caller's tensors and
+    is dropped when any of them is freed (weak references); at most ``cap`` entries (LRU)."""
+
+    def __init__(self, cap: int = 256):
+        self.cap = cap
+        self.d: "OrderedDict" = OrderedDict()
+
+    def get(self, tensors, scalars, build) -> QWeightOperands:
+        key = (scalars, tuple(None if t is None else (id(t), t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.dtype,
+                                                       t.device, t._version) for t in tensors))
+        hit = self.d.get(key)
+        if hit is not None and all((r is None) == (t is None) and (r is None or r() is t)
+                                   for r, t in zip(hit[0], tensors)):
+            self.d.move_to_end(key)
+            return hit[1]
+        ops = build()
+        d = self.d
+        refs = tuple(None if t is None else weakref.ref(t, lambda _r, k=key: d.pop(k, None)) for t in tensors)
+        d[key] = (refs, ops)
+        while len(d) > self.cap:
+            d.popitem(last=False)
+        return ops
+
+
+_OPS = _OperandCache()
+
+
+def _cached_operands(packed, scales, zeros, k, *, codebook, group_size, hadamard_block, marlin_layout, outlier_idx,
+                     outlier_w, outlier_rowptr, bias=None, packed_align=16) -> QWeightOperands:
+    tensors = (packed, scales, zeros, outlier_idx, outlier_w, outlier_rowptr, bias)
+    scalars = (k, codebook, group_size, hadamard_block, bool(marlin_layout), packed_align)
+    return _OPS.get(tensors, scalars, lambda: QWeightOperands(
+        packed, scales, zeros, k, codebook=codebook, group_size=group_size, hadamard_block=hadamard_block,
+        marlin_layout=marlin_layout, outlier_idx=outlier_idx, outlier_w=outlier_w, outlier_rowptr=outlier_rowptr,
+        bias=bias, packed_align=packed_align, hold_inputs=False))
 
 
 def _run_linear(ops: QWeightOperands, x2: torch.Tensor, out2: torch.Tensor, family: str) -> None:
@@ -199,9 +277,9 @@ def fused_w4a16_gemv_hdsq(x: torch.Tensor, packed_w: torch.Tensor, scales: torch
     if x.dim() != 2:
         raise ValueError(f"x must be [K] or [B, K], got {tuple(x.shape)}")
     B, K = x.shape
-    ops = QWeightOperands(packed_w, scales, zeros, K, codebook=codebook, group_size=group_size,
-                          hadamard_block=hadamard_block, marlin_layout=marlin_layout, outlier_idx=outlier_idx,
-                          outlier_w=outlier_w, outlier_rowptr=outlier_rowptr, bias=bias)
+    ops = _cached_operands(packed_w, scales, zeros, K, codebook=codebook, group_size=group_size,
+                           hadamard_block=hadamard_block, marlin_layout=marlin_layout, outlier_idx=outlier_idx,
+                           outlier_w=outlier_w, outlier_rowptr=outlier_rowptr, bias=bias)
     x2, in_dtype = _activations(x, K)
     N = ops.n
     if out is None:
@@ -224,9 +302,9 @@ def batched_w4a16_gemm(a: torch.Tensor, packed_b: torch.Tensor, scales: torch.Te
     """Batched / prefill GEMM (kernels.py:333-389): ``c = a . W_eff^T`` over all leading dims,
     returned in ``a.dtype`` with shape ``a.shape[:-1] + (N,)``."""
     K = a.shape[-1]
-    ops = QWeightOperands(packed_b, scales, zeros, K, codebook=codebook, group_size=group_size,
-                          hadamard_block=hadamard_block, marlin_layout=marlin_layout, outlier_idx=outlier_idx,
-                          outlier_w=outlier_w, outlier_rowptr=outlier_rowptr, bias=bias)
+    ops = _cached_operands(packed_b, scales, zeros, K, codebook=codebook, group_size=group_size,
+                           hadamard_block=hadamard_block, marlin_layout=marlin_layout, outlier_idx=outlier_idx,
+                           outlier_w=outlier_w, outlier_rowptr=outlier_rowptr, bias=bias)
     x2, in_dtype = _activations(a, K)
     c = torch.empty((x2.shape[0], ops.n), device=a.device, dtype=x2.dtype)
     _run_linear(ops, x2, c, "gemm")
@@ -248,9 +326,9 @@ def w4_dequant(packed: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch
                outlier_w: Optional[torch.Tensor] = None, outlier_rowptr: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Materialise W_eff [N, K] bit-exactly (tests/test_kernels.py:31-39, engine.py:185-210)."""
     k = k if k is not None else packed.shape[1] * 2
-    ops = QWeightOperands(packed, scales, zeros, k, codebook=codebook, group_size=group_size,
-                          marlin_layout=marlin_layout, outlier_idx=outlier_idx, outlier_w=outlier_w,
-                          outlier_rowptr=outlier_rowptr, packed_align=1)
+    ops = _cached_operands(packed, scales, zeros, k, codebook=codebook, group_size=group_size, hadamard_block=0,
+                           marlin_layout=marlin_layout, outlier_idx=outlier_idx, outlier_w=outlier_w,
+                           outlier_rowptr=outlier_rowptr, packed_align=1)
     out = torch.empty((ops.n, k), device=packed.device, dtype=out_dtype)
     lib = L.load()
     L.check("spectra_w4_dequant", lib.spectra_w4_dequant(ops.ptr(), out.data_ptr(), out.stride(0),

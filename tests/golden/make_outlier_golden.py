@@ -16,6 +16,8 @@ import importlib.util
 import os
 import sys
 
+sys.dont_write_bytecode = True  # loading the reference by path must leave no __pycache__ in its tree
+
 import numpy as np
 import torch
 

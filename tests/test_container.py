@@ -105,6 +105,57 @@ def test_corrupt_containers_raise(tmp_path):
             T.TrdcReader(p)
 
 
+def _small_nf4(n=4, k=128, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    rp = torch.tensor([0, 2, 2, 5, 6], dtype=torch.int32)[: n + 1]
+    nnz = int(rp[-1])
+    return NF4Weight(torch.randint(0, 256, (n, k // 2), generator=g, dtype=torch.uint8),
+                     torch.rand(n, k // 64, generator=g).half(), rp,
+                     torch.tensor([3, 70, 0, 64, 127, 9], dtype=torch.int32)[:nnz],
+                     torch.randn(nnz, generator=g).half(), k, 64, 128, True)
+
+
+def test_corrupt_outlier_side_tensors_raise_at_load(tmp_path):
+    """Side tensors the kernels use as addresses are checked when a tensor is loaded, before any
+    launch: CSR rowptr must start at 0, never decrease and end at nnz, columns lie in [0, K);
+    Format A outlier columns lie in [0, K)."""
+    head = {"version": "TRDC4B01", "group_size": 32, "base_outlier_ratio": 0.01, "architecture": "LlamaForCausalLM",
+            "config": {}}
+    good = _small_nf4()
+    bad = {
+        "rowptr_decreasing": dict(rowptr=torch.tensor([0, 2, 1, 5, 6], dtype=torch.int32)),
+        "rowptr_past_nnz": dict(rowptr=torch.tensor([0, 2, 2, 5, 7], dtype=torch.int32)),
+        "rowptr_not_zero": dict(rowptr=torch.tensor([1, 2, 2, 5, 6], dtype=torch.int32)),
+        "col_past_k": dict(col=torch.tensor([3, 70, 0, 128, 127, 9], dtype=torch.int32)),
+        "col_negative": dict(col=torch.tensor([3, -1, 0, 64, 127, 9], dtype=torch.int32)),
+    }
+    p = tmp_path / "good.trdc"
+    with T.TrdcWriter(p, head) as wr:
+        wr.add_nf4("w", good)
+    with T.TrdcReader(p) as rd:
+        q = rd.load("w")
+        assert torch.equal(q.rowptr, good.rowptr) and torch.equal(q.col, good.col)
+    for name, repl in bad.items():
+        f = {k: getattr(good, k) for k in ("packed", "absmax", "rowptr", "col", "val")} | repl
+        q = NF4Weight(f["packed"], f["absmax"], f["rowptr"], f["col"], f["val"], good.k, 64, 128, True)
+        p = tmp_path / f"{name}.trdc"
+        with T.TrdcWriter(p, head) as wr:
+            wr.add_nf4("w", q)
+        with T.TrdcReader(p) as rd, pytest.raises(ValueError):
+            rd.load("w")
+    # Format A: an outlier column index past K
+    n, k = 4, 64
+    w = torch.randn(n, k, generator=torch.Generator().manual_seed(1)).half()
+    idx = np.array([5, 64], dtype=np.int32)
+    packed, scales, pz = O.compute_group32_quant(_np16(w), np.array([5, 63]))
+    p = tmp_path / "fa.trdc"
+    with T.TrdcWriter(p, head) as wr:
+        wr.add_format_a("w", [n, k], torch.from_numpy(packed), torch.from_numpy(scales), torch.from_numpy(pz),
+                        torch.from_numpy(idx), w[:, [5, 63]], 0.01, 3.0)
+    with T.TrdcReader(p) as rd, pytest.raises(ValueError):
+        rd.load("w")
+
+
 def test_nf4_concat_rowptr_offsets():
     def q(n, nnz_rows, seed):
         g = torch.Generator().manual_seed(seed)

@@ -24,7 +24,7 @@ import torch
 import oracle as O
 from spectra_amd import compressor as C
 from spectra_amd import kernels as K
-from spectra_amd.engine import SpectraFusedLinear
+from spectra_amd.engine import SpectraFusedEmbedding, SpectraFusedLinear
 
 pytestmark = pytest.mark.gpu
 
@@ -331,6 +331,34 @@ def test_format_b_small_batch(hip, act, m, n, k, had, marlin):
         check_y(lin(cuda(x, TDT[act])), y_ref, TDT[act])
 
 
+@pytest.mark.parametrize("m", [1, 3, 5, 16])
+def test_nf4_block32_module_and_embedding(hip, m):
+    """NF4 with 32-element blocks (absmax [N, K/32]) through the modules built with group_size=32:
+    the GPU quantizer bit-exact against the oracle, the linear (one row: the GEMV; more: the
+    small-batch / GEMM families) against the oracle's product, the embedding rows bit-exact."""
+    case(m=m, block=32)
+    n, k, had = 384, 3072, 128
+    rng = np.random.default_rng(320 + m)
+    w = rand_np(rng, (n, k), 0.02)
+    mask = rng.random((n, k)) < 0.005
+    w[mask] = (rng.standard_normal(mask.sum()) * 0.2).astype(np.float16)
+    ref = O.nf4_quantize(w, "float16", 32, 0, mask, True)
+    q = C.quantize_nf4(cuda(w), 32, 0, cuda(mask), True)
+    assert q.absmax.shape == (n, k // 32)
+    assert np.array_equal(host(q.packed), ref["packed"]) and np.array_equal(host(q.absmax), ref["absmax"])
+    w_eff = O.nf4_dequant(ref["packed"], ref["absmax"], True, "float16", ref["rowptr"], ref["col"], ref["val"],
+                          blocksize=32)
+    lin = SpectraFusedLinear(k, n, 32, codebook="nf4", hadamard_block=had, marlin_layout=True).cuda()
+    lin.set_weights(q.packed, q.absmax, None, outlier_idx=q.col, outlier_weight=q.val, marlin_layout=True,
+                    outlier_rowptr=q.rowptr)
+    x = rand_np(rng, (m, k), 1.0)
+    check_y(lin(cuda(x)), O.linear_ref(x, "float16", w_eff, "float16", hadamard_block=had), torch.float16)
+    emb = SpectraFusedEmbedding(n, k, 32, True, codebook="nf4").cuda()
+    emb.set_weights(q.packed, q.absmax, None, q.col, q.val, True, outlier_rowptr=q.rowptr)
+    ids = torch.tensor([0, n - 1, 17, 200], device="cuda")
+    assert np.array_equal(host(emb(ids)), w_eff[ids.cpu().numpy()])
+
+
 @pytest.mark.parametrize("nnz", [1, 3, 5])
 def test_tiny_csr(hip, nnz):
     """CSR arrays shorter than one 4-entry load group (read per entry, never as a group)."""
@@ -553,6 +581,33 @@ def test_determinism_and_graph_replay(hip):
         assert torch.equal(g1, e1) and torch.equal(g8, e8)
         _ = lin(x1)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_functional_api_reuses_and_validates_descriptors(hip):
+    """fused_w4a16_gemv_hdsq builds (and validates) a weight's descriptor once: a second call
+    with the same tensors reuses it, an in-place write to an operand rebuilds and re-validates
+    it (a column past K raises before any launch), and freeing the operands drops the entry."""
+    import gc
+    q, rng = _format_b(77, 64, 1024, 128)
+    t = {k: cuda(q[k]) for k in ("packed", "absmax", "rowptr", "col", "val")}
+    x = cuda(rand_np(rng, (1, 1024), 1.0))
+
+    def call():
+        return K.fused_w4a16_gemv_hdsq(x, t["packed"], t["absmax"], None, outlier_idx=t["col"], outlier_w=t["val"],
+                                       marlin_layout=True, codebook="nf4", hadamard_block=128,
+                                       outlier_rowptr=t["rowptr"])
+    gc.collect()
+    n0 = len(K._OPS.d)
+    y1 = call()
+    assert len(K._OPS.d) == n0 + 1
+    y2 = call()
+    assert len(K._OPS.d) == n0 + 1 and torch.equal(y1, y2)
+    t["col"][0] = 1024  # past K: the next call re-validates and refuses
+    with pytest.raises(ValueError):
+        call()
+    del t, y1, y2
+    gc.collect()
+    assert len(K._OPS.d) == n0
 
 
 def test_module_edge_cases(hip):
