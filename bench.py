@@ -156,32 +156,122 @@ def pool_copies(bytes_per_copy: int, pool_bytes: float) -> int:
 
 
 # ---------------------------------------------------------------------------
-# CPU baseline: the oracle (numpy restatement of the reference dequant + matmul)
+# CPU baseline: the oracle's torch restatement of the reference path, on the host cores
 # ---------------------------------------------------------------------------
-def cpu_baseline(qs, xs, budget_s: float = 15.0):
-    import oracle as O
-    from threadpoolctl import threadpool_limits
+def _host_threads() -> int:
+    """The host cores this process may use: the box's per-GPU share (OMP_NUM_THREADS, set by
+    the box) when given, else every core."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(env))) if env and env.isdigit() else n
 
-    hq = [(q.packed.cpu().numpy(), q.absmax.cpu().numpy(), q.rowptr.cpu().numpy(), q.col.cpu().numpy(),
-           q.val.cpu().numpy()) for q in qs]
-    hx = [x.cpu().numpy() for x in xs]
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _median_time(fn, min_runs: int, budget_s: float) -> float:
+    fn()  # warm-up
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < min_runs or (time.perf_counter() < t_end and len(ts) < 1000):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baseline(qs, xs, budget_s: float = 8.0) -> dict:
+    """cfg2 step (QKV + down_proj GEMV) on the host with torch: variant A is the per-call
+    reference path (NF4 dequant -> W_eff, FWHT-128 of x, float32 product; tests/test_kernels.py:31-46,
+    engine.py:186-210), variant B the float32 product alone on pre-dequantized W_eff; medians
+    of at least 20 runs."""
+    from oracle import torch_ref as TR
+    threads = _host_threads()
+    torch.set_num_threads(threads)
+    ops = [tuple(t.cpu() for t in (q.packed, q.absmax, q.rowptr, q.col, q.val)) for q in qs]
+    hx = [x.cpu() for x in xs]
     step_bytes = sum(gemv_bytes(q) for q in qs)
-    reps, t_total = 0, 0.0
-    with threadpool_limits(limits=1):
-        while t_total < budget_s and reps < 50:
-            t0 = time.perf_counter()
-            for (p, a, rp, c, v), x in zip(hq, hx):
-                w_eff = O.nf4_dequant(p, a, True, "float16", rp, c, v)          # per-call dequant
-                x_rot = O.rotate_blocks(x.astype(np.float32), HAD)              # FWHT-128
-                y = (x_rot @ w_eff.astype(np.float32).T).astype(np.float16)     # fp32 matmul -> fp16
-            t_total += time.perf_counter() - t0
-            reps += 1
-            del y
-    per_step = t_total / reps
-    return {"value": round(step_bytes / per_step / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} cfg2 steps (QKV + down_proj GEMV, per-call NF4 dequant + FWHT-128 + fp32 matmul), "
-                      f"{per_step * 1e3:.1f} ms/step, numpy single thread on {platform.processor() or 'host'} "
-                      f"({os.cpu_count()} logical CPUs visible)"}
+
+    def step_a():
+        for o, x in zip(ops, hx):
+            TR.linear_a(x, *o, hadamard_block=HAD)
+
+    w_eff = [TR.nf4_dequant(*o) for o in ops]
+
+    def step_b():
+        for w, x in zip(w_eff, hx):
+            TR.linear_b(x, w, hadamard_block=HAD)
+
+    ta = _median_time(step_a, 20, budget_s)
+    tb = _median_time(step_b, 20, budget_s / 2)
+    return {"value": round(step_bytes / ta / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"cfg2 steps (QKV + down_proj GEMV, M=1) with oracle/torch_ref.py: variant A (per-call NF4 "
+                      f"dequant + FWHT-128 + fp32 matmul) {ta * 1e3:.2f} ms/step (median); variant B (fp32 matmul "
+                      f"on pre-dequantized W_eff) {tb * 1e3:.3f} ms/step",
+            "variant_b_value": round(step_bytes / tb / 1e9, 2), "cpu_model": _cpu_model(),
+            "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+
+
+def cpu_gemm_baseline(qs, a, budget_s: float = 10.0) -> dict:
+    """cfg4's first prefill GEMM (M=2048, K=4096, N=14336) on the host: variant A (dequant +
+    FWHT-128 of A + fp32 product) and variant B (fp32 product on pre-dequantized W_eff),
+    medians of at least 20 runs, in TFLOP/s of the 2*M*K*N product."""
+    from oracle import torch_ref as TR
+    torch.set_num_threads(_host_threads())
+    q = qs
+    o = tuple(t.cpu() for t in (q.packed, q.absmax, q.rowptr, q.col, q.val))
+    ha = a.cpu()
+    flops = 2 * ha.shape[0] * q.k * q.n
+    ta = _median_time(lambda: TR.linear_a(ha, *o, hadamard_block=q.hadamard_block), 20, budget_s)
+    w = TR.nf4_dequant(*o)
+    tb = _median_time(lambda: TR.linear_b(ha, w, hadamard_block=q.hadamard_block), 20, budget_s / 2)
+    return {"cfg4_cpu_gemm_variant_a_TFLOPs": round(flops / ta / 1e12, 4),
+            "cfg4_cpu_gemm_variant_b_TFLOPs": round(flops / tb / 1e12, 4),
+            "cfg4_cpu_note": f"M=2048 K={q.k} N={q.n}, bf16 activations, medians: variant A {ta * 1e3:.0f} ms, "
+                             f"variant B {tb * 1e3:.0f} ms"}
+
+
+def cpu_decode_baseline(dev, prompt_len: int = 16, tokens: int = 4) -> dict:
+    """cfg5 variant B on the host: the same random-init 28-layer decoder (seed 0), every
+    weight dequantized once to float32 W_eff, then the oracle's float32 decoder
+    (oracle/torch_ref.py) prefills ``prompt_len`` tokens and generates ``tokens`` greedy
+    tokens; tok/s over the generated tokens."""
+    from oracle import torch_ref as TR
+    from spectra_amd.engine import DecoderConfig, SpectraDecoder
+    torch.set_num_threads(_host_threads())
+    dec = SpectraDecoder(DecoderConfig(max_seq=768))
+    c = dec.cfg
+
+    def w(q):  # dequantized on the GPU with the oracle's restatement, kept on the host
+        col, val = q.outliers()
+        return TR.nf4_dequant(q.packed, q.absmax, q.rowptr if col is not None else None, col, val,
+                              marlin=q.marlin_layout, blocksize=q.blocksize).cpu()
+    layers = [[w(q) for q in layer] for layer in dec.layers_q]
+    had = [[q.hadamard_block for q in layer] for layer in dec.layers_q]
+    emb, head = w(dec.embed_q), w(dec.lm_q)
+    norms = [t.float().cpu() for t in dec.norm_w]
+    del dec
+    torch.cuda.empty_cache()
+    ref = TR.Decoder(layers, had, norms, emb, head, heads=c.heads, kv_heads=c.kv_heads, rope_theta=c.rope_theta,
+                     rms_eps=c.rms_eps, max_seq=c.max_seq)
+    prompt = torch.randint(0, c.vocab, (prompt_len,), generator=torch.Generator().manual_seed(5))
+    with torch.no_grad():
+        tok = int(torch.argmax(ref.forward(prompt, 0)))
+        t0 = time.perf_counter()
+        for i in range(tokens):
+            tok = int(torch.argmax(ref.forward(torch.tensor([tok]), prompt_len + i)))
+        dt = time.perf_counter() - t0
+    return {"cfg5_cpu_decode_tok_s": round(tokens / dt, 3), "cfg5_cpu_decode_ms_per_token": round(dt * 1e3 / tokens, 1),
+            "cfg5_cpu_note": f"variant B on {torch.get_num_threads()} host threads ({_cpu_model()}): float32 W_eff "
+                             f"(13 GB), {prompt_len}-token prompt, {tokens} greedy tokens timed"}
 
 
 # ---------------------------------------------------------------------------
@@ -280,11 +370,7 @@ def main():
     assert torch.equal(ref, y_down), "graph replay output differs from an eager launch"
 
     achieved = b_down / t_down / 1e9
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "traffic_gemv_cfg2_down.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic, traffic_note = measured_traffic()
     result = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warm,
         "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -293,9 +379,10 @@ def main():
                                "+ fp16 absmax + FWHT-128 activations + 0.5% fp16 CSR outliers",
                    "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)",
                    "bytes_per_step": step_bytes, "weight_pool_copies": P, "timing": "one HIP graph of all steps"},
-        "roofline": {"bound": "hbm", "kernel": "gemv_kernel (down_proj K=8192 N=3072)", "achieved": round(achieved, 2),
-                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                     "traffic": traffic, "algorithmic_bytes_per_launch": b_down,
+        "roofline": {"bound": "hbm", "kernel": "gemv_stream_kernel (down_proj K=8192 N=3072)",
+                     "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_note, "algorithmic_bytes_per_launch": b_down,
                      "avg_launch_us": round(t_down * 1e6, 3)},
     }
     detail = {"qkv_gemv_us": round(t_qkv * 1e6, 3), "qkv_gemv_GBps": round(b_qkv / t_qkv / 1e9, 1),
@@ -304,14 +391,47 @@ def main():
         detail.update(secondary(lib, dev, args.pool_gb))
     result["detail"] = detail
     if not args.no_cpu_baseline:
-        log("bench: timing the CPU oracle (bounded sample)")
+        log("bench: timing the CPU restatement (bounded sample)")
         result["cpu_baseline"] = cpu_baseline([q_qkv, q_down], [x_qkv, x_down])
+        if not args.no_detail:
+            log("bench: cfg4 GEMM on the CPU")
+            q4 = synth_nf4(14336, 4096, seed=40 + 4096)
+            a4 = torch.randn(2048, 4096, generator=torch.Generator().manual_seed(4096)).bfloat16()
+            result["cpu_baseline"].update(cpu_gemm_baseline(q4, a4))
+            del q4, a4
+            log("bench: cfg5 on the CPU (variant B, reduced token count)")
+            result["cpu_baseline"].update(cpu_decode_baseline(dev))
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
 
 
 COPY_BYTES = 16 << 20  # plain copy of known size: FETCH_SIZE / WRITE_SIZE scale factors
+
+# The sources that fix the measured kernel's memory traffic (kernel body and its launch plan).
+TRAFFIC_SOURCES = ("spectra_amd/csrc/gemv_stream.h", "spectra_amd/csrc/gemv_stream_f16.hip", "spectra_amd/csrc/gemv.hip")
+
+
+def kernel_source_hash() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def measured_traffic():
+    """HBM bytes per launch of the down_proj GEMV from the committed PMC summary, only when
+    it was measured on the kernel these sources build (same sha256); else None."""
+    tf = os.path.join(ROOT, "profiles", "traffic_gemv_cfg2_down.json")
+    if not os.path.exists(tf):
+        return None, "no PMC summary"
+    with open(tf) as f:
+        rec = json.load(f)
+    if rec.get("kernel_source_sha256") != kernel_source_hash():
+        return None, "PMC summary was measured on other kernel sources (sha256 differs): not reported"
+    return rec.get("hbm_bytes_per_launch"), "profiles/traffic_gemv_cfg2_down.json (sha256 of the kernel sources matches)"
 
 
 def calibrate_copy(dev) -> None:
@@ -359,6 +479,21 @@ def secondary(lib, dev, pool_gb: float) -> dict:
         out[f"cfg3_gate_up_m{m}_us"] = round(t * 1e6, 2)
         out[f"cfg3_gate_up_m{m}_GBps"] = round(gemv_bytes(q3, m) / t / 1e9, 1)
     del q3, pool, pool_ops
+    # cfg3 down_proj: K=8192 -> N=3072 at M=4/8/16
+    q3d = synth_nf4(3072, 8192, seed=31)
+    P = pool_copies(q3d.nbytes(), pool_gb * 1e9)
+    pool = [q3d] + [clone_nf4(q3d) for _ in range(P - 1)]
+    pool_ops = [operands(q) for q in pool]
+    for m in (4, 8, 16):
+        xm = torch.randn(m, 8192, generator=torch.Generator().manual_seed(31 + m)).half().to(dev)
+        ym = torch.empty(m, 3072, dtype=torch.float16, device=dev)
+        calls = [Launcher(lib, o, xm, ym) for o in pool_ops]
+        nl = max(P, 100)
+        t = time_graph(graph_of([calls[i % P] for i in range(nl)])) / nl
+        out[f"cfg3_down_m{m}_us"] = round(t * 1e6, 2)
+        out[f"cfg3_down_m{m}_GBps"] = round(gemv_bytes(q3d, m) / t / 1e9, 1)
+    del q3d, pool, pool_ops
+    out.update(host_overhead(lib, dev))
     # cfg4: prefill GEMM M=2048, (K,N) = (4096,14336) and (14336,4096), bf16
     for (kk, nn) in ((4096, 14336), (14336, 4096)):
         q4 = synth_nf4(nn, kk, seed=40 + kk)
@@ -390,6 +525,44 @@ def secondary(lib, dev, pool_gb: float) -> dict:
     out["cfg5_note"] = "113 GEMVs of one decode token (28 layers + lm_head) in one graph; attention/norms excluded"
     del chain, keep, layer, head
     out.update(decode_e2e(dev))
+    return out
+
+
+def host_overhead(lib, dev, n: int = 3000) -> dict:
+    """Host time to issue one eager M=1 down_proj call (cfg2 shape), measured as the issue
+    rate of ``n`` back-to-back calls: the C-ABI entry point through ctypes, the functional
+    API (fused_w4a16_gemv_hdsq, cached descriptor) and the module (SpectraFusedLinear).
+    Whichever exceeds the kernel's own time bounds an eager caller."""
+    from spectra_amd.engine import SpectraFusedLinear
+    q = synth_nf4(3072, 8192, seed=32)
+    x = torch.randn(1, 8192, generator=torch.Generator().manual_seed(32)).half().to(dev)
+    y = torch.empty(1, 3072, dtype=torch.float16, device=dev)
+    raw = Launcher(lib, operands(q), x, y)
+    stream = torch.cuda.current_stream().cuda_stream
+    col, val = q.outliers()
+    lin = SpectraFusedLinear(8192, 3072, q.blocksize, codebook="nf4", hadamard_block=HAD).to(dev)
+    lin.set_weights(q.packed, q.absmax, None, outlier_idx=col, outlier_weight=val, marlin_layout=True,
+                    outlier_rowptr=q.rowptr)
+
+    def issue(fn):
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        return (t1 - t0) / n * 1e6
+
+    with torch.no_grad():
+        out = {"eager_m1_issue_us_c_abi": round(issue(lambda: raw(stream)), 2),
+               "eager_m1_issue_us_functional": round(issue(lambda: K.fused_w4a16_gemv_hdsq(
+                   x, q.packed, q.absmax, None, outlier_idx=col, outlier_w=val, marlin_layout=True,
+                   out=y, **q.kernel_kwargs())), 2),
+               "eager_m1_issue_us_module": round(issue(lambda: lin(x)), 2)}
+    out["eager_note"] = ("host issue time per eager M=1 down_proj call (3000 back-to-back calls); the kernel itself "
+                         "takes down_gemv_us, so above that an eager caller is host-bound and a HIP graph is the remedy")
     return out
 
 

@@ -79,67 +79,23 @@ def _w_eff(q):
 
 
 class RefDecoder:
-    """fp32 restatement of SpectraDecoder's math on the dequantized weights."""
+    """fp32 restatement of SpectraDecoder's math on the dequantized weights: the oracle's
+    torch decoder (oracle/torch_ref.py) fed the bit-exact W_eff of every quantized weight."""
 
     def __init__(self, dec: SpectraDecoder):
-        self.c = dec.cfg
+        from oracle import torch_ref as TR
+        c = dec.cfg
+        self.c = c
         self.w = [[_w_eff(q) for q in layer] for layer in dec.layers_q]
         self.had = [[q.hadamard_block for q in layer] for layer in dec.layers_q]
         self.emb = _w_eff(dec.embed_q)
         self.head = _w_eff(dec.lm_q)
         self.norm = [w.float() for w in dec.norm_w]
-        hd = self.c.head_dim
-        inv = 1.0 / (self.c.rope_theta ** (torch.arange(0, hd, 2, device="cuda", dtype=torch.float32) / hd))
-        ang = torch.arange(self.c.max_seq, device="cuda", dtype=torch.float32)[:, None] * inv[None, :]
-        self.cos, self.sin = torch.cos(ang), torch.sin(ang)
-        self.k, self.v = [], []
-
-    def lin(self, x, w, had):
-        xr = K.fwht_rows(x.contiguous(), had, out_dtype=torch.float32) if had else x
-        return xr @ w.T
-
-    def rms(self, x, i):
-        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.c.rms_eps) * self.norm[i]
-
-    def rope(self, x, pos):
-        h2 = x.shape[-1] // 2
-        c, s = self.cos[pos][:, None, :], self.sin[pos][:, None, :]
-        a, b = x[..., :h2], x[..., h2:]
-        return torch.cat([a * c - b * s, b * c + a * s], dim=-1)
+        self.dec = TR.Decoder(self.w, self.had, self.norm, self.emb, self.head, heads=c.heads, kv_heads=c.kv_heads,
+                              rope_theta=c.rope_theta, rms_eps=c.rms_eps, max_seq=c.max_seq)
 
     def forward(self, ids, pos0):
-        c, hd = self.c, self.c.head_dim
-        T = ids.numel()
-        pos = torch.arange(pos0, pos0 + T, device="cuda")
-        h = self.emb[ids]
-        for li, (wqkv, wo, wgu, wd) in enumerate(self.w):
-            hq, ho, hg, hdn = self.had[li]
-            x = self.rms(h, 2 * li)
-            qkv = self.lin(x, wqkv, hq)
-            q = qkv[:, : c.hidden].reshape(T, c.heads, hd)
-            k = qkv[:, c.hidden: c.hidden + c.kv_heads * hd].reshape(T, c.kv_heads, hd)
-            v = qkv[:, c.hidden + c.kv_heads * hd:].reshape(T, c.kv_heads, hd)
-            q, k = self.rope(q, pos), self.rope(k, pos)
-            if li == len(self.k):
-                self.k.append(k)
-                self.v.append(v)
-            else:
-                self.k[li] = torch.cat([self.k[li], k])
-                self.v[li] = torch.cat([self.v[li], v])
-            kk = self.k[li].repeat_interleave(c.heads // c.kv_heads, dim=1)  # [L, heads, hd]
-            vv = self.v[li].repeat_interleave(c.heads // c.kv_heads, dim=1)
-            # fp32 matmuls on contiguous operands
-            s = torch.matmul(q.permute(1, 0, 2).contiguous(), kk.permute(1, 2, 0).contiguous()) / math.sqrt(hd)
-            L = kk.shape[0]
-            mask = torch.arange(L, device="cuda")[None, :] > pos[:, None]
-            s = s.masked_fill(mask[None], float("-inf"))
-            a = torch.matmul(torch.softmax(s, -1), vv.permute(1, 0, 2).contiguous())  # [heads, T, hd]
-            a = a.permute(1, 0, 2).reshape(T, c.hidden)
-            h = h + self.lin(a, wo, ho)
-            x = self.rms(h, 2 * li + 1)
-            gu = self.lin(x, wgu, hg)
-            h = h + self.lin(torch.nn.functional.silu(gu[:, : c.inter]) * gu[:, c.inter:], wd, hdn)
-        return self.rms(h[-1:], 2 * c.layers) @ self.head.T
+        return self.dec.forward(ids, pos0)
 
 
 def test_decoder_against_fp32_reference(hip):

@@ -381,3 +381,67 @@ def test_kv4_oracle_invariants():
     assert np.all(err <= step * (1 + 1e-2) + np.abs(xf) * 2 ** -8 + 1e-30)
     assert np.mean(err <= step / 2 * (1 + 1e-2) + np.abs(xf) * 2 ** -8) > 0.99  # clipping is rare
     assert np.array_equal(deq[0, 0], xf[0, 0]) and np.array_equal(deq[1, 1], xf[1, 1])
+
+
+# ----------------------------------------------------------------------------
+# oracle/torch_ref.py: the same arithmetic in torch (the CPU baseline's implementation)
+# ----------------------------------------------------------------------------
+from oracle import torch_ref as TR  # noqa: E402
+
+
+@pytest.mark.parametrize("marlin", [True, False])
+@pytest.mark.parametrize("block", [64, 32])
+def test_torch_ref_dequant_and_fwht_bitexact(marlin, block):
+    rng = np.random.default_rng(block + marlin)
+    n, k = 24, 512
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    mask = rng.random((n, k)) < 0.02
+    w[mask] = (rng.standard_normal(mask.sum()) * 0.2).astype(np.float16)
+    q = O.nf4_quantize(w, "float16", block, 0, mask, marlin)
+    args = [torch.from_numpy(q[a]) for a in ("packed", "absmax", "rowptr", "col", "val")]
+    for out_dtype, name in ((torch.float32, "float32"), (torch.float16, "float16")):
+        got = TR.nf4_dequant(*args, marlin=marlin, blocksize=block, out_dtype=out_dtype).numpy()
+        ref = O.nf4_dequant(q["packed"], q["absmax"], marlin, name, q["rowptr"], q["col"], q["val"], blocksize=block)
+        assert np.array_equal(got, ref)
+    x = rng.standard_normal((3, k)).astype(np.float16)
+    for had in (128, 64, 0):
+        assert np.array_equal(TR.fwht_blocks(torch.from_numpy(x), had).numpy(),
+                              O.rotate_blocks(x.astype(np.float32), had))
+
+
+def test_torch_ref_linear_matches_linear_ref():
+    rng = np.random.default_rng(7)
+    n, k = 40, 1024
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16)
+    mask = rng.random((n, k)) < 0.01
+    q = O.nf4_quantize(w, "float16", 64, 0, mask, True)
+    x = rng.standard_normal((2, k)).astype(np.float16)
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, "float32", q["rowptr"], q["col"], q["val"])
+    ref = O.linear_ref(x, "float16", w_eff, "float32", hadamard_block=128)
+    args = [torch.from_numpy(q[a]) for a in ("packed", "absmax", "rowptr", "col", "val")]
+    ya = TR.linear_a(torch.from_numpy(x).float(), *args, hadamard_block=128).double().numpy()
+    yb = TR.linear_b(torch.from_numpy(x).float(), torch.from_numpy(w_eff), hadamard_block=128).double().numpy()
+    assert np.abs(ya - ref).max() <= 1e-5 * np.abs(ref).max() and np.array_equal(ya, yb)
+
+
+def test_torch_ref_decoder_pieces_closed_forms():
+    g = torch.Generator().manual_seed(3)
+    # RoPE: a rotation of each (a_i, b_i) pair by the position's angle -- norms kept, and the
+    # unit vector e_0 goes to (cos, ..., sin, ...) in the split halves
+    x = torch.randn(5, 4, 64, generator=g)
+    ang = torch.rand(5, 32, generator=g) * 6
+    y = TR.rope(x, torch.cos(ang), torch.sin(ang))
+    assert torch.allclose(y.norm(dim=-1), x.norm(dim=-1), rtol=1e-5)
+    e0 = torch.zeros(5, 1, 64)
+    e0[..., 0] = 1
+    r = TR.rope(e0, torch.cos(ang), torch.sin(ang))
+    assert torch.allclose(r[:, 0, 0], torch.cos(ang[:, 0])) and torch.allclose(r[:, 0, 32], torch.sin(ang[:, 0]))
+    # attention at position 0 sees one key: the output is that position's value row per head
+    q = torch.randn(1, 8, 16, generator=g)
+    k = torch.randn(3, 2, 16, generator=g)
+    v = torch.randn(3, 2, 16, generator=g)
+    a = TR.attention(q, k, v, torch.tensor([0]))
+    assert torch.allclose(a.reshape(8, 16), v[0].repeat_interleave(4, dim=0))
+    # RMSNorm of a constant row is the norm weight (eps negligible)
+    wn = torch.rand(32, generator=g)
+    assert torch.allclose(TR.rms_norm(torch.full((1, 32), 3.5), wn, 1e-12), wn[None, :], rtol=1e-6)
