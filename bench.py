@@ -379,7 +379,7 @@ def main():
                                "+ fp16 absmax + FWHT-128 activations + 0.5% fp16 CSR outliers",
                    "global_batch": 1, "seq_len": 1, "parallelism": "none (1 GPU)",
                    "bytes_per_step": step_bytes, "weight_pool_copies": P, "timing": "one HIP graph of all steps"},
-        "roofline": {"bound": "hbm", "kernel": "gemv_stream_kernel (down_proj K=8192 N=3072)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_rows_kernel (down_proj K=8192 N=3072)",
                      "achieved": round(achieved, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_note, "algorithmic_bytes_per_launch": b_down,
@@ -409,7 +409,8 @@ def main():
 COPY_BYTES = 16 << 20  # plain copy of known size: FETCH_SIZE / WRITE_SIZE scale factors
 
 # The sources that fix the measured kernel's memory traffic (kernel body and its launch plan).
-TRAFFIC_SOURCES = ("spectra_amd/csrc/gemv_stream.h", "spectra_amd/csrc/gemv_stream_f16.hip", "spectra_amd/csrc/gemv.hip")
+TRAFFIC_SOURCES = ("spectra_amd/csrc/gemv_rows.h", "spectra_amd/csrc/gemv_rows_inst.h", "spectra_amd/csrc/gemv_rows_plain.hip",
+                   "spectra_amd/csrc/gemv.hip", "spectra_amd/csrc/common.h")
 
 
 def kernel_source_hash() -> str:

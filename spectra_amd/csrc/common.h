@@ -143,6 +143,29 @@ __device__ __forceinline__ void build_pair_lut(uint8_t* smem, int wave, int nwav
   }
 }
 
+// The same table in 32 copies (lanes l and l + 32 share copy l & 31: the LDS serves a
+// wave's 4-byte reads in two halves of 32 lanes, one bank per lane in each): row v at
+// v * 256, copy c at + 4 c (the upper 128 bytes of every row are not written), half the
+// LDS writes of build_pair_lut.  Wave w of nwaves fills the rows of high codes w,
+// w + nwaves, ...: 16 rows of 128 B as two wave-instructions of 1 KB (lane >> 3 picks the
+// row, lane & 7 the 16-byte chunk).  Readers address it with ((lane & 31) << 2).
+template <int FMT>
+__device__ __forceinline__ void build_pair_lut32(uint8_t* smem, int wave, int nwaves, int lane) {
+  const uint32_t* pairs = FMT == SPECTRA_FMT_NF4 ? kNf4CodePairs : kIntCodePairs;
+  const int m = lane >> 3;  // low codes m and 8 + m
+  const uint32_t pa = m < 2 ? pairs[0] : m < 4 ? pairs[1] : m < 6 ? pairs[2] : pairs[3];
+  const uint32_t pb = m < 2 ? pairs[4] : m < 4 ? pairs[5] : m < 6 ? pairs[6] : pairs[7];
+  const uint32_t c0 = (m & 1) ? (pa >> 16) : (pa & 0xffffu), c1 = (m & 1) ? (pb >> 16) : (pb & 0xffffu);
+  uint4* lut = (uint4*)smem;
+  for (int h = wave; h < 16; h += nwaves) {
+    // the high code (wave-uniform): code h sits in c0 (h < 8) or c1 of lane 8 (h & 7)
+    const uint32_t hb = (uint32_t)__builtin_amdgcn_readlane((int)(h < 8 ? c0 : c1), 8 * (h & 7)) << 16;
+    const uint32_t e0 = c0 | hb, e1 = c1 | hb;
+    lut[(16 * h + m) * 16 + (lane & 7)] = make_uint4(e0, e0, e0, e0);
+    lut[(16 * h + 8 + m) * 16 + (lane & 7)] = make_uint4(e1, e1, e1, e1);
+  }
+}
+
 // Load through a wave-uniform base plus a 32-bit per-lane byte offset: the global_load
 // saddr form (base in SGPRs, offset in one VGPR), with no per-lane 64-bit address math.
 template <typename T>

@@ -1,9 +1,11 @@
 // Host side of the decode GEMV family: decomposition, LDS layout, argument checks and
 // launch.  The kernels live in gemv_kernel.h, instantiated per activation dtype in
 // gemv_f16.hip and gemv_bf16.hip.
+#include <algorithm>
 #include <cmath>
 
 #include "gemv_kernel.h"
+#include "gemv_rows_inst.h"
 #include "gemv_stream.h"
 
 namespace spectra {
@@ -202,6 +204,133 @@ static int stream_launch(const spectra_qweight_t* w, const StreamPlan& pl, const
   return SPECTRA_OK;
 }
 
+// ---------------------------------------------------------------------------
+// row-owning kernel plan (one activation row, NF4, Hadamard block 128 or none)
+// ---------------------------------------------------------------------------
+struct RowsPlan {
+  int G, SPR, RPG, XC, W, WR, R, grid, nchunk, cpr;
+  bool split;
+  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res, off_flag, lds_bytes;
+};
+
+static gemv_rows_fn rows_fn(int g, int spr, int rpg, int xc, bool split, bool bf, int pro) {
+  return pro == kProNone ? gemv_rows_pick_plain(g, spr, rpg, xc, split, bf) : gemv_rows_pick_pro(g, spr, rpg, xc, split, pro);
+}
+
+// R = ceil(N / CUs) rows per workgroup (one workgroup per CU); lane groups of G = 64 lanes
+// (32 when K / 1024 is odd) own RPG rows each.  Preferred: the fewest rows per group whose
+// row waves leave spare waves (up to 16 per workgroup) to produce the activations, each
+// rotating at most four 512-value chunks (measured: for down_proj 12 row waves with 4
+// producers beat 6 row waves of twice the rows with 10); otherwise every wave does both
+// jobs.
+static bool plan_rows(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block, int ncu, bool bf, int pro,
+                      RowsPlan* pl) {
+  if (k % 1024 != 0 || k > 14336 || ncu <= 0 || block < 32 || block > 1024) return false;
+  if ((k / block) % 8 != 0 || (lda * 2) % 16 != 0) return false;  // absmax rows in whole 16-byte chunks
+  const int P = (int)(k / 1024);
+  const int G = P % 2 == 0 ? 64 : 32;
+  const int SPR = P * 32 / G;
+  const int64_t R = (n + ncu - 1) / ncu;
+  const int nchunk = (int)(k / 512);
+  const int cpr = (int)(k / block / 8);
+  const int nsmax = SPR == 3 ? 12 : 8;
+  if (R * ldp >= (int64_t(1) << 31) || R * lda * 2 >= (int64_t(1) << 31)) return false;
+  bool found = false;
+  for (int pass = 0; pass < 2 && !found; ++pass) {
+    const bool split = pass == 0;
+    for (int RPG = 1; RPG <= 8 && !found; RPG *= 2) {
+      if (SPR * RPG > nsmax) break;
+      const int64_t NG = (R + RPG - 1) / RPG;
+      const int64_t WR = (NG * G + 63) / 64;
+      if (WR > 16) continue;
+      int W, XC;
+      if (split) {
+        const int nh = std::min(16 - (int)WR, nchunk);
+        if (nh < 1) continue;
+        XC = (nchunk + nh - 1) / nh;
+        XC = XC <= 1 ? 1 : XC <= 2 ? 2 : XC <= 4 ? 4 : 0;
+        if (XC == 0 || R * cpr > 64 * nh) continue;
+        W = (int)WR + nh;
+      } else {
+        W = std::max((int)WR, std::min(nchunk, 16));
+        XC = (nchunk + W - 1) / W;
+        if (XC > 1 || R * cpr > 64 * W) continue;
+      }
+      if (rows_fn(G, SPR, RPG, XC, split, bf, pro) == nullptr) continue;
+      pl->G = G; pl->SPR = SPR; pl->RPG = RPG; pl->XC = XC; pl->W = W; pl->WR = (int)WR; pl->split = split;
+      found = true;
+    }
+  }
+  if (!found) return false;
+  pl->R = (int)R; pl->nchunk = nchunk; pl->cpr = cpr;
+  pl->grid = (int)((n + R - 1) / R);
+  uint32_t off = kLutBytes;
+  pl->off_xp = off;
+  off = align16(off + (uint32_t)(k * 2));
+  pl->off_xsc = off;
+  off = align16(off + (uint32_t)(k / 128 * 4));
+  pl->off_sc = off;
+  off = align16(off + (uint32_t)(R * (k / block) * 4));
+  pl->off_ss = off;
+  off = align16(off + (uint32_t)(kMaxWaves * 4));
+  pl->off_bias = off;
+  off = align16(off + (uint32_t)(R * 4));
+  pl->off_res = off;
+  off = align16(off + (uint32_t)(R * 2));
+  pl->off_flag = off;
+  off = align16(off + 8u);  // two counters
+  pl->lds_bytes = off;
+  return off <= 163840;
+}
+
+static bool rows_serves(const spectra_qweight_t* w, int m, int act_dtype, int kpro, RowsPlan* pl) {
+  if (m != 1 || w->format != SPECTRA_FMT_NF4 || w->group_size < 32) return false;
+  if (w->hadamard_block != 0 && w->hadamard_block != 128) return false;
+  if (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS) return false;
+  if (w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz >= (int64_t(1) << 29)) return false;
+  if (!ptr_aligned(w->scales, 16)) return false;
+  if (kpro != kProNone && act_dtype != SPECTRA_F16) return false;
+  return plan_rows(w->n, w->k, w->packed_stride, w->scales_stride, w->group_size, device_cu_count(),
+                   act_dtype == SPECTRA_BF16, kpro, pl);
+}
+
+static int rows_launch(const spectra_qweight_t* w, const RowsPlan& pl, const void* x, int act_dtype, void* out,
+                       hipStream_t stream, const spectra_gemv_fusion_t* fu, int kpro) {
+  RowsParams p;
+  p.packed = w->packed; p.ldp = w->packed_stride;
+  p.absmax = w->scales; p.lda = w->scales_stride;
+  const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
+  p.rowptr = csr ? w->csr_rowptr : nullptr;
+  p.ccol = csr ? w->csr_col : nullptr;
+  p.cval = csr ? w->csr_val : nullptr;
+  p.csr = csr ? 1 : 0;
+  p.csr_nnz = csr ? (int)w->csr_nnz : 0;
+  p.bias = w->bias; p.bias_dt = w->bias_dtype;
+  p.x = x; p.out = out;
+  p.nw = fu ? fu->norm_weight : nullptr;
+  p.res = fu ? fu->residual : nullptr;
+  p.eps = fu ? fu->eps : 0.0f;
+  p.had = w->hadamard_block;
+  p.out_scale = w->hadamard_block ? (float)(1.0 / std::sqrt((double)w->hadamard_block)) : 1.0f;
+  p.n = (int)w->n; p.k = (int)w->k;
+  p.R = pl.R; p.nchunk = pl.nchunk;
+  int gs = 0;
+  while ((1 << gs) < w->group_size) ++gs;
+  p.gshift = gs;
+  p.marlin = w->marlin_layout ? 1 : 0;
+  p.cpr = pl.cpr;
+  p.cmagic = (65536 + pl.cpr - 1) / pl.cpr;
+  p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_sc = pl.off_sc; p.off_ss = pl.off_ss;
+  p.off_bias = pl.off_bias; p.off_res = pl.off_res; p.off_flag = pl.off_flag;
+  p.wr = pl.WR;
+  const gemv_rows_fn fn = rows_fn(pl.G, pl.SPR, pl.RPG, pl.XC, pl.split, act_dtype == SPECTRA_BF16, kpro);
+  const int st = ensure_lds_limit((const void*)fn, true);
+  if (st != SPECTRA_OK) return st;
+  hipLaunchKernelGGL(fn, dim3(pl.grid), dim3(64 * pl.W), pl.lds_bytes, stream, p);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
 // the stream kernel serves one row of NF4 activations with CSR outliers or none, K a
 // multiple of 1024 up to 16384, and at most kStreamMaxSlots rows per lane
 static bool stream_serves(const spectra_qweight_t* w, int m, StreamPlan* pl) {
@@ -215,6 +344,8 @@ static bool stream_serves(const spectra_qweight_t* w, int m, StreamPlan* pl) {
 // workgroups of the plan for m activation rows (0 when the family does not serve the shape);
 // the descriptor is already validated
 int gemv_plan_grid(const spectra_qweight_t* w, int m) {
+  RowsPlan rp;
+  if (rows_serves(w, m, SPECTRA_F16, kProNone, &rp)) return rp.grid;
   StreamPlan sp;
   if (stream_serves(w, m, &sp)) return sp.grid;
   const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
@@ -244,6 +375,8 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
                     "CSR columns must be 16-byte and values 8-byte aligned (nnz < 2^31)");
   // the kernels pair each format with its own outlier kind and scale scheme: Format B
   // (NF4, blocks >= 64, CSR outliers), Format A (groups of 32, dense outlier columns)
+  RowsPlan rp;
+  if (rows_serves(w, m, act_dtype, kpro, &rp)) return rows_launch(w, rp, x, act_dtype, out, stream, fu, kpro);
   StreamPlan sp;
   if (stream_serves(w, m, &sp)) return stream_launch(w, sp, x, act_dtype, out, stream, fu, kpro);
   if (w->format == SPECTRA_FMT_NF4 && w->group_size < 64)

@@ -1,0 +1,535 @@
+// One-row decode GEMV for NF4 weights, rows owned by lane groups:
+//   out[0, :] = FWHT_128(x) . W_eff^T (+ CSR outliers, bias, residual), fp32 accumulation.
+//
+// Replaces the reference's single-row Triton GEMV (kernels.py:16-184) for Format B operands
+// at M = 1 with a Hadamard block of 128 (or none), the decode hot path.  A launch is bound
+// by HBM, and what keeps it from the bound is work that cannot overlap the weight stream:
+// the rotated activations must exist before the first dot product, and every cross-wave
+// reduction after the last byte lands is on the critical path.  This design keeps both
+// short.
+//
+//  * A lane group (G = 64 lanes, or 32 when K / 1024 is odd) owns RPG whole rows: slot
+//    s = j * SPR + c streams the 16-byte run c * G + li of row j, so a row's dot product
+//    never leaves its group.  The tail is one in-group butterfly sum per row, with no
+//    cross-wave reduction and no per-row phase.
+//  * The activations are rotated on the matrix cores: with H_128 = H_4 (x) H_32, a chunk of
+//    512 values (16 sub-blocks of 32) times H_32 is two v_mfma_f32_16x16x32 (columns of
+//    H_32 in the pair order the packed bytes use), and the H_4 factor combines the four
+//    sub-blocks of a 128-block that the MFMA output leaves in one lane.  Without rotation
+//    the same MFMAs multiply by a permutation (exact), so one code path serves both.
+//    Each 128-block gets a power-of-two scale (max |x| -> [2^14, 2^15)) before the fp16
+//    packing; the scale is exact and undone per slot.
+//  * Roles (SPLIT): the waves past the row waves are producers.  They issue the
+//    activation chunks and the staging loads (block scales, bias, residual) before a
+//    start barrier, so those requests sit ahead of every weight request in the CU's memory
+//    queue; after it they build the nibble-pair LUT, rotate the chunks, stage the scales
+//    and count themselves done on an LDS counter.  The row waves issue their weight runs
+//    right after the barrier, then the CSR entries of their rows (extents from scalar
+//    loads issued at entry), and wait on the counter before the first dot product.  A row
+//    wave held in its load issue (the CU's memory queue fills while the weights stream)
+//    holds up nobody else, which a second workgroup barrier would.  The wait is bounded
+//    (a counter that never completes gives wrong output, never a hang).
+//    Without spare waves (!SPLIT) every wave does both jobs: loads first, then the
+//    producer work, then a barrier.
+//  * Every wait on a weight run is exact and never covers a later load: the loads under
+//    per-thread conditions come first, every later load is issued by every lane of the
+//    path (dummy in-bounds addresses where a lane has nothing to load).
+//  * Decode: the 256-entry nibble-pair LUT in LDS in 32 copies (lane l reads bank l & 31;
+//    the LDS serves the two 32-lane halves of a read in turn, so no conflicts), one
+//    v_perm + ds_read_b32 + v_dot2_f32_f16 per packed byte.
+#pragma once
+
+#include "gemv_stream.h"  // shared helpers: load_nt_u4, pack_scaled, xs_pos
+
+namespace spectra {
+
+struct RowsParams {
+  const uint8_t* packed;
+  int64_t ldp;
+  const uint16_t* absmax;
+  int64_t lda;
+  const int32_t* rowptr;
+  const int32_t* ccol;
+  const uint16_t* cval;
+  const void* bias;
+  const void* x;
+  void* out;
+  const uint16_t* nw;  // kProRms: RMSNorm weight fp16 [K]
+  const void* res;     // optional residual [N] (act dtype, may alias out): out = res + out
+  float eps;           // kProRms
+  float out_scale;     // 1/sqrt(128) with rotation, 1 without
+  int n, k;
+  int R;               // rows per workgroup
+  int nchunk;          // K / 512
+  int gshift;          // log2(NF4 block), >= 5
+  int had;             // 128 or 0
+  int marlin;
+  int csr;             // CSR outliers present (nnz > 0)
+  int csr_nnz;
+  int bias_dt;
+  int cpr;             // 16-byte absmax chunks per row (K / block / 8)
+  int cmagic;          // ceil(65536 / cpr): t / cpr == (t * cmagic) >> 16 for t < 1024
+  int wr;              // row waves (waves wr .. W-1 are producers when split)
+  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res, off_flag;
+};
+
+constexpr int kRowsSpinLimit = 1 << 20;  // s_sleep rounds a row wave waits for the producers, at most
+
+typedef _Float16 rh8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 rb8_t __attribute__((ext_vector_type(8)));
+typedef float rf4_t __attribute__((ext_vector_type(4)));
+
+// Max over each 16-lane row with DPP only (every lane of the row ends with the row's max).
+__device__ __forceinline__ float row16_max(float v) {
+  int t;
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  v = fmaxf(v, __builtin_bit_cast(float, t));
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  v = fmaxf(v, __builtin_bit_cast(float, t));
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false);  // row_half_mirror
+  v = fmaxf(v, __builtin_bit_cast(float, t));
+  t = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false);  // row_mirror
+  return fmaxf(v, __builtin_bit_cast(float, t));
+}
+
+// Sum over a lane group of G lanes (32: a half-wave, 64: the wave), same value in every lane.
+template <int G>
+__device__ __forceinline__ float group_sum(float v, int lane) {
+  if constexpr (G == 64) v += lane_xor<32>(v, lane);
+  v += lane_xor<16>(v, lane);
+  v += lane_xor<8>(v, lane);
+  v += lane_xor<4>(v, lane);
+  v += lane_xor<2>(v, lane);
+  return v + lane_xor<1>(v, lane);
+}
+
+// ---------------------------------------------------------------------------
+// the kernel's phases (forced inline: the registers they hand over stay in registers)
+// ---------------------------------------------------------------------------
+struct RowsCtx {
+  int tid, lane, wave, W, K, Q, r0, Rw, gi, li, grow0;
+};
+
+// producer loads: the workgroup's block scales (one 16-byte chunk per producer thread below
+// R * cpr), bias and residual (producer threads below Rw), then the activation chunks
+// pw + np i (lane (i, g) = (lane & 15, lane >> 4) holds elements 32 i + 8 g .. + 7 of the
+// chunk, the MFMA A operand; chunks past the last read chunk 0)
+template <int XC, int PRO>
+struct ProducerRegs {
+  uint4 scv;
+  uint32_t bias_raw = 0;
+  uint16_t res_raw = 0;
+  uint4 xr[XC], xu[PRO == kProSiluMul ? XC : 1], nwr[PRO == kProRms ? XC : 1];
+};
+
+template <int XC, int PRO>
+__device__ __forceinline__ void rows_producer_loads(const RowsParams& p, const RowsCtx& c, int pw, int np, int ptid,
+                                                    ProducerRegs<XC, PRO>& r) {
+  const int srow = (ptid * p.cmagic) >> 16;  // ptid / cpr
+  if (pw * 64 < p.R * p.cpr) {
+    const int sr = srow < c.Rw ? srow : 0;
+    r.scv = load_at<uint4>(p.absmax + (int64_t)c.r0 * p.lda,
+                           (uint32_t)(sr * p.lda) * 2u + (uint32_t)(ptid - srow * p.cpr) * 16u);
+  }
+  if (pw * 64 < c.Rw) {
+    const uint32_t ti = (uint32_t)(ptid < c.Rw ? ptid : 0);
+    if (p.bias != nullptr) {
+      if (p.bias_dt == SPECTRA_F32) r.bias_raw = load_at<uint32_t>((const uint32_t*)p.bias + c.r0, 4u * ti);
+      else r.bias_raw = load_at<uint16_t>((const uint16_t*)p.bias + c.r0, 2u * ti);
+    }
+    if (p.res != nullptr) r.res_raw = load_at<uint16_t>((const uint16_t*)p.res + c.r0, 2u * ti);
+  }
+  const uint32_t xlo = 64u * (uint32_t)(c.lane & 15) + 16u * (uint32_t)(c.lane >> 4);
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int ch = pw + np * i;
+    const uint32_t o = (ch < p.nchunk ? (uint32_t)ch * 1024u : 0u) + xlo;
+    r.xr[i] = load_at<uint4>(p.x, o);
+    if constexpr (PRO == kProSiluMul) r.xu[i] = load_at<uint4>(p.x, o + 2u * (uint32_t)c.K);
+    if constexpr (PRO == kProRms) r.nwr[i] = load_at<uint4>(p.nw, o);
+  }
+}
+
+// producer work after the LUT: the rotated chunks as fp16 pairs with one power-of-two scale
+// per 128-block, block scales (fp32), bias, residual, RMSNorm partials
+template <int XC, bool BF, int PRO>
+__device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& c, uint8_t* smem, int pw, int np,
+                                             int ptid, const ProducerRegs<XC, PRO>& r) {
+  uint32_t* xpd = (uint32_t*)(smem + p.off_xp);  // [pair / 4][run][pair % 4] dwords
+  float* xsc = (float*)(smem + p.off_xsc);       // one scale per 128-block
+  const int lane = c.lane, Q = c.Q;
+  // B operands: column j of MFMA 1 / 2 is H_32 column (or unit column) pi1(j) / pi2(j),
+  // the low / high position of packed pair j (marlin: j, j + 16; plain: 2 j, 2 j + 1)
+  const int jj = lane & 15, g = lane >> 4;
+  const int pi1 = p.marlin ? jj : 2 * jj;
+  const uint32_t one = BF ? 0x3f80u : 0x3c00u;
+  uint32_t b1[4], b2[4];
+  if (p.had) {
+    // sign of H_32[8 g + t][pi] = parity(g & pi >> 3) ^ parity(t & pi & 7): the byte of
+    // Walsh row pi & 7 over t, complemented when the high parity is odd
+    uint32_t w8 = (uint32_t)(0x963c5af066ccaa00ull >> (8 * (pi1 & 7))) & 0xffu;
+    if (__builtin_popcount(g & (pi1 >> 3)) & 1) w8 ^= 0xffu;
+#pragma unroll
+    for (int t2 = 0; t2 < 4; ++t2)
+      b1[t2] = (one | (one << 16)) | (((w8 >> (2 * t2)) & 1u) << 15) | (((w8 >> (2 * t2 + 1)) & 1u) << 31);
+    // pi2 = pi1 + 16 (marlin: flips with bit 4 of k, i.e. bit 1 of g) or pi1 + 1 (plain:
+    // flips with bit 0 of k, the high half of every dword)
+    const uint32_t f2 = p.marlin ? ((g & 2) ? 0x80008000u : 0u) : 0x80000000u;
+#pragma unroll
+    for (int t2 = 0; t2 < 4; ++t2) b2[t2] = b1[t2] ^ f2;
+  } else {
+    // unit columns: B[k][j] = (k == pi(j)), k = 8 g + 2 t2 (+1)
+    const int pi2 = p.marlin ? jj + 16 : 2 * jj + 1;
+#pragma unroll
+    for (int t2 = 0; t2 < 4; ++t2) {
+      const int k0 = 8 * g + 2 * t2;
+      b1[t2] = (k0 == pi1 ? one : 0u) | (k0 + 1 == pi1 ? one << 16 : 0u);
+      b2[t2] = (k0 == pi2 ? one : 0u) | (k0 + 1 == pi2 ? one << 16 : 0u);
+    }
+  }
+  float ssq = 0.0f;
+  // one rolled loop over the chunks: its code is fetched once (a cold instruction cache costs
+  // more than the selects that pick the chunk's registers; all chunks land together)
+  uint4 xq[XC], uq[PRO == kProSiluMul ? XC : 1], nq[PRO == kProRms ? XC : 1];
+#pragma unroll
+  for (int t = 0; t < XC; ++t) {
+    xq[t] = r.xr[t];
+    if constexpr (PRO == kProSiluMul) uq[t] = r.xu[t];
+    if constexpr (PRO == kProRms) nq[t] = r.nwr[t];
+  }
+#pragma unroll 1
+  for (int i = 0; i < XC; ++i) {
+    const int ch = pw + np * i;
+    const uint4 xi = xq[0], ui = uq[0], ni = nq[0];
+    // the next chunk's registers move up (a queue: the loop body only ever reads slot 0)
+#pragma unroll
+    for (int t = 0; t + 1 < XC; ++t) {
+      xq[t] = xq[t + 1];
+      if constexpr (PRO == kProSiluMul) uq[t] = uq[t + 1];
+      if constexpr (PRO == kProRms) nq[t] = nq[t + 1];
+    }
+    if (ch < p.nchunk) {  // wave-uniform
+      uint32_t a[4] = {xi.x, xi.y, xi.z, xi.w};
+      if constexpr (PRO == kProSiluMul) {  // fp16(silu(g) * u), the silu_mul arithmetic
+        const uint32_t uu[4] = {ui.x, ui.y, ui.z, ui.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          uint32_t v = 0;
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const float gv = h2f((uint16_t)(a[d] >> (16 * hh))), uv = h2f((uint16_t)(uu[d] >> (16 * hh)));
+            v |= (uint32_t)f2h(gv / (1.0f + __expf(-gv)) * uv) << (16 * hh);
+          }
+          a[d] = v;
+        }
+      }
+      if constexpr (PRO == kProRms) {  // h^2 summed in fp32; h * w rounded once to fp16
+        const uint32_t nn[4] = {ni.x, ni.y, ni.z, ni.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const float h0 = h2f((uint16_t)a[d]), h1 = h2f((uint16_t)(a[d] >> 16));
+          ssq += h0 * h0;
+          ssq += h1 * h1;
+          const float w0 = h2f((uint16_t)nn[d]), w1 = h2f((uint16_t)(nn[d] >> 16));
+          a[d] = (uint32_t)f2h(h0 * w0) | ((uint32_t)f2h(h1 * w1) << 16);
+        }
+      }
+      rf4_t d1 = {0.0f, 0.0f, 0.0f, 0.0f}, d2 = {0.0f, 0.0f, 0.0f, 0.0f};
+      if constexpr (BF) {
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rb8_t, a), __builtin_bit_cast(rb8_t, b1), d1, 0, 0, 0);
+        d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rb8_t, a), __builtin_bit_cast(rb8_t, b2), d2, 0, 0, 0);
+      } else {
+        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rh8_t, a), __builtin_bit_cast(rh8_t, b1), d1, 0, 0, 0);
+        d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rh8_t, a), __builtin_bit_cast(rh8_t, b2), d2, 0, 0, 0);
+      }
+      // lane (j, g) holds sub-blocks 4 g + r (r = 0..3) of 128-block g of the chunk; H_4
+      // across them (Sylvester order: r = the high index bits of the 128-block)
+      float lo[4], hi[4];
+      if (p.had) {
+        const float s0 = d1[0] + d1[1], s1 = d1[0] - d1[1], s2 = d1[2] + d1[3], s3 = d1[2] - d1[3];
+        lo[0] = s0 + s2; lo[1] = s1 + s3; lo[2] = s0 - s2; lo[3] = s1 - s3;
+        const float t0 = d2[0] + d2[1], t1 = d2[0] - d2[1], t2 = d2[2] + d2[3], t3 = d2[2] - d2[3];
+        hi[0] = t0 + t2; hi[1] = t1 + t3; hi[2] = t0 - t2; hi[3] = t1 - t3;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) { lo[q] = d1[q]; hi[q] = d2[q]; }
+      }
+      float mx = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) mx = fmaxf(mx, fmaxf(fabsf(lo[q]), fabsf(hi[q])));
+      mx = row16_max(mx);
+      const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
+      const int eb = (int)(bits >> 23);
+      const int E = eb == 0 ? -126 : eb - 127;  // floor(log2(mx)) for normal mx
+      int F = bits == 0 ? 0 : 14 - E;           // mx * 2^F in [2^14, 2^15)
+      F = F < -126 ? -126 : (F > 126 ? 126 : F);
+      const float f = pow2f(F);
+      const int blk = 4 * ch + g;  // global 128-block
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xpd[((jj >> 2) * Q + 4 * blk + q) * 4 + (jj & 3)] = pack_scaled(lo[q], hi[q], f);
+      if (jj == 0) xsc[blk] = pow2f(-F);
+    }
+  }
+  if constexpr (PRO == kProRms) {  // per-producer sums of h^2, fixed order
+    ssq = wave_sum(ssq);
+    if (lane == 0) ((float*)(smem + p.off_ss))[pw] = ssq;
+  }
+  // block scales (fp32) [R][K / block], bias and residual
+  if (ptid < p.R * p.cpr) {
+    float* scf = (float*)(smem + p.off_sc);
+    const uint32_t sv[4] = {r.scv.x, r.scv.y, r.scv.z, r.scv.w};
+    float4* d = (float4*)(scf + ptid * 8);
+    d[0] = make_float4(h2f((uint16_t)sv[0]), h2f((uint16_t)(sv[0] >> 16)), h2f((uint16_t)sv[1]), h2f((uint16_t)(sv[1] >> 16)));
+    d[1] = make_float4(h2f((uint16_t)sv[2]), h2f((uint16_t)(sv[2] >> 16)), h2f((uint16_t)sv[3]), h2f((uint16_t)(sv[3] >> 16)));
+  }
+  if (p.bias != nullptr && ptid < c.Rw)
+    ((float*)(smem + p.off_bias))[ptid] =
+        p.bias_dt == SPECTRA_F32 ? __builtin_bit_cast(float, r.bias_raw) : to_f32_16((uint16_t)r.bias_raw, p.bias_dt);
+  if (p.res != nullptr && ptid < c.Rw) ((uint16_t*)(smem + p.off_res))[ptid] = r.res_raw;
+}
+
+// row-wave loads: the weight runs of every slot, then the CSR entries of the group's rows
+// (lane li stages entry e0 + li of each row; lanes past the row's entries, and arrays
+// without entries, read a dummy word: entry 0, or the workgroup's first weight word)
+template <int G, int SPR, int RPG>
+struct RowRegs {
+  uint4 wq[SPR * RPG];
+  int ocol[RPG], e0r[RPG], cntr[RPG];
+  uint32_t oval[RPG];
+};
+
+template <int G, int SPR, int RPG>
+__device__ __forceinline__ void rows_row_loads(const RowsParams& p, const RowsCtx& c, const int* sx,
+                                               RowRegs<G, SPR, RPG>& r) {
+  constexpr int NS = SPR * RPG;
+  const uint8_t* wbase = p.packed + (int64_t)c.r0 * p.ldp;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int j = s / SPR, ch = s % SPR;
+    const int row = c.grow0 + j;
+    const uint32_t o = row < c.Rw ? (uint32_t)(row * p.ldp) + (uint32_t)(ch * G + c.li) * 16u : 0u;  // dummy: one line
+    r.wq[s] = load_nt_u4(wbase + o);
+  }
+  asm volatile("" ::: "memory");  // the CSR entries are issued behind every weight run
+#pragma unroll
+  for (int j = 0; j < RPG; ++j) {
+    const int a = G == 32 ? ((c.lane >> 5) ? sx[RPG + j] : sx[j]) : sx[j];
+    const int b = G == 32 ? ((c.lane >> 5) ? sx[RPG + j + 1] : sx[j + 1]) : sx[j + 1];
+    r.e0r[j] = a;
+    r.cntr[j] = c.grow0 + j < c.Rw ? b - a : 0;
+    const bool ok = p.csr && c.li < r.cntr[j];
+    const void* cb = p.csr ? (const void*)p.ccol : (const void*)wbase;
+    const void* vb = p.csr ? (const void*)p.cval : (const void*)wbase;
+    const uint32_t e = ok ? (uint32_t)(a + c.li) : 0u;
+    r.ocol[j] = load_at<int>(cb, 4u * e);
+    r.oval[j] = load_at<uint16_t>(vb, 2u * e);
+  }
+}
+
+// decode one slot's 16 packed bytes into fp16 code pairs through the LUT (lane-replicated,
+// at LDS address 0: the kernel has no static LDS, the host checks)
+__device__ __forceinline__ void rows_decode(const uint4& w, uint32_t lanebits, uint32_t (&dec)[16]) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int b = 0; b < 16; ++b) {
+    const uint32_t addr = __builtin_amdgcn_perm(wd[b >> 2], lanebits, 0x0c0c0000u | ((4u + (b & 3)) << 8));
+    dec[b] = *(const __attribute__((address_space(3))) uint32_t*)(uintptr_t)addr;
+  }
+}
+
+// one slot's dot product with the rotated activations of its run, scaled into the row's sum
+template <int G, int SPR>
+__device__ __forceinline__ float rows_dot(const RowsParams& p, const RowsCtx& c, const uint8_t* smem, int s, int j,
+                                          const uint32_t (&dec)[16]) {
+  const int Q = c.Q;
+  const uint4* xp4 = (const uint4*)(smem + p.off_xp);
+  const float* xsc = (const float*)(smem + p.off_xsc);
+  const float* scf = (const float*)(smem + p.off_sc);
+  const int q = (s % SPR) * G + c.li;
+  uint32_t xpair[16];
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    const uint4 a = xp4[cc * Q + q];
+    xpair[4 * cc] = a.x; xpair[4 * cc + 1] = a.y; xpair[4 * cc + 2] = a.z; xpair[4 * cc + 3] = a.w;
+  }
+  const float xs = xsc[q >> 2];
+  const int rowc = min(c.grow0 + j, c.Rw - 1);
+  const float am = scf[rowc * (c.K >> p.gshift) + (q >> (p.gshift - 5))];
+  float d = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, dec[b]), __builtin_bit_cast(f16x2_t, xpair[b]), d, false);
+  return d * (am * xs);
+}
+
+// the row waves' work once the weights are issued: the first NP slots are decoded as they
+// land, before the activations are ready (wait_lut / wait_x: the producers' counters; both
+// no-ops when the caller already synchronised), then the dot products, the outlier
+// products and the row totals
+template <int G, int SPR, int RPG, int NP, bool BF, int PRO, typename WL, typename WX>
+__device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& c, uint8_t* smem, int np,
+                                            RowRegs<G, SPR, RPG>& r, WL wait_lut, WX wait_x) {
+  constexpr int NS = SPR * RPG;
+  const int Q = c.Q, lane = c.lane, li = c.li;
+  const uint32_t* xpd = (const uint32_t*)(smem + p.off_xp);
+  const float* xsc = (const float*)(smem + p.off_xsc);
+  const uint32_t lanebits = (uint32_t)(lane & 31) << 2;  // this lane's LUT copy: conflict-free reads
+  float acc[RPG];
+#pragma unroll
+  for (int j = 0; j < RPG; ++j) acc[j] = 0.0f;
+  uint32_t pre[NP > 0 ? NP : 1][16];
+  wait_lut();
+#pragma unroll
+  for (int s = 0; s < NP; ++s) rows_decode(r.wq[s], lanebits, pre[s]);
+  wait_x();
+#pragma unroll
+  for (int s = 0; s < NP; ++s) acc[s / SPR] += rows_dot<G, SPR>(p, c, smem, s, s / SPR, pre[s]);
+#pragma unroll
+  for (int s = NP; s < NS; ++s) {
+    uint32_t dec[16];
+    rows_decode(r.wq[s], lanebits, dec);
+    acc[s / SPR] += rows_dot<G, SPR>(p, c, smem, s, s / SPR, dec);
+  }
+  // outliers: entry value x rotated activation, into the row's lanes
+  if (p.csr) {
+    const uint16_t* xp16 = (const uint16_t*)xpd;
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+      const int cnt = r.cntr[j];
+      int col = r.ocol[j];
+      uint32_t ov = r.oval[j];
+      asm volatile("" : "+v"(col), "+v"(ov)::"memory");  // consumed here, after the stream
+      if (li < cnt) acc[j] += h2f((uint16_t)ov) * (h2f(xp16[xs_pos(col, p.marlin, Q)]) * xsc[col >> 7]);
+      // entries beyond one per lane (rare): read from the side tensor
+      for (int el = G + li; el < cnt; el += G) {
+        const int cl = p.ccol[r.e0r[j] + el];
+        acc[j] += h2f(p.cval[r.e0r[j] + el]) * (h2f(xp16[xs_pos(cl, p.marlin, Q)]) * xsc[cl >> 7]);
+      }
+    }
+  }
+  // row totals: one butterfly sum per row, lane 0 of the group stores
+  float inv = 1.0f;  // kProRms: rsqrt(mean(h^2) + eps)
+  if constexpr (PRO == kProRms) {
+    const float* ss = (const float*)(smem + p.off_ss);
+    float t = 0.0f;
+    for (int w = 0; w < np; ++w) t += ss[w];
+    inv = 1.0f / sqrtf(t / (float)c.K + p.eps);
+  }
+  constexpr int odt = BF ? SPECTRA_BF16 : SPECTRA_F16;
+  const float* bl = (const float*)(smem + p.off_bias);
+  const uint16_t* rsl = (const uint16_t*)(smem + p.off_res);
+#pragma unroll
+  for (int j = 0; j < RPG; ++j) {
+    const float v = group_sum<G>(acc[j], lane);
+    const int row = c.grow0 + j;
+    if (li == 0 && row < c.Rw) {
+      float y = v * p.out_scale;
+      if constexpr (PRO == kProRms) y *= inv;
+      if (p.bias != nullptr) y += bl[row];
+      if (p.res != nullptr) y = to_f32_16(from_f32_16(y, odt), odt) + to_f32_16(rsl[row], odt);
+      ((uint16_t*)p.out)[c.r0 + row] = from_f32_16(y, odt);
+    }
+  }
+}
+
+template <int G, int SPR, int RPG, int XC, bool BF, int PRO, bool SPLIT>
+__global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  constexpr int RW = RPG * (64 / G);  // rows per wave
+  constexpr int NS = SPR * RPG;
+  constexpr int NP = NS <= 4 ? NS : NS <= 8 ? 2 : 0;  // slots decoded before the activations are ready
+  const int tid = threadIdx.x;
+  const int W = (int)(blockDim.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int np = SPLIT ? W - p.wr : W;  // producer waves
+  // producers are waves 0 .. np - 1 (dispatched first), row waves np .. W - 1
+  const int rtid = SPLIT ? tid - 64 * np : tid;  // thread index among the row waves
+  RowsCtx c;
+  c.tid = tid;
+  c.lane = tid & 63;
+  c.wave = wave;
+  c.W = W;
+  c.K = p.k;
+  c.Q = p.k >> 5;
+  c.r0 = blockIdx.x * p.R;
+  c.Rw = min(p.R, p.n - c.r0);
+  c.gi = rtid / G;
+  c.li = rtid % G;
+  c.grow0 = c.gi * RPG;  // this group's first row inside the workgroup
+  // every argument the issue phase needs, fetched in one round trip before the first load
+  asm volatile("" ::"s"(p.x), "s"(p.packed), "s"(p.ldp), "s"(p.absmax), "s"(p.lda), "s"(p.csr), "s"(p.rowptr),
+               "s"(p.bias), "s"(p.res), "s"(p.bias_dt), "s"(p.nchunk), "s"(p.cpr), "s"(p.cmagic), "s"(p.wr));
+  uint32_t* counter = (uint32_t*)(smem + p.off_flag);  // [0]: LUT rows built, [1]: producers done
+  const int rwave = SPLIT ? wave - np : wave;          // row-wave index
+
+  if constexpr (SPLIT) {
+    if (wave < np) {
+      // ---------------- producer waves ----------------
+      ProducerRegs<XC, PRO> pr;
+      rows_producer_loads<XC, PRO>(p, c, wave, np, tid, pr);
+      __syncthreads();  // --- start barrier: counters zeroed; activation requests precede the weight runs
+      __builtin_amdgcn_s_setprio(3);  // the producers are the critical path of the workgroup
+      build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, np, c.lane);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // LDS operations of a wave complete in order
+      if (c.lane == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      rows_rotate<XC, BF, PRO>(p, c, smem, wave, np, tid, pr);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (c.lane == 0) __hip_atomic_fetch_add(counter + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      return;
+    }
+    // ---------------- row waves ----------------
+    int sx[RW + 1];  // CSR extents of the wave's rows: scalar loads, issued first
+    if (p.csr) {
+      const __attribute__((address_space(4))) int32_t* rpc = (const __attribute__((address_space(4))) int32_t*)p.rowptr;
+#pragma unroll
+      for (int j = 0; j <= RW; ++j) sx[j] = rpc[min(c.r0 + rwave * RW + j, p.n)];
+    } else {
+#pragma unroll
+      for (int j = 0; j <= RW; ++j) sx[j] = 0;
+    }
+    if (tid == 64 * np) {
+      counter[0] = 0u;
+      counter[1] = 0u;
+    }
+    __syncthreads();  // --- start barrier
+    RowRegs<G, SPR, RPG> rr;
+    rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
+    // waits on the producers' counters (bounded: an unfinished count yields wrong output,
+    // never a hang)
+    auto wait_for = [&](int which) {
+      for (int it = 0; it < kRowsSpinLimit; ++it) {
+        if (__hip_atomic_load(counter + which, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= (uint32_t)np) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      asm volatile("" ::: "memory");
+    };
+    rows_stream<G, SPR, RPG, NP, BF, PRO>(p, c, smem, np, rr, [&] { wait_for(0); }, [&] { wait_for(1); });
+  } else {
+    // every wave loads and produces, then streams its rows
+    int sx[RW + 1];
+    if (p.csr) {
+      const __attribute__((address_space(4))) int32_t* rpc = (const __attribute__((address_space(4))) int32_t*)p.rowptr;
+#pragma unroll
+      for (int j = 0; j <= RW; ++j) sx[j] = rpc[min(c.r0 + wave * RW + j, p.n)];
+    } else {
+#pragma unroll
+      for (int j = 0; j <= RW; ++j) sx[j] = 0;
+    }
+    ProducerRegs<XC, PRO> pr;
+    rows_producer_loads<XC, PRO>(p, c, wave, W, tid, pr);
+    RowRegs<G, SPR, RPG> rr;
+    rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
+    build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, W, c.lane);
+    rows_rotate<XC, BF, PRO>(p, c, smem, wave, W, tid, pr);
+    __syncthreads();  // --- LUT, activation pairs, scales
+    if (wave * RW >= c.Rw) {  // a wave without rows (it only helped with the activations)
+      __builtin_amdgcn_s_waitcnt(0);  // its dummy loads land before it ends
+      return;
+    }
+    rows_stream<G, SPR, RPG, 0, BF, PRO>(p, c, smem, W, rr, [] {}, [] {});
+  }
+}
+
+typedef void (*gemv_rows_fn)(const RowsParams);
+
+}  // namespace spectra
