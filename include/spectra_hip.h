@@ -267,7 +267,7 @@ int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t tokens, const in
  * appends k and v at *pos to k_cache / v_cache [kv_heads, max_seq, head_dim], and writes
  * out [heads, head_dim] fp16 = softmax(q k^T / sqrt(head_dim)) v over positions [0, *pos]
  * (fp32 softmax; grouped-query: query head h reads KV head h / (heads / kv_heads); 1, 2, 3,
- * 4, 6 or 8 query heads per KV head; head_dim 64, 128 or 256; operands 16-byte aligned).
+ * 4, 6 or 8 query heads per KV head; head_dim 16, 32, 64, 128 or 256; operands 16-byte aligned).
  * Two kernels: spectra_attend_spans(max_seq) spans of 64 positions per KV head, then a
  * log-sum-exp merge.  workspace: >= spectra_attend_workspace(heads, head_dim, max_seq)
  * bytes, 16-byte aligned (span partials); calls sharing a workspace must not overlap. */
@@ -291,7 +291,7 @@ int spectra_attend_decode(const void* qkv, const int64_t* pos, const float* cos_
  * appended), the last `window` positions also in fp16 rings k_window / v_window
  * [kv_heads, window, head_dim] (slot = position % window), which attention reads for them
  * (the reference keeps a recent window unquantized); older positions are read through the
- * dequant.  RoPE tables required. */
+ * dequant.  RoPE tables required; head_dim 32, 64, 128 or 256 (groups of 32 dims). */
 int spectra_kv4_quantize(const void* x, int64_t ldx, int64_t rows, int32_t heads, int64_t x_head_stride, int32_t d,
                          void* codes, void* scales, void* zeros, int64_t out_head_rows, spectra_stream_t stream);
 int spectra_kv4_dequantize(const void* codes, const void* scales, const void* zeros, int64_t rows, int32_t d,

@@ -277,14 +277,18 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
                                                               float* __restrict__ part) {
   const int lmax = kvc.lmax;
   constexpr int DG = HD / 8;               // lanes per position
-  constexpr int PPW = kDecThreads / DG;    // positions per pass
+  // positions per pass: at HD 16 the workgroup has more position rows than the span has
+  // positions, and the threads of rows >= kSpanMax only take part in the reductions (zeros)
+  constexpr int PPW = kDecThreads / DG < kSpanMax ? kDecThreads / DG : kSpanMax;
   constexpr int NP = kSpanMax / PPW;       // passes
   constexpr int H2 = HD / 2;
+  static_assert(HD % 16 == 0 && (!Q4 || HD % 32 == 0), "head_dim: a multiple of 16 (of 32 for the 4-bit cache)");
   __shared__ float sc[G][kSpanMax];        // scores, then exponentials
   __shared__ float wsum[4][G][HD];         // V sums of the four waves
   const int kh = blockIdx.x, sp = blockIdx.y, nspan = gridDim.y, tid = threadIdx.x;
   const int t0 = sp * kSpanMax;
   const int dg = tid % DG, pr = tid / DG;
+  const bool act = pr < PPW;  // a position row of the span
   // fp16 cache: the span's K / V rows first, at addresses independent of the position (rows
   // clamped into the cache; those past the position are masked below), so they are in
   // flight while the position arrives (a scalar load)
@@ -416,7 +420,7 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
 #pragma unroll
       for (int e = 0; e < 8; ++e) d += qf[j][e] * kf[e];
       d = group_sum<DG>(d);
-      if (dg == 0) sc[j][pr + i * PPW] = d * scale;
+      if (dg == 0 && act) sc[j][pr + i * PPW] = d * scale;
     }
   }
   __syncthreads();
@@ -449,7 +453,7 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
     else kv4_dequant_chunk(vr[i].x, vr[i].y, vf);
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      const float pw = sc[j][pr + i * PPW];  // 0 past the end
+      const float pw = act ? sc[j][pr + i * PPW] : 0.0f;  // 0 past the end
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[j][e] += pw * vf[e];
     }
@@ -707,8 +711,14 @@ static attend_fn pick_attend(int g) {
 
 template <bool ROPE, bool Q4>
 static attend_fn pick_attend_hd(int hd, int g) {
-  return hd == 64 ? pick_attend<64, ROPE, Q4>(g) : hd == 128 ? pick_attend<128, ROPE, Q4>(g)
-                                                             : pick_attend<256, ROPE, Q4>(g);
+  switch (hd) {
+    case 16: if constexpr (Q4) return nullptr; else return pick_attend<16, ROPE, Q4>(g);
+    case 32: return pick_attend<32, ROPE, Q4>(g);
+    case 64: return pick_attend<64, ROPE, Q4>(g);
+    case 128: return pick_attend<128, ROPE, Q4>(g);
+    case 256: return pick_attend<256, ROPE, Q4>(g);
+    default: return nullptr;
+  }
 }
 
 static int attend_launch(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t, int32_t heads,
@@ -717,7 +727,9 @@ static int attend_launch(const void* qkv, const int64_t* pos, const float* cos_t
   SPECTRA_REQUIRE(qkv && pos && kvc.k && kvc.v && out, "NULL pointer");
   SPECTRA_REQUIRE((cos_t == nullptr) == (sin_t == nullptr), "cos and sin must both be given or both be NULL");
   SPECTRA_REQUIRE(heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0, "heads must be a multiple of kv_heads");
-  SPECTRA_REQUIRE(head_dim == 64 || head_dim == 128 || head_dim == 256, "head_dim must be 64, 128 or 256");
+  SPECTRA_REQUIRE(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 || head_dim == 256,
+                  "head_dim must be 16, 32, 64, 128 or 256");
+  SPECTRA_REQUIRE(!q4 || head_dim >= 32, "the 4-bit cache needs head_dim >= 32 (groups of 32 dims)");
   SPECTRA_REQUIRE(kvc.lmax >= 1 && kvc.lmax <= (1 << 20), "bad max_seq");
   SPECTRA_REQUIRE(aligned16(qkv) && aligned16(kvc.k) && aligned16(kvc.v) &&
                       (cos_t == nullptr || (aligned16(cos_t) && aligned16(sin_t))),

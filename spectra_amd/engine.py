@@ -219,8 +219,9 @@ def _synthetic_nf4(n: int, k: int, gen: torch.Generator, had: int, ratio: float,
 
 
 class SpectraDecoder(nn.Module):
-    """Batch-1 Llama-shaped decoder whose every linear is a Format B ``SpectraFusedLinear``
-    (fused QKV and gate_up per layer, engine.py:409-437), with a tied quantized embedding /
+    """Batch-1 Llama-shaped decoder whose every linear is a ``SpectraFusedLinear`` -- Format
+    B (fused QKV and gate_up per layer, engine.py:409-437) or Format A (the container's
+    separate projections, engine.py:1004-1025) -- with a tied quantized embedding /
     lm_head (engine.py:1124-1168) and an fp16 KV cache.  Between the linears a layer runs
     the library's fused kernels (residual add + RMSNorm, RoPE + cache append, split-sequence
     decode attention, SiLU-mul) where the reference relies on Inductor fusion
@@ -231,8 +232,10 @@ class SpectraDecoder(nn.Module):
     def __init__(self, cfg: DecoderConfig = DecoderConfig(), device: Optional[torch.device] = None,
                  weights: Optional[dict] = None):
         """``weights`` (default: random init from ``cfg.seed``): ``layers`` = per layer
-        (qkv, o, gate_up, down) ``NF4Weight``s, ``embed`` (the gather's rows, no rotation),
-        ``lm_head`` (None = tied to ``embed``), ``norms`` = the 2 * layers + 1 RMSNorm weights."""
+        (qkv, o, gate_up, down) ``NF4Weight``s or ``FormatAWeight``s -- qkv and gate_up may
+        also be lists of the parts (q, k, v / gate, up) -- ``embed`` (the gather's rows, no
+        rotation), ``lm_head`` (None = tied to ``embed``), ``norms`` = the 2 * layers + 1
+        RMSNorm weights."""
         super().__init__()
         dev = device or torch.device("cuda")
         self.cfg = cfg
@@ -243,23 +246,45 @@ class SpectraDecoder(nn.Module):
         if len(weights["layers"]) != c.layers or len(weights["norms"]) != 2 * c.layers + 1:
             raise ValueError("weights do not match the config's layer count")
 
+        from .container import FormatAWeight
+
         def linear(q):
+            if isinstance(q, FormatAWeight):  # engine.py:1004-1025: group 32, no rotation
+                lin = SpectraFusedLinear(q.k, q.n, 32, marlin_layout=q.marlin_layout).to(dev)
+                lin.set_weights(q.packed, q.scales, q.zeros, outlier_idx=q.outlier_idx, outlier_weight=q.outlier_w,
+                                marlin_layout=q.marlin_layout)
+                return lin
             lin = SpectraFusedLinear(q.k, q.n, q.blocksize, codebook="nf4", hadamard_block=q.hadamard_block).to(dev)
             col, val = q.outliers()
             lin.set_weights(q.packed, q.absmax, None, outlier_idx=col, outlier_weight=val, marlin_layout=q.marlin_layout,
                             outlier_rowptr=q.rowptr if col is not None else None)
             return lin
 
+        def parts(q):  # a weight, or the parts of one concatenated along N
+            return list(q) if isinstance(q, (list, tuple)) else [q]
+
         self.layers_q = [tuple(weights["layers"][i]) for i in range(c.layers)]
-        self.blocks = [dict(qkv=linear(a), o=linear(b), gate_up=linear(g), down=linear(d)) for a, b, g, d in self.layers_q]
+        # qkv / gate_up: the parts' linears, each writing its columns of the fused output
+        self.blocks = [dict(qkv=[linear(p) for p in parts(a)], o=linear(b), gate_up=[linear(p) for p in parts(g)],
+                            down=linear(d)) for a, b, g, d in self.layers_q]
         qe = weights["embed"]
         self.embed_q = qe
-        col, val = qe.outliers()
-        self.embed = SpectraFusedEmbedding(c.vocab, c.hidden, qe.blocksize, qe.marlin_layout, codebook="nf4")
-        self.embed.set_weights(qe.packed, qe.absmax, None, col, val, qe.marlin_layout,
-                               outlier_rowptr=qe.rowptr if col is not None else None)
+        if isinstance(qe, FormatAWeight):
+            self.embed = SpectraFusedEmbedding(c.vocab, c.hidden, 32, qe.marlin_layout)
+            self.embed.set_weights(qe.packed, qe.scales, qe.zeros, qe.outlier_idx, qe.outlier_w, qe.marlin_layout)
+        else:
+            col, val = qe.outliers()
+            self.embed = SpectraFusedEmbedding(c.vocab, c.hidden, qe.blocksize, qe.marlin_layout, codebook="nf4")
+            self.embed.set_weights(qe.packed, qe.absmax, None, col, val, qe.marlin_layout,
+                                   outlier_rowptr=qe.rowptr if col is not None else None)
         self.lm_q = weights.get("lm_head") or qe
         self.lm_head = linear(self.lm_q)
+        # the fused decode step (RMSNorm / SiLU-mul prologues, one GEMV per fused projection)
+        # needs NF4 linears throughout; otherwise the step runs the norms and SiLU-mul as
+        # their own kernels and one GEMV per part
+        self.fused = all(len(b["qkv"]) == 1 and len(b["gate_up"]) == 1 for b in self.blocks) and all(
+            lin.codebook == "nf4" for b in self.blocks for lin in b["qkv"] + b["gate_up"] + [b["o"], b["down"]]) and \
+            self.lm_head.codebook == "nf4"
         self.norm_w = [w.to(device=dev, dtype=torch.float32).contiguous() for w in weights["norms"]]
         self.norm_w16 = [w.half() for w in self.norm_w]  # the fused GEMV prologues read fp16 weights
         # KV cache [layer, kv, max_seq, head_dim]: a position's head is one 16-byte-aligned run
@@ -310,30 +335,39 @@ class SpectraDecoder(nn.Module):
 
     @classmethod
     def from_trdc(cls, path, device: Optional[torch.device] = None, max_seq: int = 1024) -> "SpectraDecoder":
-        """A decoder on the Format B tensors of a TRDC container (engine.py:798-1080 binds a
-        container's tensors to the model's modules by name): HF Llama names, the separate
-        q/k/v and gate/up projections concatenated along N at load (exact: every Format B
-        operand is row-local), norms from the lossless tensors, lm_head tied to the
-        embedding when the container has none."""
-        from .container import TrdcReader, nf4_concat
+        """A decoder on the quantized tensors of a TRDC container (engine.py:798-1080 binds a
+        container's tensors to the model's modules by name): HF Llama names, norms from the
+        lossless tensors, lm_head tied to the embedding when the container has none.
+        Format B (``nf4_*``) q/k/v and gate/up are concatenated along N at load (exact: every
+        Format B operand is row-local); Format A (``q4_g32_hdsq``) parts stay separate
+        linears, since their dense outlier columns are per tensor."""
+        from .compressor import NF4Weight
+        from .container import FORMAT_A, TrdcReader, nf4_concat
         dev = device or torch.device("cuda")
         with TrdcReader(path) as rd:
             cf = rd.config
+            rp = cf.get("rope_parameters") or {}
+            theta = cf.get("rope_theta") or rp.get("rope_theta") or 10000.0
             c = DecoderConfig(layers=cf["num_hidden_layers"], hidden=cf["hidden_size"],
                               heads=cf["num_attention_heads"],
                               kv_heads=cf.get("num_key_value_heads") or cf["num_attention_heads"],
                               inter=cf["intermediate_size"], vocab=cf["vocab_size"],
-                              rope_theta=float(cf.get("rope_theta") or 10000.0),
+                              rope_theta=float(theta),
                               rms_eps=float(cf.get("rms_norm_eps") or 1e-6), max_seq=max_seq)
             if cf.get("head_dim") not in (None, c.head_dim):
                 raise ValueError(f"head_dim {cf.get('head_dim')} != hidden / heads ({c.head_dim})")
 
-            def nf4(name):
+            def q4(name):
                 if name not in rd.tensors:
                     raise ValueError(f"container has no tensor {name!r}")
-                if not rd.tensors[name]["type"].startswith("nf4_"):
-                    raise ValueError(f"{name!r} is {rd.tensors[name]['type']!r}: the decoder runs Format B tensors")
+                t = rd.tensors[name]["type"]
+                if not (t.startswith("nf4_") or t in (FORMAT_A, "q4_g32")):
+                    raise ValueError(f"{name!r} is {t!r}: the decoder runs 4-bit quantized tensors")
                 return rd.load(name, dev)
+
+            def fuse(names):
+                ws = [q4(n) for n in names]
+                return nf4_concat(ws) if all(isinstance(w, NF4Weight) for w in ws) else ws
 
             def vec(name):
                 return rd.load(name, dev).float()
@@ -343,14 +377,14 @@ class SpectraDecoder(nn.Module):
                 p = f"model.layers.{i}."
                 a = p + "self_attn."
                 m = p + "mlp."
-                layers.append((nf4_concat([nf4(a + "q_proj.weight"), nf4(a + "k_proj.weight"), nf4(a + "v_proj.weight")]),
-                               nf4(a + "o_proj.weight"),
-                               nf4_concat([nf4(m + "gate_proj.weight"), nf4(m + "up_proj.weight")]),
-                               nf4(m + "down_proj.weight")))
+                layers.append((fuse([a + "q_proj.weight", a + "k_proj.weight", a + "v_proj.weight"]),
+                               q4(a + "o_proj.weight"),
+                               fuse([m + "gate_proj.weight", m + "up_proj.weight"]),
+                               q4(m + "down_proj.weight")))
                 norms += [vec(p + "input_layernorm.weight"), vec(p + "post_attention_layernorm.weight")]
             norms.append(vec("model.norm.weight"))
-            embed = nf4("model.embed_tokens.weight")
-            head = nf4("lm_head.weight") if "lm_head.weight" in rd.tensors else None
+            embed = q4("model.embed_tokens.weight")
+            head = q4("lm_head.weight") if "lm_head.weight" in rd.tensors else None
         return cls(c, dev, dict(layers=layers, embed=embed, lm_head=head, norms=norms))
 
     # -- building blocks ---------------------------------------------------------------------
@@ -363,7 +397,7 @@ class SpectraDecoder(nn.Module):
         hd, T = c.head_dim, h.shape[0]
         g = c.heads // c.kv_heads
         x = rmsnorm(h, self.norm_w[2 * li], c.rms_eps, residual=delta)
-        qkv = blk["qkv"](x)
+        qkv = self._project(blk["qkv"], x)
         L = causal_len
         if c.kv_bits == 16:
             kc, vc = self.k_cache[li], self.v_cache[li]
@@ -391,15 +425,37 @@ class SpectraDecoder(nn.Module):
         a = a.reshape(c.heads, T, hd).permute(1, 0, 2).reshape(T, c.hidden)
         o = blk["o"](a)
         x = rmsnorm(h, self.norm_w[2 * li + 1], c.rms_eps, residual=o)
-        return blk["down"](silu_mul(blk["gate_up"](x)))
+        return blk["down"](silu_mul(self._project(blk["gate_up"], x)))
+
+    @staticmethod
+    def _project(parts, x: torch.Tensor) -> torch.Tensor:
+        """The fused projection of ``x`` through the parts' linears (columns in part order)."""
+        if len(parts) == 1:
+            return parts[0](x)
+        return torch.cat([p(x) for p in parts], dim=-1)
+
+    @staticmethod
+    def _gemv_parts(parts, x: torch.Tensor) -> torch.Tensor:
+        """One-row ``_project``: each part's GEMV writes its columns of one output row."""
+        out = torch.empty((1, sum(p.out_features for p in parts)), device=x.device, dtype=torch.float16)
+        off = 0
+        for p in parts:
+            w4a16_gemv_fused(p._operands(), x, out=out[:, off: off + p.out_features])
+            off += p.out_features
+        return out
 
     def _layer_decode(self, li: int, h: torch.Tensor, pos: torch.Tensor) -> None:
         """One decoder layer for the token at device position ``pos``, six kernels: the
         RMSNorms ride in the QKV / gate_up GEMV prologues, SiLU-mul in the down_proj prologue,
-        the residual adds in the o_proj / down_proj epilogues (``h`` updated in place)."""
+        the residual adds in the o_proj / down_proj epilogues (``h`` updated in place).
+        Without NF4 linears throughout (``fused`` False) the norms and SiLU-mul are kernels
+        of their own and each part of QKV / gate_up its own GEMV."""
         c, blk = self.cfg, self.blocks[li]
-        qkv = w4a16_gemv_fused(blk["qkv"]._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[2 * li],
-                               eps=c.rms_eps)
+        if self.fused:
+            qkv = w4a16_gemv_fused(blk["qkv"][0]._operands(), h, prologue="rmsnorm",
+                                   norm_weight=self.norm_w16[2 * li], eps=c.rms_eps)
+        else:
+            qkv = self._gemv_parts(blk["qkv"], rmsnorm(h, self.norm_w[2 * li], c.rms_eps))
         if c.kv_bits == 16:
             a = attend_decode(qkv, pos, self.cos, self.sin, c.heads, c.kv_heads, self.k_cache[li], self.v_cache[li],
                               self.attn_ws)
@@ -408,9 +464,13 @@ class SpectraDecoder(nn.Module):
                                  self.v_cache[li], tuple(t[li] for t in self.k4), tuple(t[li] for t in self.v4),
                                  self.attn_ws)
         w4a16_gemv_fused(blk["o"]._operands(), a.reshape(1, c.hidden), residual=h, out=h)
-        gu = w4a16_gemv_fused(blk["gate_up"]._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[2 * li + 1],
-                              eps=c.rms_eps)
-        w4a16_gemv_fused(blk["down"]._operands(), gu, prologue="silu_mul", residual=h, out=h)
+        if self.fused:
+            gu = w4a16_gemv_fused(blk["gate_up"][0]._operands(), h, prologue="rmsnorm",
+                                  norm_weight=self.norm_w16[2 * li + 1], eps=c.rms_eps)
+            w4a16_gemv_fused(blk["down"]._operands(), gu, prologue="silu_mul", residual=h, out=h)
+        else:
+            gu = self._gemv_parts(blk["gate_up"], rmsnorm(h, self.norm_w[2 * li + 1], c.rms_eps))
+            w4a16_gemv_fused(blk["down"]._operands(), silu_mul(gu), residual=h, out=h)
 
     def forward_tokens(self, ids: torch.Tensor, pos: torch.Tensor, causal_len: Optional[int]) -> torch.Tensor:
         h = self.embed(ids)
@@ -418,6 +478,8 @@ class SpectraDecoder(nn.Module):
         if causal_len is None:  # decode: one token, fused GEMVs
             for li in range(c.layers):
                 self._layer_decode(li, h, pos)
+            if not self.fused:
+                return w4a16_gemv_fused(self.lm_head._operands(), rmsnorm(h, self.norm_w[-1], c.rms_eps))
             return w4a16_gemv_fused(self.lm_head._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[-1],
                                     eps=c.rms_eps)
         delta = None

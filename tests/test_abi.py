@@ -111,7 +111,11 @@ def test_decode_kernels_reject_bad_arguments():
     assert lib.spectra_attend_workspace(24, 128, 1000) == 24 * 16 * 130 * 4
     args = (p, p, p, p)
     assert lib.spectra_attend_decode(*args, 24, 8, 128, 1024, p, p, None, 0, p, None) == L.ERR_WORKSPACE
-    assert lib.spectra_attend_decode(*args, 24, 8, 32, 1024, p, p, p, 1 << 20, p, None) == L.ERR_INVALID
+    assert lib.spectra_attend_decode(*args, 24, 8, 48, 1024, p, p, p, 1 << 20, p, None) == L.ERR_INVALID
+    # the 4-bit cache quantizes groups of 32 dims: head_dim 16 is refused before any launch
+    assert lib.spectra_attend_decode_q4(*args, 4, 2, 16, 64, 16, p, p, p, p, p, p, p, p, p, 1 << 20, p,
+                                        None) == L.ERR_INVALID
+    assert "head_dim" in lib.spectra_last_error().decode()
     assert lib.spectra_attend_decode(*args, 40, 8, 128, 1024, p, p, p, 1 << 24, p, None) == L.ERR_UNSUPPORTED
     assert lib.spectra_attend_decode(*args, 24, 8, 96, 1024, p, p, p, 1 << 24, p, None) == L.ERR_INVALID
     assert lib.spectra_attend_decode(p, p, p, None, 24, 8, 128, 1024, p, p, p, 1 << 24, p, None) == L.ERR_INVALID

@@ -251,3 +251,64 @@ def test_nf4_container_roundtrip_and_decoder(hip, tmp_path, monkeypatch):
         assert (dec.graph_logits.float() - lr).abs().max().item() <= 1e-2 * lr.abs().max().item()
         toks.append(int(torch.argmax(lr)))
         assert int(dec.cur_id) == toks[-1]
+
+
+def _format_a_w_eff(q, dtype="float32"):
+    """W_eff of a Format A tensor: (q - z) * s, then the outlier columns (oracle dequant)."""
+    w = O.dequant_group32(q.packed.cpu().numpy(), q.scales.cpu().numpy(), q.zeros.cpu().numpy(), q.marlin_layout,
+                          dtype)
+    if q.outlier_idx is not None:
+        w = O.apply_outlier_columns(w, q.outlier_idx.cpu().numpy(), q.outlier_w.cpu().numpy(), dtype)
+    return torch.from_numpy(np.ascontiguousarray(w)).float().cuda()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("source", ["reference_golden", "compressor"])
+def test_format_a_container_decoder(hip, tmp_path, monkeypatch, source):
+    """A Format A (q4_g32_hdsq) container drives the decoder (engine.py:1004-1025 binds its
+    tensors): q/k/v and gate/up stay separate Format A linears (the MFMA GEMM over the
+    prompt, one GEMV per part in the captured decode step), the embedding gathers Format A
+    rows and the tied lm_head is a Format A GEMV.  ``reference_golden`` is the file the
+    reference's compressor wrote (head_dim 16); ``compressor`` is this package's compressor
+    on a hidden-256 checkpoint (head_dim 64).  Against the fp32 restatement on the oracle's
+    W_eff (the embedding rows in fp16, as the gather returns them): logits within 1e-2 of the
+    logit scale, the greedy token the restatement's unless its top two are within that."""
+    from oracle import torch_ref as TR
+    from spectra_amd.engine import SpectraDecoder
+    from test_decoder import _greedy_consistent
+
+    if source == "reference_golden":
+        path = GOLDEN
+    else:
+        import golden.make_trdc_golden as G
+        monkeypatch.setattr(G, "TINY", DEC)
+        ck = tmp_path / "ck"
+        make_checkpoint(str(ck), seed=5)
+        path = tmp_path / "a.trdc"
+        T.compress_checkpoint(ck, path, fmt="q4_g32")
+    dec = SpectraDecoder.from_trdc(path, max_seq=64)
+    c = dec.cfg
+    assert not dec.fused and dec.lm_q is dec.embed_q and len(dec.blocks[0]["qkv"]) == 3
+    assert c.head_dim == (16 if source == "reference_golden" else 64)
+    layers = [[torch.cat([_format_a_w_eff(p) for p in (q if isinstance(q, list) else [q])]) for q in layer]
+              for layer in dec.layers_q]
+    ref = TR.Decoder(layers, [[0, 0, 0, 0]] * c.layers, [w.float() for w in dec.norm_w],
+                     _format_a_w_eff(dec.embed_q, "float16"), _format_a_w_eff(dec.lm_q), heads=c.heads,
+                     kv_heads=c.kv_heads, rope_theta=c.rope_theta, rms_eps=c.rms_eps, max_seq=c.max_seq)
+    prompt = torch.randint(0, c.vocab, (7,), generator=torch.Generator().manual_seed(2)).cuda()
+    print("case: source", source, "prefill", flush=True)
+    lg = dec.prefill(prompt).float()
+    lr = ref.forward(prompt, 0)
+    tol = 1e-2 * lr.abs().max().item()
+    assert (lg - lr).abs().max().item() <= tol
+    _greedy_consistent(int(dec.cur_id), lr, tol)
+    dec.capture_decode()
+    for step in range(6):
+        print("case: source", source, "decode step", step, flush=True)
+        tok = int(dec.cur_id)
+        dec.graph.replay()
+        lr = ref.forward(torch.tensor([tok], device="cuda"), prompt.numel() + step)
+        tol = 1e-2 * lr.abs().max().item()
+        assert (dec.graph_logits.float() - lr).abs().max().item() <= tol, step
+        _greedy_consistent(int(dec.cur_id), lr, tol)
+        assert int(dec.cur_pos) == prompt.numel() + step + 1

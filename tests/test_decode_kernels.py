@@ -85,7 +85,8 @@ def _tables(L, hd):
 
 
 @pytest.mark.parametrize("heads,kv,hd,L", [(24, 8, 128, 768), (4, 4, 64, 1000), (8, 2, 256, 130), (6, 3, 64, 64),
-                                           (32, 4, 128, 300), (12, 2, 64, 200), (24, 8, 128, 1100)])
+                                           (32, 4, 128, 300), (12, 2, 64, 200), (24, 8, 128, 1100),
+                                           (4, 2, 16, 128), (4, 2, 16, 70), (8, 4, 32, 150)])
 @pytest.mark.parametrize("rope", [True, False])
 def test_attend_decode(hip, heads, kv, hd, L, rope):
     g = torch.Generator(device="cuda").manual_seed(heads * L + rope)
@@ -313,7 +314,8 @@ def test_kv4_quantize_and_dequant_reference_vectors(hip, name):
     assert np.array_equal(deq.cpu().view(torch.int16).numpy(), g[name + "_deq"])
 
 
-@pytest.mark.parametrize("heads,kv,hd,L,W", [(24, 8, 128, 300, 128), (8, 2, 64, 200, 16), (6, 3, 256, 130, 64)])
+@pytest.mark.parametrize("heads,kv,hd,L,W", [(24, 8, 128, 300, 128), (8, 2, 64, 200, 16), (6, 3, 256, 130, 64),
+                                              (8, 4, 32, 100, 16)])
 def test_attend_decode_q4(hip, heads, kv, hd, L, W):
     import oracle as O
     g = torch.Generator(device="cuda").manual_seed(heads + L)
