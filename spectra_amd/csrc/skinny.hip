@@ -19,7 +19,8 @@
 //    MFMAs of a block accumulate from zero; the block's absmax scales them into the
 //    running fp32 sum (exact codes, one fp32 scale per block, as W_eff defines it up to
 //    the fp32 summation order).  Waves meet in LDS in a fixed order (deterministic);
-//    CSR outliers are staged in LDS and added per output in entry order.
+//    CSR outliers are staged in LDS; each output's entries are summed in parts by
+//    adjacent lanes that meet in a fixed butterfly order.
 #include <cmath>
 
 #include "common.h"
@@ -247,7 +248,7 @@ struct SkinnyParams {
   void* out;
   int64_t ldo;
   int m, mp, n, k, nchunks, nrounds, csr_nnz, okind, bias_dt, act_dt, ecap;
-  uint32_t off_rp, off_bias, off_xe, off_ve, off_sums;
+  uint32_t off_rp, off_bias, off_fx, off_xe, off_ve, off_sums, off_csum;
 };
 
 template <int T, int CPW>
@@ -273,6 +274,8 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
   // lanes 0/1: the workgroup's first / end CSR row pointer (packed bytes when no CSR)
   const int rpe = *(csr ? p.rowptr + r0 + (lane == 1 ? Rw : 0) : (const int32_t*)p.packed);
   const int rp_v = *(csr ? p.rowptr + r0 + min(tid, Rw) : (const int32_t*)p.packed);
+  // the activation rows' exponents (lanes m < M), stored to LDS in the tail
+  const int32_t fx_reg = p.fexp[min(tid, p.m - 1)];
   uint32_t bias_raw = 0;
   if (p.bias != nullptr) {
     const int64_t bi = r0 + (tid < Rw ? tid : 0);
@@ -387,7 +390,29 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
     }
   }
 
-  // ---- (6) wave partials -> LDS (the LUT is dead once every wave has streamed) ----
+  // ---- (6) CSR staging loads first (their latency runs under the barrier below): the mp
+  //      activations of each of this thread's four entries' columns (k-major copy), every
+  //      lane loading from an in-bounds address; the stores to LDS are predicated ----
+  const int e_stage = csr ? min(min(e1, e0 + p.ecap), p.csr_nnz & ~3) : 0;
+  const int g4 = (e0 & ~3) + 4 * tid;
+  // Two 16-byte loads per entry whatever the row count (no branches between the loads and
+  // the stores, whose register moves would wait for the loads): mp = 16 reads the column's
+  // 32 bytes; mp = 8 its 16 bytes twice; mp = 4 the aligned 16 bytes holding the column
+  // and its even/odd neighbour (K is even, so both are in the tensor).  Without CSR the
+  // loads re-read the first 32 bytes of the k-major copy and nothing is stored.
+  auto gload = [&](int c, uint4& a, uint4& b) __attribute__((always_inline)) {
+    const uint32_t col = csr ? min((uint32_t)c, (uint32_t)(p.k - 1)) : 0u;
+    const uint32_t oa = p.mp == 4 ? (col * 8u) & ~15u : col * (uint32_t)p.mp * 2u;
+    const uint32_t ob = p.mp == 16 ? oa + 16u : oa;
+    a = *(const uint4*)((const uint8_t*)p.xk + oa);
+    b = *(const uint4*)((const uint8_t*)p.xk + ob);
+  };
+  uint4 ga0, gb0, ga1, gb1, ga2, gb2, ga3, gb3;
+  gload(ocv.x, ga0, gb0);
+  gload(ocv.y, ga1, gb1);
+  gload(ocv.z, ga2, gb2);
+  gload(ocv.w, ga3, gb3);
+  // ---- (7) wave partials -> LDS (the LUT is dead once every wave has streamed) ----
   __syncthreads();
   sf4_t* red = (sf4_t*)smem;  // [wave][T][64 lanes]
 #pragma unroll
@@ -397,38 +422,37 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
   float* bl = (float*)(smem + p.off_bias);
   if (p.bias != nullptr && tid < Rw)
     bl[tid] = p.bias_dt == SPECTRA_F32 ? __builtin_bit_cast(float, bias_raw) : to_f32_16((uint16_t)bias_raw, p.bias_dt);
-  // CSR entries: gather the mp activations of each entry's column (k-major copy) and
-  // stage them with the value; entries beyond the staging capacity (or in a partial
-  // last group of the array) are read directly in the per-output phase
+  int32_t* fxs = (int32_t*)(smem + p.off_fx);
+  if (tid < p.m) fxs[tid] = fx_reg;
+  // CSR entries: the gathered mp activations of each entry's column, staged with the
+  // value; entries beyond the staging capacity (or in a partial last group of the
+  // array) are read directly in the per-output phase
   uint16_t* xe = (uint16_t*)(smem + p.off_xe);
   uint16_t* ve = (uint16_t*)(smem + p.off_ve);
-  const int e_stage = csr ? min(min(e1, e0 + p.ecap), p.csr_nnz & ~3) : 0;
   if (csr) {
-    const int g4 = (e0 & ~3) + 4 * tid;
-    const int cols[4] = {ocv.x, ocv.y, ocv.z, ocv.w};
-    const uint32_t vals[4] = {ovv.x & 0xffffu, ovv.x >> 16, ovv.y & 0xffffu, ovv.y >> 16};
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    auto stage = [&](int u, int col, uint32_t val, const uint4& a, const uint4& b) __attribute__((always_inline)) {
       const int e = g4 + u;
       if (e >= e0 && e < e_stage && g4 + 4 <= p.csr_nnz) {
         const int el = e - e0;
-        const uint16_t* src = p.xk + (int64_t)min((uint32_t)cols[u], (uint32_t)(p.k - 1)) * p.mp;
         if (p.mp == 16) {
-          const uint4 a = ((const uint4*)src)[0], b = ((const uint4*)src)[1];
           ((uint4*)(xe + el * 16))[0] = a;
           ((uint4*)(xe + el * 16))[1] = b;
         } else if (p.mp == 8) {
-          *(uint4*)(xe + el * 8) = *(const uint4*)src;
+          *(uint4*)(xe + el * 8) = a;
         } else {
-          *(uint2*)(xe + el * 4) = *(const uint2*)src;
+          *(uint2*)(xe + el * 4) = (col & 1) ? make_uint2(a.z, a.w) : make_uint2(a.x, a.y);
         }
-        ve[el] = (uint16_t)vals[u];
+        ve[el] = (uint16_t)val;
       }
-    }
+    };
+    stage(0, ocv.x, ovv.x & 0xffffu, ga0, gb0);
+    stage(1, ocv.y, ovv.x >> 16, ga1, gb1);
+    stage(2, ocv.z, ovv.y & 0xffffu, ga2, gb2);
+    stage(3, ocv.w, ovv.y >> 16, ga3, gb3);
   }
   __syncthreads();
 
-  // ---- (7) cross-wave sums in a fixed wave order: thread (t, lane) adds the float4 of
+  // ---- (8) cross-wave sums in a fixed wave order: thread (t, lane) adds the float4 of
   //      every wave (conflict-free 16-byte reads) into sums[m][row] (m-major) ----
   float* sums = (float*)(smem + p.off_sums);
   for (int i = tid; i < T * 64; i += BD) {
@@ -440,30 +464,56 @@ __global__ void __launch_bounds__(512) skinny_kernel(const SkinnyParams p) {
     for (int r = 0; r < 4; ++r)
       if (mq + r < p.m) sums[(mq + r) * R + row] = v[r];
   }
+  // ---- (8b) CSR sums: thread (row, group of 4 m, part) takes a contiguous part of the
+  //      row's entries (P parts on adjacent lanes), 4 activations per entry in one 8-byte
+  //      read; the parts meet in a fixed butterfly order (deterministic) ----
+  float* csums = (float*)(smem + p.off_csum);
+  if (csr) {
+    const int ng = p.mp >> 2;                       // groups of 4 activation rows
+    const int pairs = Rw * ng;
+    int P = 1;                                      // parts per (row, group): a power of two <= 64
+    while (P < 64 && pairs * P * 2 <= BD) P *= 2;
+    const int part = tid & (P - 1);
+    for (int q = tid / P; q < (pairs + BD / P - 1) / (BD / P) * (BD / P); q += BD / P) {  // uniform trip count
+      const bool okq = q < pairs;
+      const int row = okq ? q / ng : 0, mg = okq ? q - (q / ng) * ng : 0;
+      const int lo = rps[row], hi = rps[row + 1];
+      const int hs = min(hi, e_stage);
+      const int len = max(hs - lo, 0), per = (len + P - 1) / P;
+      const int a = lo + part * per, b = min(a + per, hs);
+      float acc4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int e = a; okq && e < b; ++e) {
+        const float vv = h2f(ve[e - e0]);
+        const uint2 xx = *(const uint2*)(xe + (e - e0) * p.mp + 4 * mg);
+        acc4[0] += vv * h2f((uint16_t)(xx.x & 0xffffu));
+        acc4[1] += vv * h2f((uint16_t)(xx.x >> 16));
+        acc4[2] += vv * h2f((uint16_t)(xx.y & 0xffffu));
+        acc4[3] += vv * h2f((uint16_t)(xx.y >> 16));
+      }
+      if (okq && part == 0)
+        for (int e = max(lo, hs); e < hi; ++e) {  // beyond the staged entries: the side tensors directly
+          const uint32_t col = min((uint32_t)p.ccol[e], (uint32_t)(p.k - 1));
+          const float vv = h2f(p.cval[e]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc4[i] += vv * h2f(p.xk[(int64_t)col * p.mp + 4 * mg + i]);
+        }
+      for (int o = 1; o < P; o <<= 1)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc4[i] += __shfl_xor(acc4[i], o);
+      if (okq && part == 0)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * mg + i < p.m) csums[(4 * mg + i) * R + row] = acc4[i];
+    }
+  }
   __syncthreads();
 
-  // ---- (8) per output (row, m): outliers in entry order, scale, bias, store ----
+  // ---- (9) per output (row, m): dense sum + outliers, scale, bias, store ----
   for (int idx = tid; idx < Rw * p.m; idx += BD) {
     const int m = idx / Rw, row = idx - m * Rw;
     float v = sums[m * R + row];
-    if (csr) {
-      const int lo = rps[row], hi = rps[row + 1];
-      const int hs = min(hi, e_stage);
-      int e = lo;
-      for (; e + 4 <= hs; e += 4) {  // staged entries, four reads in flight, summed in order
-        float pr[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) pr[u] = h2f(ve[e - e0 + u]) * h2f(xe[(e - e0 + u) * p.mp + m]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v += pr[u];
-      }
-      for (; e < hs; ++e) v += h2f(ve[e - e0]) * h2f(xe[(e - e0) * p.mp + m]);
-      for (; e < hi; ++e) {  // beyond the staged entries: the side tensors directly
-        const uint32_t col = min((uint32_t)p.ccol[e], (uint32_t)(p.k - 1));
-        v += h2f(p.cval[e]) * h2f(p.xk[(int64_t)col * p.mp + m]);
-      }
-    }
-    float y = v * __builtin_bit_cast(float, (uint32_t)(127 - p.fexp[m]) << 23);
+    if (csr) v += csums[m * R + row];
+    float y = v * __builtin_bit_cast(float, (uint32_t)(127 - fxs[m]) << 23);
     if (p.bias != nullptr) y += bl[row];
     ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + row] = from_f32_16(y, p.act_dt);
   }
@@ -610,14 +660,16 @@ int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_
     stage_end = red_bytes + (uint32_t)ecap * (uint32_t)(2 * mp + 2) + 32;
   }
   p.off_sums = (stage_end + 15u) & ~15u;  // [16][16 T] fp32 cross-wave sums
-  stage_end = p.off_sums + (uint32_t)(16 * 16 * pl.T * 4);
+  p.off_csum = p.off_sums + (uint32_t)(16 * 16 * pl.T * 4);  // [16][16 T] fp32 outlier sums
+  stage_end = p.off_csum + (uint32_t)(16 * 16 * pl.T * 4);
   const uint32_t base = stage_end > (uint32_t)kSkLut ? ((stage_end + 15u) & ~15u) : (uint32_t)kSkLut;
   p.off_xe = red_bytes;
   p.off_ve = (red_bytes + (uint32_t)ecap * (uint32_t)(2 * mp) + 15u) & ~15u;
   p.ecap = ecap;
   p.off_rp = base;
   p.off_bias = (p.off_rp + (uint32_t)(16 * pl.T + 1) * 4 + 15u) & ~15u;
-  const uint32_t lds = p.off_bias + (uint32_t)(16 * pl.T) * 4;
+  p.off_fx = (p.off_bias + (uint32_t)(16 * pl.T) * 4 + 15u) & ~15u;
+  const uint32_t lds = p.off_fx + 16u * 4u;
   if (lds > 163840) return fail(SPECTRA_ERR_UNSUPPORTED, "small-batch LDS plan too large");
   skinny_fn fn = pick_skinny(pl.T, pl.cpw);
   if (fn == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "no small-batch kernel for this plan");
