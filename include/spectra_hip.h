@@ -24,7 +24,8 @@
  *                           <- the Inductor-fused RMSNorm / RoPE / SiLU submodules and the
  *                              static-cache attention of the decode step (engine.py:1240-1250,
  *                              :1387-1415)
- *   spectra_greedy_next     <- spectra/engine.py:1690-1697 sample_token (temperature 0)
+ *   spectra_greedy_next, spectra_greedy_finish
+ *                           <- spectra/engine.py:1690-1697 sample_token (temperature 0)
  *   spectra_kv4_quantize, spectra_kv4_dequantize, spectra_attend_decode_q4
  *                           <- spectra/engine.py:614-700 the 4-bit KV cache
  */
@@ -113,7 +114,16 @@ int spectra_w4a16_gemv(const spectra_qweight_t* w, const void* x, int64_t ldx, i
  *                      [m, N] row stride residual_stride, may alias out (in-place update).
  * Prologues serve m = 1, fp16 activations and NF4 weights (SPECTRA_ERR_UNSUPPORTED
  * otherwise); the residual serves every GEMV.
+ *   argmax_key:        optional (m = 1): the outputs' greedy pick folded into the epilogue.
+ *                      Points at SPECTRA_ARGMAX_SLOTS slots of SPECTRA_ARGMAX_STRIDE device
+ *                      uint64 each (the first of each slot is used; one slot per 256 bytes,
+ *                      so that the slots' atomics spread over the memory channels), all 0
+ *                      before the call (spectra_greedy_finish leaves them 0); each wave
+ *                      merges its best (value, index) of the stored outputs into one slot
+ *                      with an atomic max.  spectra_greedy_finish then reads the token.
  */
+#define SPECTRA_ARGMAX_SLOTS 256
+#define SPECTRA_ARGMAX_STRIDE 32
 typedef enum {
   SPECTRA_PROLOGUE_NONE = 0,
   SPECTRA_PROLOGUE_RMSNORM = 1,
@@ -126,6 +136,7 @@ typedef struct spectra_gemv_fusion {
   const uint16_t* norm_weight; /* RMSNORM: fp16 [K], 16-byte aligned */
   const void* residual;      /* optional, act dtype [m, N] */
   int64_t residual_stride;
+  void* argmax_key;          /* optional: SPECTRA_ARGMAX_SLOTS x SPECTRA_ARGMAX_STRIDE uint64, 8-byte aligned */
 } spectra_gemv_fusion_t;
 
 int spectra_w4a16_gemv_fused(const spectra_qweight_t* w, const void* x, int64_t ldx, int32_t m,
@@ -314,6 +325,13 @@ int spectra_silu_mul(const void* gate_up, int64_t ldgu, int64_t rows, int64_t in
  * *token (if inside [0, hist_len) and history != NULL), then *pos += 1. */
 int spectra_greedy_next(const void* logits, int64_t n, int64_t* token, int64_t* history, int64_t hist_len,
                         int64_t* pos, spectra_stream_t stream);
+
+/* spectra_greedy_next for outputs whose pick a fused GEMV already gathered into argmax_key
+ * (spectra_gemv_fusion_t): same token, history and position update, same tie and NaN
+ * rule; resets the slots to 0 for the next call.  One 64-thread launch
+ * instead of a scan of the logits (engine.py:1690-1697, with the argmax in the lm_head). */
+int spectra_greedy_finish(void* argmax_key, int64_t* token, int64_t* history, int64_t hist_len, int64_t* pos,
+                          spectra_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -39,12 +39,13 @@ class QWeight(ctypes.Structure):
 
 
 PROLOGUE_NONE, PROLOGUE_RMSNORM, PROLOGUE_SILU_MUL = 0, 1, 2
+ARGMAX_SLOTS, ARGMAX_STRIDE = 256, 32  # SPECTRA_ARGMAX_SLOTS, SPECTRA_ARGMAX_STRIDE
 
 
 class GemvFusion(ctypes.Structure):
     """Mirror of ``spectra_gemv_fusion_t``."""
     _fields_ = [("prologue", c_int32), ("eps", ctypes.c_float), ("norm_weight", c_void_p),
-                ("residual", c_void_p), ("residual_stride", c_int64)]
+                ("residual", c_void_p), ("residual_stride", c_int64), ("argmax_key", c_void_p)]
 
 
 # name -> (restype, argtypes); every symbol include/spectra_hip.h declares
@@ -84,6 +85,7 @@ SIGNATURES = {
                                         c_void_p, c_void_p, c_void_p, c_size_t, c_void_p, c_void_p]),
     "spectra_silu_mul": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "spectra_greedy_next": (c_int32, [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "spectra_greedy_finish": (c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "spectra_kv4_quantize": (c_int32, [c_void_p, c_int64, c_int64, c_int32, c_int64, c_int32, c_void_p, c_void_p,
                                        c_void_p, c_int64, c_void_p]),
     "spectra_kv4_dequantize": (c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p]),

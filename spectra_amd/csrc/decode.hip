@@ -650,6 +650,38 @@ __global__ void __launch_bounds__(kArgThreads) greedy_kernel(const uint16_t* __r
   }
 }
 
+// The token of a fused greedy pick: the largest of the SPECTRA_ARGMAX_SLOTS keys (value
+// order in the high word, complemented index in the low word), then the history / position
+// update of greedy_kernel; the slots are left at 0 for the next pick.
+__global__ void __launch_bounds__(64) greedy_finish_kernel(unsigned long long* __restrict__ key,
+                                                           int64_t* __restrict__ token, int64_t* __restrict__ history,
+                                                           int64_t hist_len, int64_t* __restrict__ pos) {
+  const int lane = threadIdx.x;
+  constexpr int PER = SPECTRA_ARGMAX_SLOTS / 64;
+  unsigned long long k = 0ull;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const unsigned long long t = key[(lane + 64 * i) * SPECTRA_ARGMAX_STRIDE];
+    k = t > k ? t : k;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const unsigned long long t = __shfl_xor(k, o);
+    k = t > k ? t : k;
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) key[(lane + 64 * i) * SPECTRA_ARGMAX_STRIDE] = 0ull;
+  if (lane == 0) {
+    const int64_t tok = (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffull));
+    *token = tok;
+    if (pos != nullptr) {
+      const int64_t p = *pos + 1;
+      if (history != nullptr && p >= 0 && p < hist_len) history[p] = tok;
+      *pos = p;
+    }
+  }
+}
+
 }  // namespace spectra
 
 using namespace spectra;
@@ -837,6 +869,18 @@ extern "C" int spectra_silu_mul(const void* gate_up, int64_t ldgu, int64_t rows,
   SPECTRA_REQUIRE((n + kDecThreads - 1) / kDecThreads < (int64_t(1) << 31), "too many elements");
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + kDecThreads - 1) / kDecThreads)), dim3(kDecThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)gate_up, ldgu, (int)inter, n, (uint16_t*)act);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
+extern "C" int spectra_greedy_finish(void* argmax_key, int64_t* token, int64_t* history, int64_t hist_len,
+                                     int64_t* pos, spectra_stream_t stream) {
+  SPECTRA_REQUIRE(argmax_key && token, "NULL pointer");
+  SPECTRA_REQUIRE((reinterpret_cast<uintptr_t>(argmax_key) & 7) == 0, "argmax slots must be 8-byte aligned");
+  SPECTRA_REQUIRE(history == nullptr || (pos != nullptr && hist_len >= 1), "history needs pos and a length");
+  static_assert(SPECTRA_ARGMAX_SLOTS % 64 == 0, "one wave reads the slots, the same count per lane");
+  hipLaunchKernelGGL(greedy_finish_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                     (unsigned long long*)argmax_key, token, history, hist_len, pos);
   SPECTRA_HIP_CHECK(hipGetLastError());
   return SPECTRA_OK;
 }

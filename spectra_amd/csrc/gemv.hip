@@ -375,10 +375,12 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
                     "CSR columns must be 16-byte and values 8-byte aligned (nnz < 2^31)");
   // the kernels pair each format with its own outlier kind and scale scheme: Format B
   // (NF4, blocks >= 64, CSR outliers), Format A (groups of 32, dense outlier columns)
+  // (the greedy pick rides on the epilogue of the kernel below only)
+  const bool pick = fu != nullptr && fu->argmax_key != nullptr;
   RowsPlan rp;
-  if (rows_serves(w, m, act_dtype, kpro, &rp)) return rows_launch(w, rp, x, act_dtype, out, stream, fu, kpro);
+  if (!pick && rows_serves(w, m, act_dtype, kpro, &rp)) return rows_launch(w, rp, x, act_dtype, out, stream, fu, kpro);
   StreamPlan sp;
-  if (stream_serves(w, m, &sp)) return stream_launch(w, sp, x, act_dtype, out, stream, fu, kpro);
+  if (!pick && stream_serves(w, m, &sp)) return stream_launch(w, sp, x, act_dtype, out, stream, fu, kpro);
   if (w->format == SPECTRA_FMT_NF4 && w->group_size < 64)
     return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMV family needs an NF4 block of at least 64");
   if (outliers && (w->format == SPECTRA_FMT_NF4) != csr)
@@ -412,6 +414,7 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
   p.eps = fu ? fu->eps : 0.0f;
   p.res = fu ? fu->residual : nullptr;
   p.ldr = fu ? fu->residual_stride : 0;
+  p.akey = pick ? (unsigned long long*)fu->argmax_key : nullptr;
   gemv_fn fn = pro != SPECTRA_PROLOGUE_NONE
                    ? gemv_pick_f16_pro(pro == SPECTRA_PROLOGUE_RMSNORM ? kProRms : kProSiluMul, pl.rpw, pl.wide)
                : act_dtype == SPECTRA_BF16 ? gemv_pick_bf16(w->format, pl.mt, pl.rpw, pl.wide)
@@ -456,5 +459,8 @@ extern "C" int spectra_w4a16_gemv_fused(const spectra_qweight_t* w, const void* 
                       "RMSNorm needs a 16-byte aligned fp16 weight");
   }
   if (fusion->residual != nullptr) SPECTRA_REQUIRE(fusion->residual_stride >= w->n, "residual row stride too small");
+  if (fusion->argmax_key != nullptr)
+    SPECTRA_REQUIRE(m == 1 && (reinterpret_cast<uintptr_t>(fusion->argmax_key) & 7) == 0 && w->n < (int64_t(1) << 31),
+                    "the fused greedy pick serves one row, with 8-byte aligned slots");
   return spectra::gemv_launch(w, x, ldx, m, act_dtype, out, ldo, (hipStream_t)stream, fusion);
 }

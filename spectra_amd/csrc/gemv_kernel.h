@@ -73,7 +73,24 @@ struct GemvParams {
   float eps;        // PRO 2
   const void* res;  // optional residual [m, N] (act dtype, may alias out): out = res + out
   int64_t ldr;
+  unsigned long long* akey;  // optional (m = 1): greedy-pick slots, merged with an atomic max
 };
+
+// Greedy-pick key of an output: the value's order (NaN above every number, -0 == +0) in the
+// high word, the complement of the index in the low word, so that the largest key is the
+// largest value and, among equal values, the lowest index (torch.argmax's rule).  0 is
+// below every key (the slots' empty state).
+__device__ __forceinline__ unsigned long long argmax_key(float f, int idx) {
+  uint32_t b = __builtin_bit_cast(uint32_t, f);
+  uint32_t o;
+  if (f != f) {
+    o = 0xffffffffu;
+  } else {
+    if (f == 0.0f) b = 0u;
+    o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  }
+  return ((unsigned long long)o << 32) | (unsigned long long)(0xffffffffu - (uint32_t)idx);
+}
 
 // activation prologues fused into the GEMV
 constexpr int kProNone = 0;     // x as given
@@ -713,6 +730,7 @@ __global__ void __launch_bounds__(LB, (MT == 1 && LB == 512 && RPW <= gemv_rpw_t
   // ---------------- (10) per-row totals: 16 lanes per row, four rows per wave per pass ----------------
   // fixed order (deterministic): lane gl of a group takes slice gl and outlier entries
   // gl, gl + 16, ... of its row, then a DPP tree sums the 16 lanes
+  unsigned long long best_key = 0;  // (11): this lane's greedy pick
   {
     float inv = 1.0f;  // PRO kProRms: rsqrt(mean(h^2) + eps) of the row
     if constexpr (PRO == kProRms) {
@@ -776,10 +794,30 @@ __global__ void __launch_bounds__(LB, (MT == 1 && LB == 512 && RPW <= gemv_rpw_t
           if constexpr (PRO == kProRms) y *= inv;
           if (p.bias != nullptr) y += bl[rr];
           if (p.res != nullptr) y = to_f32_16(from_f32_16(y, odt), odt) + to_f32_16(rl[m * Rw + rr], odt);
-          ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + rr] = from_f32_16(y, odt);
+          const uint16_t yo = from_f32_16(y, odt);
+          ((uint16_t*)p.out)[(int64_t)m * p.ldo + r0 + rr] = yo;
+          if (m == 0) {  // greedy pick of the stored value
+            const unsigned long long kk = argmax_key(to_f32_16(yo, odt), r0 + rr);
+            best_key = kk > best_key ? kk : best_key;
+          }
         }
       }
     }
+  }
+  // ---------------- (11) greedy pick: one atomic max per wave, no barrier ----------------
+  // (the keys sit in lanes 0, 16, 32, 48: the groups' store lanes)
+  if (p.akey != nullptr) {  // (uniform)
+    unsigned long long kw = best_key;
+#pragma unroll
+    for (int l = 16; l < 64; l += 16) {
+      const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)best_key, l);
+      const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(best_key >> 32), l);
+      const unsigned long long t = ((unsigned long long)hi << 32) | lo;
+      kw = t > kw ? t : kw;
+    }
+    if (lane == 0 && kw != 0)
+      __hip_atomic_fetch_max(p.akey + ((blockIdx.x * nwaves + wave) & (SPECTRA_ARGMAX_SLOTS - 1)) * SPECTRA_ARGMAX_STRIDE,
+                             kw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

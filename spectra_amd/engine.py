@@ -15,9 +15,9 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from .kernels import (GEMV_MAX_M, QWeightOperands, attend_decode, attend_decode_q4, attend_workspace_bytes,
-                      greedy_next, kv4_quantize, rmsnorm, rope_append, silu_mul, w4_embedding, w4a16_gemv_fused,
-                      w4a16_linear)
+from .kernels import (GEMV_MAX_M, QWeightOperands, argmax_slots, attend_decode, attend_decode_q4,
+                      attend_workspace_bytes, greedy_finish, greedy_next, kv4_quantize, rmsnorm, rope_append, silu_mul,
+                      w4_embedding, w4a16_gemv_fused, w4a16_linear)
 
 __all__ = ["SpectraFusedLinear", "SpectraFusedEmbedding", "DecoderConfig", "SpectraDecoder"]
 
@@ -312,6 +312,7 @@ class SpectraDecoder(nn.Module):
         self.cur_id = torch.zeros(1, dtype=torch.int64, device=dev)
         self.cur_pos = torch.zeros(1, dtype=torch.int64, device=dev)
         self.history = torch.zeros(c.max_seq + 1, dtype=torch.int64, device=dev)  # token at each position
+        self.pick = argmax_slots(dev)  # the lm_head GEMV's fused greedy pick (left at 0 by greedy_finish)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
         self.graph_logits: Optional[torch.Tensor] = None
         self.device = dev
@@ -472,16 +473,21 @@ class SpectraDecoder(nn.Module):
             gu = self._gemv_parts(blk["gate_up"], rmsnorm(h, self.norm_w[2 * li + 1], c.rms_eps))
             w4a16_gemv_fused(blk["down"]._operands(), silu_mul(gu), residual=h, out=h)
 
-    def forward_tokens(self, ids: torch.Tensor, pos: torch.Tensor, causal_len: Optional[int]) -> torch.Tensor:
+    def forward_tokens(self, ids: torch.Tensor, pos: torch.Tensor, causal_len: Optional[int],
+                       pick: bool = False) -> torch.Tensor:
+        """Logits of the last token.  ``pick`` (decode only): the lm_head GEMV also gathers the
+        greedy pick into ``self.pick``, which ``greedy_finish`` must then consume."""
         h = self.embed(ids)
         c = self.cfg
         if causal_len is None:  # decode: one token, fused GEMVs
             for li in range(c.layers):
                 self._layer_decode(li, h, pos)
+            key = self.pick if pick else None
             if not self.fused:
-                return w4a16_gemv_fused(self.lm_head._operands(), rmsnorm(h, self.norm_w[-1], c.rms_eps))
+                return w4a16_gemv_fused(self.lm_head._operands(), rmsnorm(h, self.norm_w[-1], c.rms_eps),
+                                        argmax_key=key)
             return w4a16_gemv_fused(self.lm_head._operands(), h, prologue="rmsnorm", norm_weight=self.norm_w16[-1],
-                                    eps=c.rms_eps)
+                                    eps=c.rms_eps, argmax_key=key)
         delta = None
         for li in range(c.layers):
             delta = self._layer(li, h, delta, pos, causal_len)
@@ -502,8 +508,8 @@ class SpectraDecoder(nn.Module):
         return logits
 
     def _decode_step(self) -> torch.Tensor:
-        logits = self.forward_tokens(self.cur_id, self.cur_pos, None)
-        greedy_next(logits[0], self.cur_id, self.history, self.cur_pos)
+        logits = self.forward_tokens(self.cur_id, self.cur_pos, None, pick=True)  # the pick rides on the lm_head
+        greedy_finish(self.pick, self.cur_id, self.history, self.cur_pos)
         return logits
 
     def cache_tensors(self):

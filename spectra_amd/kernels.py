@@ -28,7 +28,8 @@ from . import _lib as L
 
 __all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_dequant", "fwht_rows",
            "QWeightOperands", "GEMV_MAX_M", "w4_embedding", "rmsnorm", "rope_append", "attend_decode",
-           "attend_workspace_bytes", "silu_mul", "greedy_next", "w4a16_gemv_fused", "kv4_quantize",
+           "attend_workspace_bytes", "silu_mul", "greedy_next", "argmax_slots", "greedy_finish",
+           "w4a16_gemv_fused", "kv4_quantize",
            "kv4_dequantize", "attend_decode_q4", "validate_outliers"]
 
 GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
@@ -503,16 +504,43 @@ def greedy_next(logits: torch.Tensor, token: torch.Tensor, history: Optional[tor
     return token
 
 
+def argmax_slots(device: Optional[torch.device] = None) -> torch.Tensor:
+    """Zeroed slots for a GEMV's fused greedy pick (``w4a16_gemv_fused(argmax_key=...)``)."""
+    return torch.zeros(L.ARGMAX_SLOTS * L.ARGMAX_STRIDE, dtype=torch.int64, device=device or torch.device("cuda"))
+
+
+def greedy_finish(argmax_key: torch.Tensor, token: torch.Tensor, history: Optional[torch.Tensor] = None,
+                  pos: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``greedy_next`` for outputs whose pick a fused GEMV gathered into ``argmax_key``: same
+    token, history and position update; leaves the slots at 0 for the next pick."""
+    if argmax_key.dtype != torch.int64 or argmax_key.numel() != L.ARGMAX_SLOTS * L.ARGMAX_STRIDE or \
+            not argmax_key.is_cuda or not argmax_key.is_contiguous():
+        raise ValueError("argmax_key must come from argmax_slots()")
+    for t, name in ((token, "token"), (history, "history"), (pos, "pos")):
+        if t is not None and (t.dtype != torch.int64 or not t.is_cuda or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous int64 GPU tensor")
+    lib = L.load()
+    L.check("spectra_greedy_finish", lib.spectra_greedy_finish(argmax_key.data_ptr(), token.data_ptr(),
+                                                                history.data_ptr() if history is not None else None,
+                                                                history.numel() if history is not None else 0,
+                                                                pos.data_ptr() if pos is not None else None,
+                                                                _stream(argmax_key.device)))
+    return token
+
+
 def w4a16_gemv_fused(ops: QWeightOperands, x: torch.Tensor, *, prologue: str = "none",
                      norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-5,
-                     residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                     argmax_key: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One-row GEMV with a decoder layer's neighbouring work fused in:
 
     * ``prologue="rmsnorm"``: x is the residual stream h; computes linear(rmsnorm(h)) with
       ``norm_weight`` (fp16 [K]) and ``eps``;
     * ``prologue="silu_mul"``: x is a fused gate_up row [2K]; computes linear(silu(g) * u);
     * ``residual`` [1, N]: returns residual + linear(...) (fp16 roundings of both, as the
-      separate add); ``out`` may be ``residual`` itself (in-place update).
+      separate add); ``out`` may be ``residual`` itself (in-place update);
+    * ``argmax_key`` (``argmax_slots()``): the greedy pick of the stored outputs gathered
+      in the epilogue, for ``greedy_finish``.
     """
     codes = {"none": L.PROLOGUE_NONE, "rmsnorm": L.PROLOGUE_RMSNORM, "silu_mul": L.PROLOGUE_SILU_MUL}
     if prologue not in codes:
@@ -540,6 +568,11 @@ def w4a16_gemv_fused(ops: QWeightOperands, x: torch.Tensor, *, prologue: str = "
         if r2.stride(1) != 1:
             raise ValueError("residual rows must be contiguous")
         fu.residual, fu.residual_stride = r2.data_ptr(), r2.stride(0)
+    if argmax_key is not None:
+        if argmax_key.dtype != torch.int64 or argmax_key.numel() != L.ARGMAX_SLOTS * L.ARGMAX_STRIDE or \
+                not argmax_key.is_cuda or not argmax_key.is_contiguous():
+            raise ValueError("argmax_key must come from argmax_slots()")
+        fu.argmax_key = argmax_key.data_ptr()
     lib = L.load()
     L.check("spectra_w4a16_gemv_fused", lib.spectra_w4a16_gemv_fused(ops.ptr(), x2.data_ptr(), ldx, x2.shape[0],
                                                                       L.F16, ctypes.byref(fu), out2.data_ptr(),

@@ -287,6 +287,60 @@ def test_gemv_residual_without_prologue(hip):
     assert torch.equal(r, res + y)
 
 
+@pytest.mark.parametrize("n,k,had,pro", [(128256, 3072, 0, "rmsnorm"),  # the decoder's lm_head
+                                          (1000, 1024, 128, "none"), (257, 2048, 0, "rmsnorm")])
+def test_gemv_fused_greedy_pick(hip, n, k, had, pro):
+    """The greedy pick gathered in the GEMV epilogue (one atomic max per workgroup into 64
+    slots) then read by greedy_finish: the same token, history and position update as
+    greedy_next on the stored outputs, and the slots left at 0 for the next pick."""
+    case(n=n, k=k, had=had, pro=pro)
+    ops, _ = _nf4_ops(n, k, had, seed=n + 3)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    nw = (torch.rand(k, device="cuda", generator=g) + 0.5).half()
+    kw = dict(prologue="rmsnorm", norm_weight=nw) if pro == "rmsnorm" else {}
+    pick = K.argmax_slots()
+    for trial in range(3):
+        h = (torch.randn(1, k, device="cuda", generator=g) * 3).half()
+        y = K.w4a16_gemv_fused(ops, h, argmax_key=pick, **kw)
+        # (the pick runs on one GEMV kernel; without it the planner may choose another, whose
+        # fp32 summation order differs)
+        y0 = K.w4a16_gemv_fused(ops, h, **kw)
+        assert float((y.float() - y0.float()).abs().max()) <= 1e-2 * max(1.0, float(y0.float().abs().max()))
+        tok, hist, pos = (torch.zeros(1, dtype=torch.int64, device="cuda"),
+                          torch.full((8,), -1, dtype=torch.int64, device="cuda"),
+                          torch.tensor([2], dtype=torch.int64, device="cuda"))
+        K.greedy_finish(pick, tok, hist, pos)
+        ref_tok, ref_hist, ref_pos = tok.clone(), hist.clone(), torch.tensor([2], dtype=torch.int64, device="cuda")
+        ref_hist.fill_(-1)
+        K.greedy_next(y.reshape(-1), ref_tok, ref_hist, ref_pos)
+        assert int(tok) == int(ref_tok) == _argmax_rule(y.reshape(-1)), trial
+        assert torch.equal(hist, ref_hist) and int(pos) == int(ref_pos) == 3
+        assert int(pick.abs().sum()) == 0
+
+
+def test_gemv_fused_greedy_pick_ties_and_nans(hip):
+    """Equal outputs (every weight row the same): the lowest index; a NaN activation (every
+    output NaN): index 0, as torch.argmax."""
+    n, k = 3000, 1024
+    case(n=n, k=k, rows="identical")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    w = (torch.randn(1, k, device="cuda", generator=g) * 0.02).half().expand(n, k).contiguous()
+    q = C.quantize_nf4(w, 64, 0, None, True)
+    ops = K.QWeightOperands(q.packed, q.absmax, None, k, codebook="nf4", group_size=64, marlin_layout=True)
+    pick = K.argmax_slots()
+    tok = torch.zeros(1, dtype=torch.int64, device="cuda")
+    h = torch.randn(1, k, device="cuda", generator=g).half()
+    y = K.w4a16_gemv_fused(ops, h, argmax_key=pick)
+    assert bool((y == y[0, 0]).all())
+    K.greedy_finish(pick, tok)
+    assert int(tok) == 0
+    h[0, 17] = float("nan")
+    y = K.w4a16_gemv_fused(ops, h, argmax_key=pick)
+    assert bool(torch.isnan(y).all())
+    K.greedy_finish(pick, tok)
+    assert int(tok) == 0 and int(pick.abs().sum()) == 0
+
+
 # ---------------------------------------------------------------------------
 # the 4-bit KV cache (reference engine.py:614-700)
 # ---------------------------------------------------------------------------
