@@ -279,9 +279,11 @@ int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t tokens, const in
  * out [heads, head_dim] fp16 = softmax(q k^T / sqrt(head_dim)) v over positions [0, *pos]
  * (fp32 softmax; grouped-query: query head h reads KV head h / (heads / kv_heads); 1, 2, 3,
  * 4, 6 or 8 query heads per KV head; head_dim 16, 32, 64, 128 or 256; operands 16-byte aligned).
- * Two kernels: spectra_attend_spans(max_seq) spans of 64 positions per KV head, then a
- * log-sum-exp merge.  workspace: >= spectra_attend_workspace(heads, head_dim, max_seq)
- * bytes, 16-byte aligned (span partials); calls sharing a workspace must not overlap. */
+ * One kernel: spectra_attend_spans(max_seq) workgroups of 64 positions per KV head; the
+ * last of a head to finish merges the spans (log-sum-exp).  workspace: >=
+ * spectra_attend_workspace(heads, head_dim, max_seq) bytes, 16-byte aligned (span partials
+ * and per-head arrival counters), ZEROED before its first use (every call leaves the
+ * counters at zero again); calls sharing a workspace must not overlap. */
 int32_t spectra_attend_spans(int32_t max_seq);
 size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq);
 int spectra_attend_decode(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t, int32_t heads,

@@ -10,11 +10,12 @@
 //   attend_kernel       batch-1 decode attention on the fused-QKV row: rotates q and the new
 //                       k, appends k and v to the caches, and attends over [0, pos] split
 //                       into spans of 64 positions (one workgroup per KV head and span,
-//                       fp32 softmax pieces)
-//   combine_kernel      merges the spans of every head (log-sum-exp) into fp16
+//                       fp32 softmax pieces); the last span workgroup of a KV head merges
+//                       the spans (log-sum-exp) into fp16
 //   silu_mul_kernel     act = fp16(silu(g) * u) on the fused gate_up output
 //   greedy_kernel       greedy sampling: token = argmax(logits), appended to the history at
 //                       pos + 1, pos advanced (the decode step's whole sampling tail)
+//   greedy_finish_kernel the same tail for a pick gathered in a GEMV epilogue
 //
 // The position of the decoded token is read from device memory, so a decode step has no
 // host-side value and is captured once as a HIP graph.
@@ -257,6 +258,68 @@ __device__ __forceinline__ uint4 rope_chunk(const uint4& own, const uint4& partn
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// Partials cross workgroups (and XCDs, whose L2 caches are not coherent with each other)
+// as device-scope relaxed atomics: stores write through to the device's coherence point,
+// loads read from it.
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Arrival of a span workgroup, and the merge by the last one of its KV head: every thread's
+// partial stores have completed before the workgroup counts itself in (one device-scope
+// atomic on the head's counter, 256 bytes apart per head); the workgroup that brings the
+// count to nspan merges the G heads' spans exactly as a separate merge kernel would (16
+// spans' loads in flight, m = -inf marks an empty span) and leaves the counter at 0.
+template <int G, int HD>
+__device__ __forceinline__ void attend_arrive_merge(const float* part, uint32_t* counter, uint16_t* out, int kh,
+                                                    int nspan, int tid, int* last_l) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0)
+    *last_l = __hip_atomic_fetch_add(counter + kh * 64, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (uint32_t)(nspan - 1);
+  __syncthreads();
+  if (!*last_l) return;
+  if (tid == 0) __hip_atomic_store(counter + kh * 64, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  constexpr int B = 16;
+  for (int o = tid; o < G * HD; o += kDecThreads) {
+    const int j = o / HD, d = o - j * HD;
+    const int h = kh * G + j;
+    const float* ph = part + (int64_t)h * nspan * (HD + 2);
+    float m = -INFINITY, l = 0.0f, a = 0.0f;
+    for (int s0 = 0; s0 < nspan; s0 += B) {
+      float mv[B], lv[B], av[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const bool ok = s0 + u < nspan;
+        const float* pp = ph + (int64_t)(ok ? s0 + u : 0) * (HD + 2);
+        mv[u] = ok ? load_dev(pp + HD) : -INFINITY;
+        lv[u] = load_dev(pp + HD + 1);
+        av[u] = load_dev(pp + d);
+      }
+      float mb = m;
+#pragma unroll
+      for (int u = 0; u < B; ++u) mb = fmaxf(mb, mv[u]);
+      if (mb == -INFINITY) continue;  // nothing yet
+      const float r = __expf(m - mb);  // rescale what came before (0 when m = -inf)
+      l *= r;
+      a *= r;
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        if (mv[u] == -INFINITY) continue;  // empty span: its V sums were never written
+        const float f = __expf(mv[u] - mb);
+        l += lv[u] * f;
+        a += av[u] * f;
+      }
+      m = mb;
+    }
+    out[(int64_t)h * HD + d] = f2h(a / l);
+  }
+}
+
 // grid (kv_heads, nspan), 256 threads.  Span sp covers positions [64 sp, 64 sp + 64) of
 // [0, pos]; spans past the position only mark themselves empty.  Each workgroup:
 //   * rotates the query heads of its group from the fused-QKV row (ROPE) -- every
@@ -265,16 +328,17 @@ __device__ __forceinline__ uint4 rope_chunk(const uint4& own, const uint4& partn
 //   * thread = (dg: 8 consecutive head dims, pr: position row), pass i = positions
 //     pr + i * PPW; every K and V chunk of the span is loaded up front (16 bytes each);
 //   * writes its span's max score, sum of exponentials and exponential-weighted V sums
-//     to part [heads][nspan][hd + 2] (fp32), which combine_kernel merges.  (Merging in the
-//     last workgroup to finish needs device-scope fences, which write back the L2 of
-//     every XCD and cost more than the second launch.)
+//     to part [heads][nspan][hd + 2] (fp32, device-coherent stores); the last span
+//     workgroup of the KV head merges them into out (attend_arrive_merge).
 template <int G, int HD, bool ROPE, bool Q4>
 __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __restrict__ qkv,
                                                               const int64_t* __restrict__ pos_p,
                                                               const float* __restrict__ cos_t,
                                                               const float* __restrict__ sin_t, int heads,
                                                               int kv_heads, float scale, const KvCache kvc,
-                                                              float* __restrict__ part) {
+                                                              float* __restrict__ part,
+                                                              uint32_t* __restrict__ counter,
+                                                              uint16_t* __restrict__ out) {
   const int lmax = kvc.lmax;
   constexpr int DG = HD / 8;               // lanes per position
   // positions per pass: at HD 16 the workgroup has more position rows than the span has
@@ -305,12 +369,13 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
   pos = pos < 0 ? 0 : (pos >= lmax ? lmax - 1 : pos);
   const int n = (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform
   float* pbase = part + ((int64_t)kh * G * nspan + sp) * (HD + 2);  // head j: + j * nspan * (HD + 2)
+  __shared__ int last_l;
   if (n <= 0) {  // span past the position: an empty piece for the merge
     if (tid < G) {
-      pbase[(int64_t)tid * nspan * (HD + 2) + HD] = -INFINITY;
-      pbase[(int64_t)tid * nspan * (HD + 2) + HD + 1] = 0.0f;
+      store_dev(pbase + (int64_t)tid * nspan * (HD + 2) + HD, -INFINITY);
+      store_dev(pbase + (int64_t)tid * nspan * (HD + 2) + HD + 1, 0.0f);
     }
-    if constexpr (!Q4) __builtin_amdgcn_s_waitcnt(0x0f70);  // the span's loads land before the wave ends
+    attend_arrive_merge<G, HD>(part, counter, out, kh, nspan, tid, &last_l);  // (waits for the span's loads)
     return;
   }
   const bool upper = dg * 8 >= H2;
@@ -433,8 +498,8 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
       sc[j][tid] = e;
       const float l = wave_sum(e);
       if (tid == 0) {
-        pbase[(int64_t)j * nspan * (HD + 2) + HD] = m;
-        pbase[(int64_t)j * nspan * (HD + 2) + HD + 1] = l;
+        store_dev(pbase + (int64_t)j * nspan * (HD + 2) + HD, m);
+        store_dev(pbase + (int64_t)j * nspan * (HD + 2) + HD + 1, l);
       }
     }
   }
@@ -472,44 +537,10 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
   __syncthreads();
   for (int o = tid; o < G * HD; o += kDecThreads) {
     const int j = o / HD, d = o - j * HD;
-    pbase[(int64_t)j * nspan * (HD + 2) + d] = (wsum[0][j][d] + wsum[1][j][d]) + (wsum[2][j][d] + wsum[3][j][d]);
+    store_dev(pbase + (int64_t)j * nspan * (HD + 2) + d,
+              (wsum[0][j][d] + wsum[1][j][d]) + (wsum[2][j][d] + wsum[3][j][d]));
   }
-}
-
-// grid heads, blockDim hd: out[h][d] = sum_s acc_s[d] e^(m_s - M) / sum_s l_s e^(m_s - M)
-// over the spans of head h (empty spans carry m = -inf); 16 spans' loads in flight at once.
-__global__ void combine_kernel(const float* __restrict__ part, int nspan, int hd, uint16_t* __restrict__ out) {
-  constexpr int B = 16;
-  const int h = blockIdx.x, d = threadIdx.x;
-  const float* ph = part + (int64_t)h * nspan * (hd + 2);
-  float m = -INFINITY, l = 0.0f, a = 0.0f;
-  for (int s0 = 0; s0 < nspan; s0 += B) {
-    float mv[B], lv[B], av[B];
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-      const bool ok = s0 + u < nspan;
-      const float* p = ph + (int64_t)(ok ? s0 + u : 0) * (hd + 2);
-      mv[u] = ok ? p[hd] : -INFINITY;
-      lv[u] = p[hd + 1];
-      av[u] = p[d];
-    }
-    float mb = m;
-#pragma unroll
-    for (int u = 0; u < B; ++u) mb = fmaxf(mb, mv[u]);
-    if (mb == -INFINITY) continue;  // nothing yet
-    const float r = __expf(m - mb);  // rescale what came before (0 when m = -inf)
-    l *= r;
-    a *= r;
-#pragma unroll
-    for (int u = 0; u < B; ++u) {
-      if (mv[u] == -INFINITY) continue;  // empty span: its V sums were never written
-      const float f = __expf(mv[u] - mb);
-      l += lv[u] * f;
-      a += av[u] * f;
-    }
-    m = mb;
-  }
-  out[h * hd + d] = f2h(a / l);
+  attend_arrive_merge<G, HD>(part, counter, out, kh, nspan, tid, &last_l);
 }
 
 // grid (ceil(rows * d / 8 / 256), heads): one lane per 8 values (groups of 32 = 4 lanes)
@@ -720,13 +751,19 @@ extern "C" int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t token
 
 extern "C" int32_t spectra_attend_spans(int32_t max_seq) { return (max_seq + kSpanMax - 1) / kSpanMax; }
 
+// [heads][nspan][head_dim + 2] fp32 partials, then one arrival counter per head, 256 bytes apart
+static size_t attend_part_bytes(int32_t heads, int32_t head_dim, int32_t max_seq) {
+  const size_t b = (size_t)heads * spectra_attend_spans(max_seq) * (head_dim + 2) * sizeof(float);
+  return (b + 255) & ~(size_t)255;
+}
+
 extern "C" size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq) {
   if (heads < 1 || head_dim < 1 || max_seq < 1) return 0;
-  return (size_t)heads * spectra_attend_spans(max_seq) * (head_dim + 2) * sizeof(float);
+  return attend_part_bytes(heads, head_dim, max_seq) + (size_t)heads * 256;
 }
 
 typedef void (*attend_fn)(const uint16_t*, const int64_t*, const float*, const float*, int, int, float, const KvCache,
-                          float*);
+                          float*, uint32_t*, uint16_t*);
 
 template <int HD, bool ROPE, bool Q4>
 static attend_fn pick_attend(int g) {
@@ -787,11 +824,9 @@ static int attend_launch(const void* qkv, const int64_t* pos, const float* cos_t
   const float scale = 1.0f / sqrtf((float)head_dim);
   float* part = (float*)workspace;
   const hipStream_t s = (hipStream_t)stream;
+  uint32_t* counter = (uint32_t*)((uint8_t*)workspace + attend_part_bytes(heads, head_dim, kvc.lmax));
   hipLaunchKernelGGL(fn, dim3((unsigned)kv_heads, (unsigned)nspan), dim3(kDecThreads), 0, s, (const uint16_t*)qkv,
-                     pos, cos_t, sin_t, heads, kv_heads, scale, kvc, part);
-  SPECTRA_HIP_CHECK(hipGetLastError());
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)heads), dim3((unsigned)head_dim), 0, s, part, nspan, head_dim,
-                     (uint16_t*)out);
+                     pos, cos_t, sin_t, heads, kv_heads, scale, kvc, part, counter, (uint16_t*)out);
   SPECTRA_HIP_CHECK(hipGetLastError());
   return SPECTRA_OK;
 }

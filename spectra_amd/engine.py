@@ -307,7 +307,8 @@ class SpectraDecoder(nn.Module):
         ang = torch.arange(c.max_seq, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)  # [max_seq, hd/2]
         self.arange = torch.arange(c.max_seq, device=dev)
-        self.attn_ws = torch.empty(attend_workspace_bytes(c.heads, hd, c.max_seq), device=dev, dtype=torch.uint8)
+        # attention partials and the merge's arrival counters (zero before the first call)
+        self.attn_ws = torch.zeros(attend_workspace_bytes(c.heads, hd, c.max_seq), device=dev, dtype=torch.uint8)
         # device-side decode state
         self.cur_id = torch.zeros(1, dtype=torch.int64, device=dev)
         self.cur_pos = torch.zeros(1, dtype=torch.int64, device=dev)

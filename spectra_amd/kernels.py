@@ -459,8 +459,8 @@ def attend_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: Optional[torch.Tens
         if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or t.shape != (lmax, hd // 2)):
             raise ValueError(f"{name} must be contiguous fp32 [L, d/2]")
     need = attend_workspace_bytes(heads, hd, lmax)
-    if workspace is None:
-        workspace = torch.empty(need, device=qkv.device, dtype=torch.uint8)
+    if workspace is None:  # (zeroed: the merge's arrival counters; every call leaves them at zero)
+        workspace = torch.zeros(need, device=qkv.device, dtype=torch.uint8)
     if out is None:
         out = torch.empty((heads, hd), device=qkv.device, dtype=torch.float16)
     _need_f16(out, "out")
@@ -639,8 +639,8 @@ def attend_decode_q4(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, si
     if pos.dtype != torch.int64 or pos.numel() != 1:
         raise ValueError("pos must be int64 [1]")
     need = attend_workspace_bytes(heads, hd, lmax)
-    if workspace is None:
-        workspace = torch.empty(need, device=qkv.device, dtype=torch.uint8)
+    if workspace is None:  # (zeroed: the merge's arrival counters; every call leaves them at zero)
+        workspace = torch.zeros(need, device=qkv.device, dtype=torch.uint8)
     if out is None:
         out = torch.empty((heads, hd), device=qkv.device, dtype=torch.float16)
     ptrs = [t.data_ptr() for t in (k_window, v_window, k4[0], v4[0], k4[1], v4[1], k4[2], v4[2])]

@@ -108,7 +108,8 @@ def test_decode_kernels_reject_bad_arguments():
     assert "stride" in lib.spectra_last_error().decode()
     # 64 spans of 64 positions for max_seq 4096; the partials are fp32 [heads][spans][d + 2]
     assert lib.spectra_attend_spans(4096) == 64 and lib.spectra_attend_spans(4097) == 65
-    assert lib.spectra_attend_workspace(24, 128, 1000) == 24 * 16 * 130 * 4
+    # partials rounded up to 256 bytes, then one 256-byte arrival counter per head
+    assert lib.spectra_attend_workspace(24, 128, 1000) == (24 * 16 * 130 * 4 + 255) // 256 * 256 + 24 * 256
     args = (p, p, p, p)
     assert lib.spectra_attend_decode(*args, 24, 8, 128, 1024, p, p, None, 0, p, None) == L.ERR_WORKSPACE
     assert lib.spectra_attend_decode(*args, 24, 8, 48, 1024, p, p, p, 1 << 20, p, None) == L.ERR_INVALID

@@ -93,7 +93,7 @@ def test_attend_decode(hip, heads, kv, hd, L, rope):
     kc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
     vc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
     cos, sin = _tables(L, hd) if rope else (None, None)
-    ws = torch.full((K.attend_workspace_bytes(heads, hd, L),), 255, device="cuda", dtype=torch.uint8)  # reused
+    ws = torch.zeros((K.attend_workspace_bytes(heads, hd, L),), device="cuda", dtype=torch.uint8)  # reused
     grp = heads // kv
     for p in sorted({0, 1, 62, 63, 64, 65, 511, 512, 513, L // 2, L - 2, L - 1}):
         if p >= L:
@@ -380,7 +380,7 @@ def test_attend_decode_q4(hip, heads, kv, hd, L, W):
     v4 = K.kv4_quantize(vfull)
     kw = torch.zeros(kv, W, hd, device="cuda", dtype=torch.float16)
     vw = torch.zeros_like(kw)
-    ws = torch.empty(K.attend_workspace_bytes(heads, hd, L), device="cuda", dtype=torch.uint8)
+    ws = torch.zeros(K.attend_workspace_bytes(heads, hd, L), device="cuda", dtype=torch.uint8)
     grp = heads // kv
     p0 = L // 2
     last = torch.arange(max(0, p0 - W), p0, device="cuda")  # the window before the first step
