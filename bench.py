@@ -289,6 +289,8 @@ def main():
                     help="only run plain device copies of COPY_BYTES each (PMC traffic calibration)")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="only run the cfg4 prefill GEMMs a few times (for rocprofv3 counter runs)")
+    ap.add_argument("--profile-small-batch", action="store_true",
+                    help="only run cfg3's M=16 small-batch calls (down_proj, gate_up) a few times (rocprofv3 runs)")
     ap.add_argument("--decode-e2e", action="store_true",
                     help="only run the cfg5 end-to-end decode (for rocprofv3 runs); prints its JSON fields")
     args = ap.parse_args()
@@ -311,6 +313,9 @@ def main():
         return
     if args.profile_gemm:
         print(json.dumps(profile_gemm(dev)), flush=True)
+        return
+    if args.profile_small_batch:
+        print(json.dumps(profile_small_batch(L.load(), dev, args.pool_gb)), flush=True)
         return
 
     # ---- cfg2 operands
@@ -578,6 +583,25 @@ def profile_gemm(dev, iters: int = 3) -> dict:
         t = _time_eager(fn, iters)
         out[f"cfg4_gemm_k{kk}_n{nn}_us"] = round(t * 1e6, 1)
         del q4, a
+    return out
+
+
+def profile_small_batch(lib, dev, pool_gb: float, m: int = 16, reps: int = 3) -> dict:
+    """cfg3 at M=16: down_proj (K=8192, N=3072) and gate_up (K=3072, N=16384) through the
+    module dispatch over a rotated weight pool, each graph replayed ``reps`` times."""
+    out = {}
+    for name, nn, kk, seed in (("down", 3072, 8192, 31), ("gate_up", 16384, 3072, 30)):
+        q = synth_nf4(nn, kk, seed=seed)
+        P = pool_copies(q.nbytes(), pool_gb * 1e9)
+        pool = [q] + [clone_nf4(q) for _ in range(P - 1)]
+        xm = torch.randn(m, kk, generator=torch.Generator().manual_seed(seed + m)).half().to(dev)
+        ym = torch.empty(m, nn, dtype=torch.float16, device=dev)
+        calls = [Launcher(lib, operands(o), xm, ym) for o in pool]
+        nl = max(P, 60)
+        g = graph_of([calls[i % P] for i in range(nl)])
+        ts = [time_graph(g) / nl for _ in range(reps)]
+        out[f"cfg3_{name}_m{m}_us"] = round(min(ts) * 1e6, 2)
+        del q, pool, calls, g
     return out
 
 
