@@ -447,8 +447,8 @@ class SpectraDecoder(nn.Module):
         return out
 
     def _layer_decode(self, li: int, h: torch.Tensor, pos: torch.Tensor) -> None:
-        """One decoder layer for the token at device position ``pos``, six kernels: the
-        RMSNorms ride in the QKV / gate_up GEMV prologues, SiLU-mul in the down_proj prologue,
+        """One decoder layer for the token at device position ``pos``, five kernels: the
+        span merge rides in the attention kernel, the RMSNorms ride in the QKV / gate_up GEMV prologues, SiLU-mul in the down_proj prologue,
         the residual adds in the o_proj / down_proj epilogues (``h`` updated in place).
         Without NF4 linears throughout (``fused`` False) the norms and SiLU-mul are kernels
         of their own and each part of QKV / gate_up its own GEMV."""
