@@ -283,7 +283,8 @@ int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t tokens, const in
  * last of a head to finish merges the spans (log-sum-exp).  workspace: >=
  * spectra_attend_workspace(heads, head_dim, max_seq) bytes, 16-byte aligned (span partials
  * and per-head arrival counters), ZEROED before its first use (every call leaves the
- * counters at zero again); calls sharing a workspace must not overlap. */
+ * counters at zero again); calls sharing a workspace must not overlap.  A *pos outside
+ * [0, max_seq) appends nothing (the caches are left as they are) and yields NaN outputs. */
 int32_t spectra_attend_spans(int32_t max_seq);
 size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq);
 int spectra_attend_decode(const void* qkv, const int64_t* pos, const float* cos_t, const float* sin_t, int32_t heads,

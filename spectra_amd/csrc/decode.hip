@@ -365,9 +365,11 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
       vr[i] = *(const uint4*)(kvc.v + ((int64_t)kh * lmax + t) * HD + dg * 8);
     }
   }
-  int64_t pos = *pos_p;
-  pos = pos < 0 ? 0 : (pos >= lmax ? lmax - 1 : pos);
-  const int n = (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform
+  const int64_t pos = *pos_p;
+  // a position outside the cache: every span reports itself empty, so nothing is appended
+  // and the merge's 0 / 0 gives NaN outputs (rope_append likewise writes nothing)
+  const bool outside = pos < 0 || pos >= lmax;
+  const int n = outside ? 0 : (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform
   float* pbase = part + ((int64_t)kh * G * nspan + sp) * (HD + 2);  // head j: + j * nspan * (HD + 2)
   __shared__ int last_l;
   if (n <= 0) {  // span past the position: an empty piece for the merge

@@ -615,10 +615,11 @@ def kv4_dequantize(codes: torch.Tensor, scales: torch.Tensor, zeros: torch.Tenso
     d = codes.shape[-1] * 2
     rows = codes.numel() // (d // 2)
     out = torch.empty(codes.shape[:-1] + (d,), device=codes.device, dtype=torch.bfloat16)
+    # contiguous operands bound to names: a temporary copy must outlive the launch that reads it
+    codes_c, scales_c, zeros_c = codes.contiguous(), scales.contiguous(), zeros.contiguous()
     lib = L.load()
-    L.check("spectra_kv4_dequantize", lib.spectra_kv4_dequantize(codes.contiguous().data_ptr(),
-                                                                  scales.contiguous().data_ptr(),
-                                                                  zeros.contiguous().data_ptr(), rows, d,
+    L.check("spectra_kv4_dequantize", lib.spectra_kv4_dequantize(codes_c.data_ptr(), scales_c.data_ptr(),
+                                                                  zeros_c.data_ptr(), rows, d,
                                                                   out.data_ptr(), _stream(codes.device)))
     return out
 
@@ -636,8 +637,21 @@ def attend_decode_q4(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, si
     lmax = k4[0].shape[1]
     if v_window.shape != k_window.shape or kv != kv_heads or k4[0].shape != (kv, lmax, hd // 2):
         raise ValueError("windows [kv_heads, W, d] and codes [kv_heads, L, d/2] expected")
+    if qkv.numel() != (heads + 2 * kv_heads) * hd:
+        raise ValueError("qkv must hold (heads + 2 kv_heads) * d values")
     if pos.dtype != torch.int64 or pos.numel() != 1:
         raise ValueError("pos must be int64 [1]")
+    for t, name in ((cos, "cos"), (sin, "sin")):  # the kernel reads row pos of each
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.shape != (lmax, hd // 2):
+            raise ValueError(f"{name} must be contiguous fp32 [L, d/2]")
+    for cache, name in ((k4, "k4"), (v4, "v4")):  # codes, fp16 scales, uint8 zero points
+        codes, sc, zp = cache
+        if codes.shape != (kv, lmax, hd // 2) or codes.dtype != torch.uint8 or \
+                sc.shape != (kv, lmax, hd // 32) or sc.dtype != torch.float16 or \
+                zp.shape != (kv, lmax, hd // 32) or zp.dtype != torch.uint8 or \
+                not all(t.is_contiguous() and t.device == qkv.device for t in cache):
+            raise ValueError(f"{name} must be contiguous (codes uint8 [kv, L, d/2], scales fp16 and "
+                             f"zero points uint8 [kv, L, d/32]) on the qkv's device")
     need = attend_workspace_bytes(heads, hd, lmax)
     if workspace is None:  # (zeroed: the merge's arrival counters; every call leaves them at zero)
         workspace = torch.zeros(need, device=qkv.device, dtype=torch.uint8)

@@ -368,6 +368,49 @@ def test_kv4_quantize_and_dequant_reference_vectors(hip, name):
     assert np.array_equal(deq.cpu().view(torch.int16).numpy(), g[name + "_deq"])
 
 
+@pytest.mark.gpu
+@pytest.mark.parametrize("q4", [False, True])
+def test_attend_decode_position_outside_cache(hip, q4):
+    """A position outside [0, max_seq) appends nothing and gives NaN outputs; the next call
+    at a valid position is unaffected (the merge counters were left at zero)."""
+    heads, kv, hd, L, W = 8, 4, 64, 200, 32
+    g = torch.Generator(device="cuda").manual_seed(77)
+    cos, sin = _tables(L, hd)
+    ws = torch.zeros(K.attend_workspace_bytes(heads, hd, L), device="cuda", dtype=torch.uint8)
+    if q4:
+        k4 = K.kv4_quantize(torch.randn(kv, L, hd, device="cuda", generator=g).half())
+        v4 = K.kv4_quantize(torch.randn(kv, L, hd, device="cuda", generator=g).half())
+        kc = torch.randn(kv, W, hd, device="cuda", generator=g).half()
+        vc = torch.randn(kv, W, hd, device="cuda", generator=g).half()
+        state = [kc, vc, *k4, *v4]
+        run = lambda qkv, pos: K.attend_decode_q4(qkv, pos, cos, sin, heads, kv, kc, vc, k4, v4, ws)
+    else:
+        kc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+        vc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+        state = [kc, vc]
+        run = lambda qkv, pos: K.attend_decode(qkv, pos, cos, sin, heads, kv, kc, vc, ws)
+    for p in (L, L + 5, -1):
+        case(q4=q4, pos=p)
+        before = [t.clone() for t in state]
+        qkv = torch.randn((heads + 2 * kv) * hd, device="cuda", generator=g).half()
+        out = run(qkv, torch.tensor([p], device="cuda", dtype=torch.int64))
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(state, before)), f"pos={p}: the cache changed"
+        assert torch.isnan(out.float()).all(), f"pos={p}: outputs are not NaN"
+    # a valid position afterwards: the same outputs as on a fresh workspace
+    case(q4=q4, pos=L - 1)
+    qkv = torch.randn((heads + 2 * kv) * hd, device="cuda", generator=g).half()
+    pos = torch.tensor([L - 1], device="cuda", dtype=torch.int64)
+    before = [t.clone() for t in state]
+    out = run(qkv, pos).clone()
+    for t, b in zip(state, before):
+        t.copy_(b)
+    ws.zero_()
+    ref = run(qkv, pos)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("heads,kv,hd,L,W", [(24, 8, 128, 300, 128), (8, 2, 64, 200, 16), (6, 3, 256, 130, 64),
                                               (8, 4, 32, 100, 16)])
 def test_attend_decode_q4(hip, heads, kv, hd, L, W):
