@@ -389,6 +389,10 @@ def main():
                      "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                      "traffic_source": traffic_note, "algorithmic_bytes_per_launch": b_down,
                      "avg_launch_us": round(t_down * 1e6, 3)},
+        # the bars the -m gpu parity tests hold these kernels to (tests/test_gpu_parity.py)
+        "parity": {"fp16_out": "max-abs <= max(1e-2, 1 fp16 ulp of |y|), rel-L2 <= 1e-3 vs fp64(x_rot) . fp64(W_eff)",
+                   "bf16_out": "max-abs <= 1 bf16 ulp + 1e-2, rel-L2 <= 5e-3",
+                   "w_eff_quantizers_fwht": "bit-exact", "replay_check": "graph output equals an eager launch"},
     }
     detail = {"qkv_gemv_us": round(t_qkv * 1e6, 3), "qkv_gemv_GBps": round(b_qkv / t_qkv / 1e9, 1),
               "down_gemv_us": round(t_down * 1e6, 3), "down_gemv_GBps": round(achieved, 1)}
