@@ -288,9 +288,11 @@ __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& 
   if (p.res != nullptr && ptid < c.Rw) ((uint16_t*)(smem + p.off_res))[ptid] = r.res_raw;
 }
 
-// row-wave loads: the weight runs of every slot, then the CSR entries of the group's rows
+// row-wave loads: the CSR entries of the group's rows, then the weight runs of every slot
 // (lane li stages entry e0 + li of each row; lanes past the row's entries, and arrays
-// without entries, read a dummy word: entry 0, or the workgroup's first weight word)
+// without entries, read a dummy word: entry 0, or the workgroup's first weight word).  The
+// few entry loads go first so that they land with the first weight runs rather than behind
+// the last (measured: gate_up N=16384 9.13 -> 8.78 us, the other decoder shapes unchanged).
 template <int G, int SPR, int RPG>
 struct RowRegs {
   uint4 wq[SPR * RPG];
@@ -304,14 +306,6 @@ __device__ __forceinline__ void rows_row_loads(const RowsParams& p, const RowsCt
   constexpr int NS = SPR * RPG;
   const uint8_t* wbase = p.packed + (int64_t)c.r0 * p.ldp;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int j = s / SPR, ch = s % SPR;
-    const int row = c.grow0 + j;
-    const uint32_t o = row < c.Rw ? (uint32_t)(row * p.ldp) + (uint32_t)(ch * G + c.li) * 16u : 0u;  // dummy: one line
-    r.wq[s] = load_nt_u4(wbase + o);
-  }
-  asm volatile("" ::: "memory");  // the CSR entries are issued behind every weight run
-#pragma unroll
   for (int j = 0; j < RPG; ++j) {
     const int a = G == 32 ? ((c.lane >> 5) ? sx[RPG + j] : sx[j]) : sx[j];
     const int b = G == 32 ? ((c.lane >> 5) ? sx[RPG + j + 1] : sx[j + 1]) : sx[j + 1];
@@ -323,6 +317,14 @@ __device__ __forceinline__ void rows_row_loads(const RowsParams& p, const RowsCt
     const uint32_t e = ok ? (uint32_t)(a + c.li) : 0u;
     r.ocol[j] = load_at<int>(cb, 4u * e);
     r.oval[j] = load_at<uint16_t>(vb, 2u * e);
+  }
+  asm volatile("" ::: "memory");  // the weight runs are issued behind the CSR entries
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int j = s / SPR, ch = s % SPR;
+    const int row = c.grow0 + j;
+    const uint32_t o = row < c.Rw ? (uint32_t)(row * p.ldp) + (uint32_t)(ch * G + c.li) * 16u : 0u;  // dummy: one line
+    r.wq[s] = load_nt_u4(wbase + o);
   }
 }
 
