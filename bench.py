@@ -417,9 +417,30 @@ def main():
 
 COPY_BYTES = 16 << 20  # plain copy of known size: FETCH_SIZE / WRITE_SIZE scale factors
 
-# The sources that fix the measured kernel's memory traffic (kernel body and its launch plan).
-TRAFFIC_SOURCES = ("spectra_amd/csrc/gemv_rows.h", "spectra_amd/csrc/gemv_rows_inst.h", "spectra_amd/csrc/gemv_rows_plain.hip",
-                   "spectra_amd/csrc/gemv.hip", "spectra_amd/csrc/common.h")
+# The translation units that fix the measured kernel's memory traffic (the kernel's
+# instantiation and its launch plan); the hash covers them and every header they include.
+TRAFFIC_ROOTS = ("spectra_amd/csrc/gemv_rows_plain.hip", "spectra_amd/csrc/gemv.hip")
+
+
+def include_closure(roots) -> list:
+    """The files ``roots`` name and every local header they include, directly or through
+    other headers (``#include "..."`` resolved next to the including file, else in
+    ``include/``, the library's public header directory)."""
+    import re
+    seen, todo = [], list(roots)
+    while todo:
+        rel = os.path.normpath(todo.pop())
+        if rel in seen:
+            continue
+        seen.append(rel)
+        with open(os.path.join(ROOT, rel)) as f:
+            for inc in re.findall(r'^\s*#\s*include\s+"([^"]+)"', f.read(), re.M):
+                near = os.path.join(os.path.dirname(rel), inc)
+                todo.append(near if os.path.exists(os.path.join(ROOT, near)) else os.path.join("include", inc))
+    return sorted(seen)
+
+
+TRAFFIC_SOURCES = tuple(include_closure(TRAFFIC_ROOTS))
 
 
 def kernel_source_hash() -> str:

@@ -11,7 +11,12 @@ numpy oracle (whose own pins are listed in ``oracle/__init__.py``); ``linear_a``
 ``linear_b`` agree with ``spectra_oracle.linear_ref`` to float32 rounding; the decoder
 pieces satisfy closed forms (RoPE preserves norms and rotates by the position's angles,
 attention over one position returns its value row, RMSNorm of a constant row is the norm
-weight) and ``Decoder`` is checked against the GPU decoder in ``tests/test_decoder.py``.
+weight); ``Decoder`` and ``rope_inv_freq`` reproduce Hugging Face's ``LlamaForCausalLM``
+(the reference engine's model class, engine.py:919-939) on a tiny grouped-query Llama, for
+the unscaled and the llama3-scaled RoPE table: logits of a 96-token prefill and 4 decode
+steps, greedy tokens and the inverse-frequency tables (fixture
+``tests/golden/llama_hf_decode.npz``, written by ``tests/golden/make_llama_golden.py``).
+``Decoder`` is then the checker of the GPU decoder in ``tests/test_decoder.py``.
 """
 from __future__ import annotations
 
@@ -22,7 +27,8 @@ import torch
 
 from .spectra_oracle import NF4_CODEBOOK
 
-__all__ = ["nf4_dequant", "fwht_blocks", "linear_a", "linear_b", "rms_norm", "rope", "attention", "Decoder"]
+__all__ = ["nf4_dequant", "fwht_blocks", "linear_a", "linear_b", "rms_norm", "rope", "rope_inv_freq", "attention",
+           "Decoder"]
 
 _CODES = torch.from_numpy(NF4_CODEBOOK.copy())  # compressor.py:22-27, float32
 
@@ -93,6 +99,35 @@ def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
 
 
+def rope_inv_freq(head_dim: int, theta: float, scaling: Optional[dict] = None) -> torch.Tensor:
+    """Inverse RoPE frequencies theta^(-2i/d), i < d/2, as float32.  ``scaling`` with
+    ``rope_type: llama3`` applies Llama 3.1's published frequency scaling, element by element
+    in float64: wavelength w = 2 pi / f; w below original_context / high_freq_factor keeps f,
+    w above original_context / low_freq_factor takes f / factor, between them
+    f ((1 - s) / factor + s) with s = (original_context / w - low) / (high - low)."""
+    base = (torch.arange(0, head_dim, 2, dtype=torch.int64).to(torch.float32) / head_dim)
+    inv = 1.0 / (theta ** base)
+    kind = (scaling or {}).get("rope_type", (scaling or {}).get("type", "default"))
+    if kind == "default":
+        return inv
+    if kind != "llama3":
+        raise ValueError(f"rope_type {kind!r} is not restated here")
+    factor = float(scaling["factor"])
+    lo, hi = float(scaling["low_freq_factor"]), float(scaling["high_freq_factor"])
+    ctx = float(scaling["original_max_position_embeddings"])
+    out = []
+    for f in inv.tolist():
+        w = 2.0 * math.pi / f
+        if w < ctx / hi:
+            out.append(f)
+        elif w > ctx / lo:
+            out.append(f / factor)
+        else:
+            s = (ctx / w - lo) / (hi - lo)
+            out.append((1.0 - s) * f / factor + s * f)
+    return torch.tensor(out, dtype=torch.float64).to(torch.float32)
+
+
 def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
     """Rotary embedding, half-split (Llama's rotate_half): x [T, H, d], cos/sin [T, d/2]."""
     h2 = x.shape[-1] // 2
@@ -121,18 +156,19 @@ class Decoder:
     (layers[i] = (W_qkv, W_o, W_gate_up, W_down), each float32 [N, K] in the rotated basis
     with its Hadamard block ``had[i]``), RMSNorm, RoPE, grouped-query attention over a
     growing KV cache, SiLU-mul; ``norms`` holds 2 per layer then the final one; the logits
-    come from ``head`` (float32 [vocab, hidden])."""
+    come from ``head`` (float32 [vocab, hidden]).  ``rope_scaling``: the config's RoPE
+    parameters (``rope_inv_freq``); None for the unscaled table."""
 
     def __init__(self, layers: Sequence[Sequence[torch.Tensor]], had: Sequence[Sequence[int]], norms: List[torch.Tensor],
                  emb: torch.Tensor, head: torch.Tensor, *, heads: int, kv_heads: int, rope_theta: float,
-                 rms_eps: float, max_seq: int):
+                 rms_eps: float, max_seq: int, rope_scaling: Optional[dict] = None):
         self.layers, self.had, self.norms, self.emb, self.head = layers, had, norms, emb, head
         self.heads, self.kv_heads, self.eps = heads, kv_heads, rms_eps
         self.hidden = emb.shape[1]
         self.hd = self.hidden // heads
         self.inter = layers[0][2].shape[0] // 2
         dev = emb.device
-        inv = 1.0 / (rope_theta ** (torch.arange(0, self.hd, 2, device=dev, dtype=torch.float32) / self.hd))
+        inv = rope_inv_freq(self.hd, rope_theta, rope_scaling).to(dev)
         ang = torch.arange(max_seq, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)
         self.k: List[torch.Tensor] = []

@@ -9,6 +9,7 @@ HIP graph.  Format B operands arrive through keyword-only arguments.
 from __future__ import annotations
 
 import math
+import warnings
 from dataclasses import dataclass
 from typing import Optional
 
@@ -19,7 +20,7 @@ from .kernels import (GEMV_MAX_M, QWeightOperands, argmax_slots, attend_decode, 
                       attend_workspace_bytes, greedy_finish, greedy_next, kv4_quantize, rmsnorm, rope_append, silu_mul,
                       w4_embedding, w4a16_gemv_fused, w4a16_linear)
 
-__all__ = ["SpectraFusedLinear", "SpectraFusedEmbedding", "DecoderConfig", "SpectraDecoder"]
+__all__ = ["SpectraFusedLinear", "SpectraFusedEmbedding", "DecoderConfig", "SpectraDecoder", "rope_inv_freq"]
 
 
 def _block(group_size: Optional[int], codebook: str) -> int:
@@ -195,10 +196,37 @@ class DecoderConfig:
     hadamard_block: int = 128
     outlier_ratio: float = 0.005
     seed: int = 0
+    rope_scaling: Optional[dict] = None  # the RoPE parameters ``rope_inv_freq`` applies; None: unscaled
 
     @property
     def head_dim(self) -> int:
         return self.hidden // self.heads
+
+
+def rope_inv_freq(head_dim: int, theta: float, scaling: Optional[dict] = None) -> torch.Tensor:
+    """float32 inverse RoPE frequencies theta^(-2i/d) for i < d/2 (transformers' default table,
+    which the reference's loader installs in every rotary module: engine.py:1172-1179).
+    ``scaling`` with ``rope_type`` ``llama3`` applies the Llama 3.1 frequency scaling: with
+    wavelength w = 2 pi / f, frequencies whose w is shorter than original_context /
+    high_freq_factor stay, those longer than original_context / low_freq_factor are divided
+    by ``factor``, and between them s = (original_context / w - low) / (high - low) blends
+    f / factor and f.  Any other ``rope_type`` raises ``ValueError``."""
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+    kind = (scaling or {}).get("rope_type", (scaling or {}).get("type", "default"))
+    if kind == "default":
+        return inv
+    if kind != "llama3":
+        raise ValueError(f"rope_type {kind!r} is not supported (default and llama3 are)")
+    try:
+        factor, lo, hi = float(scaling["factor"]), float(scaling["low_freq_factor"]), float(scaling["high_freq_factor"])
+        ctx = float(scaling["original_max_position_embeddings"])
+    except KeyError as e:
+        raise ValueError(f"llama3 rope parameters lack {e.args[0]!r}") from None
+    wavelen = (2.0 * math.pi) / inv
+    blend = ((ctx / wavelen - lo) / (hi - lo)).clamp(0.0, 1.0)
+    scaled = inv / factor
+    return torch.where(wavelen < ctx / hi, inv,
+                       torch.where(wavelen > ctx / lo, scaled, (1.0 - blend) * scaled + blend * inv))
 
 
 def _synthetic_nf4(n: int, k: int, gen: torch.Generator, had: int, ratio: float, dev) -> "NF4Weight":
@@ -303,7 +331,7 @@ class SpectraDecoder(nn.Module):
                         torch.zeros(c.layers, c.kv_heads, c.max_seq, hd // 32, device=dev, dtype=torch.float16),
                         torch.zeros(c.layers, c.kv_heads, c.max_seq, hd // 32, device=dev, dtype=torch.uint8))
             self.k4, self.v4 = q4(), q4()
-        inv = 1.0 / (c.rope_theta ** (torch.arange(0, hd, 2, device=dev, dtype=torch.float32) / hd))
+        inv = rope_inv_freq(hd, c.rope_theta, c.rope_scaling).to(dev)
         ang = torch.arange(c.max_seq, device=dev, dtype=torch.float32)[:, None] * inv[None, :]
         self.cos, self.sin = torch.cos(ang), torch.sin(ang)  # [max_seq, hd/2]
         self.arange = torch.arange(c.max_seq, device=dev)
@@ -336,25 +364,45 @@ class SpectraDecoder(nn.Module):
         return dict(layers=layers, embed=embed, lm_head=None, norms=norms)
 
     @classmethod
-    def from_trdc(cls, path, device: Optional[torch.device] = None, max_seq: int = 1024) -> "SpectraDecoder":
+    def from_trdc(cls, path, device: Optional[torch.device] = None, max_seq: int = 1024,
+                  rope: str = "reference") -> "SpectraDecoder":
         """A decoder on the quantized tensors of a TRDC container (engine.py:798-1080 binds a
         container's tensors to the model's modules by name): HF Llama names, norms from the
         lossless tensors, lm_head tied to the embedding when the container has none.
         Format B (``nf4_*``) q/k/v and gate/up are concatenated along N at load (exact: every
         Format B operand is row-local); Format A (``q4_g32_hdsq``) parts stay separate
-        linears, since their dense outlier columns are per tensor."""
+        linears, since their dense outlier columns are per tensor.
+
+        ``rope``: ``"reference"`` decodes with the unscaled table of the config's
+        ``rope_theta`` whatever ``rope_type`` the config names, as the reference's loader
+        does (engine.py:1170-1179 replaces every rotary module's table by
+        ``compute_default_rope_parameters``), and warns when the config names a scaling;
+        ``"config"`` applies the config's scaling (``rope_inv_freq``: llama3; other types
+        raise ``ValueError``)."""
         from .compressor import NF4Weight
         from .container import FORMAT_A, TrdcReader, nf4_concat
+        if rope not in ("reference", "config"):
+            raise ValueError("rope must be 'reference' or 'config'")
         dev = device or torch.device("cuda")
         with TrdcReader(path) as rd:
             cf = rd.config
-            rp = cf.get("rope_parameters") or {}
+            rp = cf.get("rope_parameters") or cf.get("rope_scaling") or {}
             theta = cf.get("rope_theta") or rp.get("rope_theta") or 10000.0
+            kind = rp.get("rope_type", rp.get("type", "default"))
+            scaling = None
+            if kind != "default":
+                if rope == "config":
+                    scaling = dict(rp)
+                    rope_inv_freq(2, 1.0, scaling)  # unsupported types and missing keys raise here
+                else:
+                    warnings.warn(f"container config names rope_type {kind!r}; decoding with the unscaled "
+                                  "table as the reference's loader does (from_trdc(..., rope='config') "
+                                  "applies the scaling)", stacklevel=2)
             c = DecoderConfig(layers=cf["num_hidden_layers"], hidden=cf["hidden_size"],
                               heads=cf["num_attention_heads"],
                               kv_heads=cf.get("num_key_value_heads") or cf["num_attention_heads"],
                               inter=cf["intermediate_size"], vocab=cf["vocab_size"],
-                              rope_theta=float(theta),
+                              rope_theta=float(theta), rope_scaling=scaling,
                               rms_eps=float(cf.get("rms_norm_eps") or 1e-6), max_seq=max_seq)
             if cf.get("head_dim") not in (None, c.head_dim):
                 raise ValueError(f"head_dim {cf.get('head_dim')} != hidden / heads ({c.head_dim})")

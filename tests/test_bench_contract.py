@@ -41,8 +41,23 @@ def test_traffic_only_from_the_sources_it_was_measured_on(monkeypatch):
 
 
 def test_traffic_hash_covers_the_kernel_sources():
+    """Every header the measured kernel's translation units include, directly or through
+    other headers, is hashed (found here by a scan of its own, not bench's)."""
     import bench
+    import re
     for rel in bench.TRAFFIC_SOURCES:
         assert os.path.exists(os.path.join(ROOT, rel)), rel
-    assert any(rel.endswith("gemv_rows.h") for rel in bench.TRAFFIC_SOURCES)
+    csrc = os.path.join(ROOT, "spectra_amd", "csrc")
+    todo, found = ["gemv_rows_plain.hip", "gemv.hip"], set()
+    while todo:
+        name = todo.pop()
+        if name in found:
+            continue
+        found.add(name)
+        path = os.path.join(csrc, name)
+        with open(path if os.path.exists(path) else os.path.join(ROOT, "include", name)) as f:
+            todo += re.findall(r'#include "([^"]+)"', f.read())
+    hashed = {os.path.basename(rel) for rel in bench.TRAFFIC_SOURCES}
+    assert found <= hashed, found - hashed
+    assert {"gemv_rows.h", "gemv_stream.h", "gemv_kernel.h", "common.h"} <= hashed
     assert bench.kernel_source_hash() == bench.kernel_source_hash()

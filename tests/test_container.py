@@ -253,6 +253,61 @@ def test_nf4_container_roundtrip_and_decoder(hip, tmp_path, monkeypatch):
         assert int(dec.cur_id) == toks[-1]
 
 
+LLAMA3_ROPE = dict(rope_type="llama3", rope_theta=10000.0, factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                   original_max_position_embeddings=32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rope", ["reference", "config"])
+def test_from_trdc_rope_scaling(hip, tmp_path, monkeypatch, rope):
+    """A container whose config names llama3 RoPE scaling (original context 32, so a 48-token
+    prompt reaches the scaled frequencies).  ``rope='reference'`` decodes with the unscaled
+    table as the reference's loader does (engine.py:1170-1179) and warns; ``rope='config'``
+    applies the scaling.  Each against the fp32 restatement with its table (the restatement's
+    tables and wiring are pinned to transformers' LlamaForCausalLM on the CPU), and the two
+    tables' logits apart by more than the bar."""
+    import golden.make_trdc_golden as G
+    from oracle import torch_ref as TR
+    from spectra_amd.engine import SpectraDecoder
+    from test_decoder import RefDecoder
+
+    cfg = {k: v for k, v in DEC.items() if k != "rope_theta"}
+    cfg["rope_parameters"] = dict(LLAMA3_ROPE)
+    monkeypatch.setattr(G, "TINY", cfg)
+    ck = tmp_path / "ck"
+    make_checkpoint(str(ck), seed=12)
+    out = tmp_path / "r.trdc"
+    T.compress_checkpoint(ck, out, fmt="nf4", hadamard_block=128, csr_ratio=0.01)
+    case = f"case: rope {rope}"
+    print(case, flush=True)
+    if rope == "reference":
+        with pytest.warns(UserWarning, match="llama3"):
+            dec = SpectraDecoder.from_trdc(out, max_seq=64)
+        assert dec.cfg.rope_scaling is None
+    else:
+        dec = SpectraDecoder.from_trdc(out, max_seq=64, rope="config")
+        assert dec.cfg.rope_scaling["rope_type"] == "llama3"
+    ref = RefDecoder(dec)
+    other = RefDecoder(dec)
+    c = dec.cfg
+    other.dec = TR.Decoder(other.w, other.had, other.norm, other.emb, other.head, heads=c.heads, kv_heads=c.kv_heads,
+                           rope_theta=c.rope_theta, rms_eps=c.rms_eps, max_seq=c.max_seq,
+                           rope_scaling=None if c.rope_scaling else dict(LLAMA3_ROPE))
+    prompt = torch.randint(0, cfg["vocab_size"], (48,), generator=torch.Generator().manual_seed(4)).cuda()
+    lg = dec.prefill(prompt).float()
+    lr, lo = ref.forward(prompt, 0), other.forward(prompt, 0)
+    tol = 1e-2 * lr.abs().max().item()
+    assert (lg - lr).abs().max().item() <= tol
+    assert (lo - lr).abs().max().item() > 3 * tol  # the tables are told apart at these positions
+    dec.capture_decode()
+    for step in range(2):
+        tok = int(dec.cur_id)
+        assert tok == int(torch.argmax(lr)) or (lr.max() - lr.reshape(-1)[tok]).item() <= 2 * tol
+        dec.graph.replay()
+        lr = ref.forward(torch.tensor([tok], device="cuda"), prompt.numel() + step)
+        assert (dec.graph_logits.float() - lr).abs().max().item() <= 1e-2 * lr.abs().max().item()
+
+
 def _format_a_w_eff(q, dtype="float32"):
     """W_eff of a Format A tensor: (q - z) * s, then the outlier columns (oracle dequant)."""
     w = O.dequant_group32(q.packed.cpu().numpy(), q.scales.cpu().numpy(), q.zeros.cpu().numpy(), q.marlin_layout,

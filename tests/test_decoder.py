@@ -92,7 +92,8 @@ class RefDecoder:
         self.head = _w_eff(dec.lm_q)
         self.norm = [w.float() for w in dec.norm_w]
         self.dec = TR.Decoder(self.w, self.had, self.norm, self.emb, self.head, heads=c.heads, kv_heads=c.kv_heads,
-                              rope_theta=c.rope_theta, rms_eps=c.rms_eps, max_seq=c.max_seq)
+                              rope_theta=c.rope_theta, rms_eps=c.rms_eps, max_seq=c.max_seq,
+                              rope_scaling=c.rope_scaling)
 
     def forward(self, ids, pos0):
         return self.dec.forward(ids, pos0)

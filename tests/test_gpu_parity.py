@@ -432,11 +432,34 @@ def test_gemm_split_k_outliers_across_splits(hip, m):
 # ---------------------------------------------------------------------------
 # BASELINE shapes (configs 1-3) at full size, M=1..16, against the oracle
 # ---------------------------------------------------------------------------
+def _sampled_rows_bitexact(q, w, mask, out_dtype):
+    """Rows 0, 1, N/2 and N-1 of a full-size quantization: packed codes, absmax, CSR and
+    W_eff (dequantized by the HIP kernel in ``out_dtype``) bit-identical to the oracle's
+    quantizer and dequant run on the same source rows."""
+    n = w.shape[0]
+    rows = np.array([0, 1, n // 2, n - 1])
+    wn = w.numpy()[rows]
+    mk = mask.numpy()[rows] if mask is not None else None
+    sub = O.nf4_quantize(wn, "float16", 64, 0, mk, True)
+    assert np.array_equal(host(q.packed)[rows], sub["packed"]) and np.array_equal(host(q.absmax)[rows], sub["absmax"])
+    rp = host(q.rowptr).astype(np.int64)
+    for i, r in enumerate(rows):
+        assert np.array_equal(host(q.col)[rp[r]:rp[r + 1]], sub["col"][sub["rowptr"][i]:sub["rowptr"][i + 1]])
+        assert np.array_equal(host(q.val)[rp[r]:rp[r + 1]].view(np.uint16),
+                              sub["val"][sub["rowptr"][i]:sub["rowptr"][i + 1]].view(np.uint16))
+    w_eff = K.w4_dequant(q.packed, q.absmax, None, out_dtype=TDT[out_dtype], codebook="nf4", marlin_layout=True,
+                         outlier_idx=q.col if q.col.numel() else None, outlier_w=q.val if q.col.numel() else None,
+                         outlier_rowptr=q.rowptr if q.col.numel() else None)
+    ref = O.nf4_dequant(sub["packed"], sub["absmax"], True, out_dtype, sub["rowptr"], sub["col"], sub["val"])
+    assert np.array_equal(host(w_eff)[rows], ref)  # bf16 compares as bit patterns on both sides
+    return w_eff
+
+
 @pytest.mark.parametrize("name,n,k,had,ratio,ms", [
     ("cfg1", 4096, 4096, 0, 0.0, (1,)),
     ("cfg2_qkv", 5120, 3072, 128, 0.005, (1,)),
-    ("cfg2_down", 3072, 8192, 128, 0.005, (1, 4, 16)),
-    ("cfg3_gate_up", 16384, 3072, 128, 0.005, (2, 4, 8)),
+    ("cfg2_down", 3072, 8192, 128, 0.005, (1, 4, 8, 16)),
+    ("cfg3_gate_up", 16384, 3072, 128, 0.005, (2, 4, 8, 16)),
 ])
 def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
     g = torch.Generator().manual_seed(0)
@@ -452,9 +475,7 @@ def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
         mask = mask.view(n, k)
     q = C.quantize_nf4(w.cuda(), 64, 0, mask.cuda() if mask is not None else None, True)
     # the full-size quantizer and dequant agree bit for bit with the oracle on sampled rows
-    rows = np.array([0, 1, n // 2, n - 1])
-    sub = O.nf4_quantize(w.numpy()[rows], "float16", 64, 0, mask.numpy()[rows] if mask is not None else None, True)
-    assert np.array_equal(host(q.packed)[rows], sub["packed"]) and np.array_equal(host(q.absmax)[rows], sub["absmax"])
+    _sampled_rows_bitexact(q, w, mask, "float16")
     w_eff_t = K.w4_dequant(q.packed, q.absmax, None, codebook="nf4", marlin_layout=True,
                            outlier_idx=q.col if q.col.numel() else None, outlier_w=q.val if q.col.numel() else None,
                            outlier_rowptr=q.rowptr if q.col.numel() else None)
@@ -501,9 +522,13 @@ def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     x = torch.randn(m, k, generator=g).bfloat16().cuda()
     y = K.batched_w4a16_gemm(x, q.packed, q.absmax, None, outlier_idx=q.col, outlier_w=q.val, marlin_layout=True,
                              **q.kernel_kwargs() | dict(hadamard_block=128))
-    w_eff = K.w4_dequant(q.packed, q.absmax, None, out_dtype=torch.float32, codebook="nf4", marlin_layout=True,
-                         outlier_idx=q.col, outlier_w=q.val, outlier_rowptr=q.rowptr)
+    # the reference's operands are the oracle's on sampled rows: quantized codes, CSR and W_eff
+    # (float32 and bf16) bit for bit, and the rotated activations
+    w_eff = _sampled_rows_bitexact(q, w, mask.view(n, k), "float32")
+    _sampled_rows_bitexact(q, w, mask.view(n, k), "bfloat16")
     x_rot = K.fwht_rows(x, 128, out_dtype=torch.float32)
+    xr = np.array([0, m // 2, m - 1])
+    assert np.array_equal(host(x_rot)[xr], O.rotate_blocks(O.to_f32(host(x)[xr], "bfloat16"), 128))
     y_t = (x_rot @ w_eff.float().T).double().cpu().numpy()
     check_y(y, y_t, torch.bfloat16)
 

@@ -445,3 +445,77 @@ def test_torch_ref_decoder_pieces_closed_forms():
     # RMSNorm of a constant row is the norm weight (eps negligible)
     wn = torch.rand(32, generator=g)
     assert torch.allclose(TR.rms_norm(torch.full((1, 32), 3.5), wn, 1e-12), wn[None, :], rtol=1e-6)
+
+
+# ----------------------------------------------------------------------------
+# oracle/torch_ref.Decoder against Hugging Face's LlamaForCausalLM (the reference engine's
+# model class, engine.py:919-939): fixture written by tests/golden/make_llama_golden.py
+# ----------------------------------------------------------------------------
+sys.path.insert(0, HERE)
+from golden import make_llama_golden as LG  # noqa: E402
+
+
+def _hf_fixture():
+    g = np.load(os.path.join(HERE, "golden", "llama_hf_decode.npz"))
+    sd = LG.llama_state_dict()
+    assert str(g["weights_sha256"]) == LG.weights_sha256(sd), "regenerated weights differ from the fixture's"
+    return g, sd
+
+
+def _tr_decoder(sd, scaling):
+    c = LG.TINY
+    L = c["num_hidden_layers"]
+    layers, norms = [], []
+    for i in range(L):
+        p = f"model.layers.{i}."
+        a, m = p + "self_attn.", p + "mlp."
+        layers.append((torch.cat([sd[a + "q_proj.weight"], sd[a + "k_proj.weight"], sd[a + "v_proj.weight"]]),
+                       sd[a + "o_proj.weight"],
+                       torch.cat([sd[m + "gate_proj.weight"], sd[m + "up_proj.weight"]]),
+                       sd[m + "down_proj.weight"]))
+        norms += [sd[p + "input_layernorm.weight"], sd[p + "post_attention_layernorm.weight"]]
+    norms.append(sd["model.norm.weight"])
+    return TR.Decoder(layers, [(0, 0, 0, 0)] * L, norms, sd["model.embed_tokens.weight"], sd["lm_head.weight"],
+                      heads=c["num_attention_heads"], kv_heads=c["num_key_value_heads"], rope_theta=LG.THETA,
+                      rms_eps=c["rms_norm_eps"], max_seq=LG.PROMPT_LEN + LG.DECODE_STEPS + 1, rope_scaling=scaling)
+
+
+@pytest.mark.parametrize("rope", ["default", "llama3"])
+def test_torch_decoder_matches_hf_llama(rope):
+    """Prefill of 96 tokens then 4 greedy decode steps: logits within 1e-4 of the logit scale
+    (both float32; the summation orders differ) and the same greedy tokens.  The two RoPE
+    tables give logits apart by far more than the bar (the fixture's script checks it), so
+    a wrong table, a missing final norm, a swapped residual or the wrong KV head fails."""
+    g, sd = _hf_fixture()
+    dec = _tr_decoder(sd, None if rope == "default" else dict(LG.LLAMA3))
+    ref_logits, ref_toks = g[f"logits_{rope}"], g[f"tokens_{rope}"]
+    ids = torch.from_numpy(g["prompt"])
+    lg = dec.forward(ids, 0)
+    for step in range(LG.DECODE_STEPS + 1):
+        ref = ref_logits[step]
+        got = lg.reshape(-1).numpy()
+        assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max(), (step, np.abs(got - ref).max())
+        assert int(np.argmax(got)) == int(ref_toks[step])
+        if step < LG.DECODE_STEPS:
+            lg = dec.forward(torch.tensor([int(ref_toks[step])]), LG.PROMPT_LEN + step)
+
+
+def test_rope_tables_match_transformers():
+    """The oracle's and the product's inverse-frequency tables against transformers' own:
+    the unscaled table, the llama3-scaled one (within 2 float32 ulp: the blend's rounding
+    order is not transformers'), and what the reference's loader installs for a llama3
+    config (engine.py:1172-1179: the unscaled table)."""
+    from spectra_amd.engine import rope_inv_freq
+    g, _ = _hf_fixture()
+    hd = LG.TINY["hidden_size"] // LG.TINY["num_attention_heads"]
+    assert np.array_equal(g["inv_reference_reinit"], g["inv_default"])
+    for fn in (TR.rope_inv_freq, rope_inv_freq):
+        assert np.array_equal(fn(hd, LG.THETA).numpy(), g["inv_default"])
+        got = fn(hd, LG.THETA, dict(LG.LLAMA3)).numpy()
+        ref = g["inv_llama3"]
+        assert np.all(np.abs(got - ref) <= 2 * np.spacing(ref)), (got, ref)
+        assert not np.array_equal(got, g["inv_default"])
+        with pytest.raises(ValueError):
+            fn(hd, LG.THETA, dict(rope_type="yarn", factor=4.0))
+    with pytest.raises(ValueError):
+        rope_inv_freq(hd, LG.THETA, dict(rope_type="llama3", factor=8.0))  # keys missing
