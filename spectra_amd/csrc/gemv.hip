@@ -210,7 +210,7 @@ static int stream_launch(const spectra_qweight_t* w, const StreamPlan& pl, const
 struct RowsPlan {
   int G, SPR, RPG, XC, W, WR, R, grid, nchunk, cpr;
   bool split;
-  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res, off_flag, lds_bytes;
+  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res, lds_bytes;
 };
 
 static gemv_rows_fn rows_fn(int g, int spr, int rpg, int xc, bool split, bool bf, int pro) {
@@ -277,8 +277,6 @@ static bool plan_rows(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block,
   off = align16(off + (uint32_t)(R * 4));
   pl->off_res = off;
   off = align16(off + (uint32_t)(R * 2));
-  pl->off_flag = off;
-  off = align16(off + 8u);  // two counters
   pl->lds_bytes = off;
   return off <= 163840;
 }
@@ -321,7 +319,7 @@ static int rows_launch(const spectra_qweight_t* w, const RowsPlan& pl, const voi
   p.cpr = pl.cpr;
   p.cmagic = (65536 + pl.cpr - 1) / pl.cpr;
   p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_sc = pl.off_sc; p.off_ss = pl.off_ss;
-  p.off_bias = pl.off_bias; p.off_res = pl.off_res; p.off_flag = pl.off_flag;
+  p.off_bias = pl.off_bias; p.off_res = pl.off_res;
   p.wr = pl.WR;
   const gemv_rows_fn fn = rows_fn(pl.G, pl.SPR, pl.RPG, pl.XC, pl.split, act_dtype == SPECTRA_BF16, kpro);
   const int st = ensure_lds_limit((const void*)fn, true);

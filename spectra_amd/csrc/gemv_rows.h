@@ -39,6 +39,8 @@
 //    v_perm + ds_read_b32 + v_dot2_f32_f16 per packed byte.
 #pragma once
 
+#include <type_traits>
+
 #include "gemv_stream.h"  // shared helpers: load_nt_u4, pack_scaled, xs_pos
 
 namespace spectra {
@@ -70,10 +72,14 @@ struct RowsParams {
   int cpr;             // 16-byte absmax chunks per row (K / block / 8)
   int cmagic;          // ceil(65536 / cpr): t / cpr == (t * cmagic) >> 16 for t < 1024
   int wr;              // row waves (waves wr .. W-1 are producers when split)
-  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res, off_flag;
+  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res;
 };
 
 constexpr int kRowsSpinLimit = 1 << 20;  // s_sleep rounds a row wave waits for the producers, at most
+// LDS byte offset of the producers' two counters: the unused upper half of the nibble-pair
+// LUT's first 256-byte row (the 32 copies fill bytes 0..127 of each row), a constant so
+// that zeroing them waits for no kernel argument
+constexpr uint32_t kRowsCounterOff = 128;
 
 typedef _Float16 rh8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 rb8_t __attribute__((ext_vector_type(8)));
@@ -188,86 +194,124 @@ __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& 
     }
   }
   float ssq = 0.0f;
-  // one rolled loop over the chunks: its code is fetched once (a cold instruction cache costs
-  // more than the selects that pick the chunk's registers; all chunks land together)
-  uint4 xq[XC], uq[PRO == kProSiluMul ? XC : 1], nq[PRO == kProRms ? XC : 1];
+  // every chunk's operand and MFMAs first, then the per-chunk VALU work: the XC chains are
+  // independent, so their latencies overlap (chunks past the last one compute on the dummy
+  // registers the loads left and are not written)
+  uint32_t a[XC][4];
 #pragma unroll
   for (int t = 0; t < XC; ++t) {
-    xq[t] = r.xr[t];
-    if constexpr (PRO == kProSiluMul) uq[t] = r.xu[t];
-    if constexpr (PRO == kProRms) nq[t] = r.nwr[t];
-  }
-#pragma unroll 1
-  for (int i = 0; i < XC; ++i) {
-    const int ch = pw + np * i;
-    const uint4 xi = xq[0], ui = uq[0], ni = nq[0];
-    // the next chunk's registers move up (a queue: the loop body only ever reads slot 0)
+    const uint4 xi = r.xr[t];
+    a[t][0] = xi.x; a[t][1] = xi.y; a[t][2] = xi.z; a[t][3] = xi.w;
+    if constexpr (PRO == kProSiluMul) {  // fp16(silu(g) * u), the silu_mul arithmetic
+      const uint4 ui = r.xu[t];
+      const uint32_t uu[4] = {ui.x, ui.y, ui.z, ui.w};
 #pragma unroll
-    for (int t = 0; t + 1 < XC; ++t) {
-      xq[t] = xq[t + 1];
-      if constexpr (PRO == kProSiluMul) uq[t] = uq[t + 1];
-      if constexpr (PRO == kProRms) nq[t] = nq[t + 1];
-    }
-    if (ch < p.nchunk) {  // wave-uniform
-      uint32_t a[4] = {xi.x, xi.y, xi.z, xi.w};
-      if constexpr (PRO == kProSiluMul) {  // fp16(silu(g) * u), the silu_mul arithmetic
-        const uint32_t uu[4] = {ui.x, ui.y, ui.z, ui.w};
+      for (int d = 0; d < 4; ++d) {
+        uint32_t v = 0;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          uint32_t v = 0;
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const float gv = h2f((uint16_t)(a[d] >> (16 * hh))), uv = h2f((uint16_t)(uu[d] >> (16 * hh)));
-            v |= (uint32_t)f2h(gv / (1.0f + __expf(-gv)) * uv) << (16 * hh);
-          }
-          a[d] = v;
+        for (int hh = 0; hh < 2; ++hh) {
+          const float gv = h2f((uint16_t)(a[t][d] >> (16 * hh))), uv = h2f((uint16_t)(uu[d] >> (16 * hh)));
+          v |= (uint32_t)f2h(gv / (1.0f + __expf(-gv)) * uv) << (16 * hh);
         }
+        a[t][d] = v;
       }
-      if constexpr (PRO == kProRms) {  // h^2 summed in fp32; h * w rounded once to fp16
-        const uint32_t nn[4] = {ni.x, ni.y, ni.z, ni.w};
+    }
+    if constexpr (PRO == kProRms) {  // h^2 summed in fp32; h * w rounded once to fp16
+      const uint4 ni = r.nwr[t];
+      const uint32_t nn[4] = {ni.x, ni.y, ni.z, ni.w};
+      const bool live = pw + np * t < p.nchunk;
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const float h0 = h2f((uint16_t)a[d]), h1 = h2f((uint16_t)(a[d] >> 16));
+      for (int d = 0; d < 4; ++d) {
+        const float h0 = h2f((uint16_t)a[t][d]), h1 = h2f((uint16_t)(a[t][d] >> 16));
+        if (live) {
           ssq += h0 * h0;
           ssq += h1 * h1;
-          const float w0 = h2f((uint16_t)nn[d]), w1 = h2f((uint16_t)(nn[d] >> 16));
-          a[d] = (uint32_t)f2h(h0 * w0) | ((uint32_t)f2h(h1 * w1) << 16);
         }
+        const float w0 = h2f((uint16_t)nn[d]), w1 = h2f((uint16_t)(nn[d] >> 16));
+        a[t][d] = (uint32_t)f2h(h0 * w0) | ((uint32_t)f2h(h1 * w1) << 16);
       }
-      rf4_t d1 = {0.0f, 0.0f, 0.0f, 0.0f}, d2 = {0.0f, 0.0f, 0.0f, 0.0f};
-      if constexpr (BF) {
-        d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rb8_t, a), __builtin_bit_cast(rb8_t, b1), d1, 0, 0, 0);
-        d2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rb8_t, a), __builtin_bit_cast(rb8_t, b2), d2, 0, 0, 0);
-      } else {
-        d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rh8_t, a), __builtin_bit_cast(rh8_t, b1), d1, 0, 0, 0);
-        d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rh8_t, a), __builtin_bit_cast(rh8_t, b2), d2, 0, 0, 0);
-      }
-      // lane (j, g) holds sub-blocks 4 g + r (r = 0..3) of 128-block g of the chunk; H_4
-      // across them (Sylvester order: r = the high index bits of the 128-block)
-      float lo[4], hi[4];
-      if (p.had) {
-        const float s0 = d1[0] + d1[1], s1 = d1[0] - d1[1], s2 = d1[2] + d1[3], s3 = d1[2] - d1[3];
-        lo[0] = s0 + s2; lo[1] = s1 + s3; lo[2] = s0 - s2; lo[3] = s1 - s3;
-        const float t0 = d2[0] + d2[1], t1 = d2[0] - d2[1], t2 = d2[2] + d2[3], t3 = d2[2] - d2[3];
-        hi[0] = t0 + t2; hi[1] = t1 + t3; hi[2] = t0 - t2; hi[3] = t1 - t3;
+    }
+  }
+  rf4_t d1[XC], d2[XC];
+#pragma unroll
+  for (int t = 0; t < XC; ++t) {
+    d1[t] = rf4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    d2[t] = rf4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (BF) {
+      d1[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rb8_t, a[t]), __builtin_bit_cast(rb8_t, b1), d1[t], 0, 0, 0);
+      d2[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(rb8_t, a[t]), __builtin_bit_cast(rb8_t, b2), d2[t], 0, 0, 0);
+    } else {
+      d1[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rh8_t, a[t]), __builtin_bit_cast(rh8_t, b1), d1[t], 0, 0, 0);
+      d2[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(rh8_t, a[t]), __builtin_bit_cast(rh8_t, b2), d2[t], 0, 0, 0);
+    }
+  }
+  uint32_t packed[XC][4];
+  float bsc[XC];
+  // lane (j, g) holds sub-blocks 4 g + r (r = 0..3) of 128-block g of the chunk; H_4 across
+  // them (Sylvester order: r = the high index bits of the 128-block), then the block's
+  // power-of-two scale (max |x| -> [2^14, 2^15)) and the fp16 pairs.  One branch on the
+  // rotation outside the chunk loop keeps the XC chains in one block, free to interleave.
+  auto finish = [&](auto had_t) __attribute__((always_inline)) {
+    constexpr bool HAD = decltype(had_t)::value;
+    float lo[XC][4], hi[XC][4];
+    uint32_t mx[XC];
+#pragma unroll
+    for (int t = 0; t < XC; ++t) {
+      if constexpr (HAD) {
+        const float s0 = d1[t][0] + d1[t][1], s1 = d1[t][0] - d1[t][1], s2 = d1[t][2] + d1[t][3], s3 = d1[t][2] - d1[t][3];
+        lo[t][0] = s0 + s2; lo[t][1] = s1 + s3; lo[t][2] = s0 - s2; lo[t][3] = s1 - s3;
+        const float t0 = d2[t][0] + d2[t][1], t1 = d2[t][0] - d2[t][1], t2 = d2[t][2] + d2[t][3], t3 = d2[t][2] - d2[t][3];
+        hi[t][0] = t0 + t2; hi[t][1] = t1 + t3; hi[t][2] = t0 - t2; hi[t][3] = t1 - t3;
       } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) { lo[q] = d1[q]; hi[q] = d2[q]; }
+        for (int q = 0; q < 4; ++q) { lo[t][q] = d1[t][q]; hi[t][q] = d2[t][q]; }
       }
-      float mx = 0.0f;
+      // max |value| (v_max3_f32 with |.| source modifiers: a NaN input yields a NaN maximum,
+      // whose exponent field (all ones) then gives the smallest scale, as an infinity does)
+      float m0, m1;
+      asm("v_max3_f32 %0, |%1|, |%2|, |%3|" : "=v"(m0) : "v"(lo[t][0]), "v"(lo[t][1]), "v"(lo[t][2]));
+      asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(m0) : "v"(m0), "v"(lo[t][3]), "v"(hi[t][0]));
+      asm("v_max3_f32 %0, |%1|, |%2|, |%3|" : "=v"(m1) : "v"(hi[t][1]), "v"(hi[t][2]), "v"(hi[t][3]));
+      asm("v_max_f32 %0, %1, %2" : "=v"(m0) : "v"(m0), "v"(m1));
+      mx[t] = __builtin_bit_cast(uint32_t, m0);
+    }
+    // max over each 16-lane row (quad permutes, half-row mirror, row mirror) as integer maxima
+    // of the non-negative bit patterns, one v_max_u32_dpp per chunk and step, the XC chunks
+    // interleaved behind one wait state pair
+#define SPECTRA_ROWMAX_STEP(CTRL)                                                                     \
+    _Pragma("unroll") for (int t = 0; t < XC; ++t) {                                                    \
+      if (t == 0) asm volatile("s_nop 1" ::: );                                                         \
+      asm volatile("v_max_u32_dpp %0, %0, %0 " CTRL " row_mask:0xf bank_mask:0xf" : "+v"(mx[t]));       \
+    }
+    SPECTRA_ROWMAX_STEP("quad_perm:[1,0,3,2]")
+    SPECTRA_ROWMAX_STEP("quad_perm:[2,3,0,1]")
+    SPECTRA_ROWMAX_STEP("row_half_mirror")
+    SPECTRA_ROWMAX_STEP("row_mirror")
+#undef SPECTRA_ROWMAX_STEP
 #pragma unroll
-      for (int q = 0; q < 4; ++q) mx = fmaxf(mx, fmaxf(fabsf(lo[q]), fabsf(hi[q])));
-      mx = row16_max(mx);
-      const uint32_t bits = __builtin_bit_cast(uint32_t, mx);
-      const int eb = (int)(bits >> 23);
-      const int E = eb == 0 ? -126 : eb - 127;  // floor(log2(mx)) for normal mx
-      int F = bits == 0 ? 0 : 14 - E;           // mx * 2^F in [2^14, 2^15)
-      F = F < -126 ? -126 : (F > 126 ? 126 : F);
-      const float f = pow2f(F);
+    for (int t = 0; t < XC; ++t) {
+      // 2^F with F = 14 - floor(log2 max) (max * 2^F in [2^14, 2^15)), clamped to F <= 126
+      // (exponent field >= 15); 1 for an all-zero block.  The scale and its inverse are
+      // built directly as float bit patterns.
+      const int eb = max((int)(mx[t] >> 23), 15);
+      const bool zero = mx[t] == 0u;
+      const float f = __builtin_bit_cast(float, zero ? 0x3f800000u : (uint32_t)(268 - eb) << 23);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) packed[t][q] = pack_scaled(lo[t][q], hi[t][q], f);
+      bsc[t] = __builtin_bit_cast(float, zero ? 0x3f800000u : (uint32_t)(eb - 14) << 23);
+    }
+  };
+  if (p.had) finish(std::true_type{});
+  else finish(std::false_type{});
+
+#pragma unroll
+  for (int t = 0; t < XC; ++t) {
+    const int ch = pw + np * t;
+    if (ch < p.nchunk) {  // wave-uniform
       const int blk = 4 * ch + g;  // global 128-block
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xpd[((jj >> 2) * Q + 4 * blk + q) * 4 + (jj & 3)] = pack_scaled(lo[q], hi[q], f);
-      if (jj == 0) xsc[blk] = pow2f(-F);
+      for (int q = 0; q < 4; ++q) xpd[((jj >> 2) * Q + 4 * blk + q) * 4 + (jj & 3)] = packed[t][q];
+      if (jj == 0) xsc[blk] = bsc[t];
     }
   }
   if constexpr (PRO == kProRms) {  // per-producer sums of h^2, fixed order
@@ -288,11 +332,11 @@ __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& 
   if (p.res != nullptr && ptid < c.Rw) ((uint16_t*)(smem + p.off_res))[ptid] = r.res_raw;
 }
 
-// row-wave loads: the CSR entries of the group's rows, then the weight runs of every slot
+// row-wave loads: the weight runs of every slot, then the CSR entries of the group's rows
 // (lane li stages entry e0 + li of each row; lanes past the row's entries, and arrays
 // without entries, read a dummy word: entry 0, or the workgroup's first weight word).  The
-// few entry loads go first so that they land with the first weight runs rather than behind
-// the last (measured: gate_up N=16384 9.13 -> 8.78 us, the other decoder shapes unchanged).
+// entries' addresses wait for the row pointers' scalar loads, which are issued after the
+// start barrier; the weight runs, which wait for nothing, go first.
 template <int G, int SPR, int RPG>
 struct RowRegs {
   uint4 wq[SPR * RPG];
@@ -306,6 +350,14 @@ __device__ __forceinline__ void rows_row_loads(const RowsParams& p, const RowsCt
   constexpr int NS = SPR * RPG;
   const uint8_t* wbase = p.packed + (int64_t)c.r0 * p.ldp;
 #pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int j = s / SPR, ch = s % SPR;
+    const int row = c.grow0 + j;
+    const uint32_t o = row < c.Rw ? (uint32_t)(row * p.ldp) + (uint32_t)(ch * G + c.li) * 16u : 0u;  // dummy: one line
+    r.wq[s] = load_nt_u4(wbase + o);
+  }
+  asm volatile("" ::: "memory");  // the CSR entries (which wait for the row pointers) behind the weight runs
+#pragma unroll
   for (int j = 0; j < RPG; ++j) {
     const int a = G == 32 ? ((c.lane >> 5) ? sx[RPG + j] : sx[j]) : sx[j];
     const int b = G == 32 ? ((c.lane >> 5) ? sx[RPG + j + 1] : sx[j + 1]) : sx[j + 1];
@@ -317,14 +369,6 @@ __device__ __forceinline__ void rows_row_loads(const RowsParams& p, const RowsCt
     const uint32_t e = ok ? (uint32_t)(a + c.li) : 0u;
     r.ocol[j] = load_at<int>(cb, 4u * e);
     r.oval[j] = load_at<uint16_t>(vb, 2u * e);
-  }
-  asm volatile("" ::: "memory");  // the weight runs are issued behind the CSR entries
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const int j = s / SPR, ch = s % SPR;
-    const int row = c.grow0 + j;
-    const uint32_t o = row < c.Rw ? (uint32_t)(row * p.ldp) + (uint32_t)(ch * G + c.li) * 16u : 0u;  // dummy: one line
-    r.wq[s] = load_nt_u4(wbase + o);
   }
 }
 
@@ -370,7 +414,7 @@ __device__ __forceinline__ float rows_dot(const RowsParams& p, const RowsCtx& c,
 // products and the row totals
 template <int G, int SPR, int RPG, int NP, bool BF, int PRO, typename WL, typename WX>
 __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& c, uint8_t* smem, int np,
-                                            RowRegs<G, SPR, RPG>& r, WL wait_lut, WX wait_x) {
+                                            RowRegs<G, SPR, RPG>& r, WL wait_lut, WX wait_x, const bool* late) {
   constexpr int NS = SPR * RPG;
   const int Q = c.Q, lane = c.lane, li = c.li;
   const uint32_t* xpd = (const uint32_t*)(smem + p.off_xp);
@@ -429,6 +473,7 @@ __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& 
       if constexpr (PRO == kProRms) y *= inv;
       if (p.bias != nullptr) y += bl[row];
       if (p.res != nullptr) y = to_f32_16(from_f32_16(y, odt), odt) + to_f32_16(rsl[row], odt);
+      if (late != nullptr && *late) y = __builtin_nanf("");
       ((uint16_t*)p.out)[c.r0 + row] = from_f32_16(y, odt);
     }
   }
@@ -461,15 +506,22 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
   // every argument the issue phase needs, fetched in one round trip before the first load
   asm volatile("" ::"s"(p.x), "s"(p.packed), "s"(p.ldp), "s"(p.absmax), "s"(p.lda), "s"(p.csr), "s"(p.rowptr),
                "s"(p.bias), "s"(p.res), "s"(p.bias_dt), "s"(p.nchunk), "s"(p.cpr), "s"(p.cmagic), "s"(p.wr));
-  uint32_t* counter = (uint32_t*)(smem + p.off_flag);  // [0]: LUT rows built, [1]: producers done
-  const int rwave = SPLIT ? wave - np : wave;          // row-wave index
+  // [0]: LUT rows built, [1]: producers done
+  uint32_t* counter = (uint32_t*)(smem + kRowsCounterOff);
+  const int rwave = SPLIT ? wave - np : wave;  // row-wave index
 
   if constexpr (SPLIT) {
     if (wave < np) {
       // ---------------- producer waves ----------------
+      if (tid == 0) {
+        counter[0] = 0u;
+        counter[1] = 0u;
+      }
       ProducerRegs<XC, PRO> pr;
       rows_producer_loads<XC, PRO>(p, c, wave, np, tid, pr);
-      __syncthreads();  // --- start barrier: counters zeroed; activation requests precede the weight runs
+      // --- start barrier: counters zeroed (this wave waits for its LDS writes); the
+      //     activation requests precede the weight runs
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       __builtin_amdgcn_s_setprio(3);  // the producers are the critical path of the workgroup
       build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, np, c.lane);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // LDS operations of a wave complete in order
@@ -480,7 +532,9 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
       return;
     }
     // ---------------- row waves ----------------
-    int sx[RW + 1];  // CSR extents of the wave's rows: scalar loads, issued first
+    // --- start barrier, with no wait: a row wave publishes nothing before it
+    asm volatile("s_barrier" ::: "memory");
+    int sx[RW + 1];  // CSR extents of the wave's rows: scalar loads, in flight while the weights issue
     if (p.csr) {
       const __attribute__((address_space(4))) int32_t* rpc = (const __attribute__((address_space(4))) int32_t*)p.rowptr;
 #pragma unroll
@@ -489,23 +543,23 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
 #pragma unroll
       for (int j = 0; j <= RW; ++j) sx[j] = 0;
     }
-    if (tid == 64 * np) {
-      counter[0] = 0u;
-      counter[1] = 0u;
-    }
-    __syncthreads();  // --- start barrier
     RowRegs<G, SPR, RPG> rr;
     rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
-    // waits on the producers' counters (bounded: an unfinished count yields wrong output,
-    // never a hang)
+    // waits on the producers' counters.  The producers are co-resident waves of this
+    // workgroup that wait for nothing but their own loads, so the count always completes;
+    // the wait is still bounded, and a wave whose wait ran out stores NaN for its rows
+    // rather than a value from incomplete activations.
+    bool late = false;
     auto wait_for = [&](int which) {
-      for (int it = 0; it < kRowsSpinLimit; ++it) {
+      int it = 0;
+      for (; it < kRowsSpinLimit; ++it) {
         if (__hip_atomic_load(counter + which, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= (uint32_t)np) break;
         __builtin_amdgcn_s_sleep(1);
       }
+      late = late || it == kRowsSpinLimit;
       asm volatile("" ::: "memory");
     };
-    rows_stream<G, SPR, RPG, NP, BF, PRO>(p, c, smem, np, rr, [&] { wait_for(0); }, [&] { wait_for(1); });
+    rows_stream<G, SPR, RPG, NP, BF, PRO>(p, c, smem, np, rr, [&] { wait_for(0); }, [&] { wait_for(1); }, &late);
   } else {
     // every wave loads and produces, then streams its rows
     int sx[RW + 1];
@@ -528,7 +582,7 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
       __builtin_amdgcn_s_waitcnt(0);  // its dummy loads land before it ends
       return;
     }
-    rows_stream<G, SPR, RPG, 0, BF, PRO>(p, c, smem, W, rr, [] {}, [] {});
+    rows_stream<G, SPR, RPG, 0, BF, PRO>(p, c, smem, W, rr, [] {}, [] {}, nullptr);
   }
 }
 
