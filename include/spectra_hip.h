@@ -281,9 +281,11 @@ int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t tokens, const in
  * 4, 6 or 8 query heads per KV head; head_dim 16, 32, 64, 128 or 256; operands 16-byte aligned).
  * One kernel: spectra_attend_spans(max_seq) workgroups of 64 positions per KV head; the
  * last of a head to finish merges the spans (log-sum-exp).  workspace: >=
- * spectra_attend_workspace(heads, head_dim, max_seq) bytes, 16-byte aligned (span partials
- * and per-head arrival counters), ZEROED before its first use (every call leaves the
- * counters at zero again); calls sharing a workspace must not overlap.  A *pos outside
+ * spectra_attend_workspace(heads, head_dim, max_seq) bytes, 16-byte aligned: per-KV-head
+ * arrival counters at its start (the same offset for every shape), then the span partials.
+ * ZERO the workspace before its first use; every complete call leaves the counters at zero
+ * again, so a workspace stays valid for later calls of any shape that fits it.  Calls
+ * sharing a workspace must not overlap.  A *pos outside
  * [0, max_seq) appends nothing (the caches are left as they are) and yields NaN outputs. */
 int32_t spectra_attend_spans(int32_t max_seq);
 size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq);

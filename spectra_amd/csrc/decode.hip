@@ -753,7 +753,10 @@ extern "C" int spectra_rope_append(const void* qkv, int64_t ldqkv, int64_t token
 
 extern "C" int32_t spectra_attend_spans(int32_t max_seq) { return (max_seq + kSpanMax - 1) / kSpanMax; }
 
-// [heads][nspan][head_dim + 2] fp32 partials, then one arrival counter per head, 256 bytes apart
+// Workspace: one arrival counter per KV head, 256 bytes apart, at the start (the same
+// offset for every shape, so counters left at zero by one call stay zero for a call of
+// another shape on the same workspace), then [heads][nspan][head_dim + 2] fp32 partials.
+static size_t attend_counter_bytes(int32_t heads) { return (size_t)heads * 256; }
 static size_t attend_part_bytes(int32_t heads, int32_t head_dim, int32_t max_seq) {
   const size_t b = (size_t)heads * spectra_attend_spans(max_seq) * (head_dim + 2) * sizeof(float);
   return (b + 255) & ~(size_t)255;
@@ -761,7 +764,7 @@ static size_t attend_part_bytes(int32_t heads, int32_t head_dim, int32_t max_seq
 
 extern "C" size_t spectra_attend_workspace(int32_t heads, int32_t head_dim, int32_t max_seq) {
   if (heads < 1 || head_dim < 1 || max_seq < 1) return 0;
-  return attend_part_bytes(heads, head_dim, max_seq) + (size_t)heads * 256;
+  return attend_counter_bytes(heads) + attend_part_bytes(heads, head_dim, max_seq);
 }
 
 typedef void (*attend_fn)(const uint16_t*, const int64_t*, const float*, const float*, int, int, float, const KvCache,
@@ -824,9 +827,9 @@ static int attend_launch(const void* qkv, const int64_t* pos, const float* cos_t
                                          "(the 4-bit cache with RoPE)");
   const int nspan = spectra_attend_spans(kvc.lmax);
   const float scale = 1.0f / sqrtf((float)head_dim);
-  float* part = (float*)workspace;
+  uint32_t* counter = (uint32_t*)workspace;
+  float* part = (float*)((uint8_t*)workspace + attend_counter_bytes(heads));
   const hipStream_t s = (hipStream_t)stream;
-  uint32_t* counter = (uint32_t*)((uint8_t*)workspace + attend_part_bytes(heads, head_dim, kvc.lmax));
   hipLaunchKernelGGL(fn, dim3((unsigned)kv_heads, (unsigned)nspan), dim3(kDecThreads), 0, s, (const uint16_t*)qkv,
                      pos, cos_t, sin_t, heads, kv_heads, scale, kvc, part, counter, (uint16_t*)out);
   SPECTRA_HIP_CHECK(hipGetLastError());

@@ -671,7 +671,8 @@ static GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
   g.nt = (int)((n + g.BN - 1) / g.BN);
   const int tiles = g.mt * g.nt;
   const int steps = (int)(k / kBK);
-  int ks = tiles < 256 && n % 4 == 0 ? 256 / tiles : 1;
+  const int ncu = device_cu_count();  // K splits while the tiles fill fewer workgroups than CUs
+  int ks = tiles < ncu && n % 4 == 0 ? ncu / tiles : 1;
   ks = ks > 8 ? 8 : ks;
   while (ks > 1 && steps / ks < 8) --ks;
   g.ksteps = (steps + ks - 1) / ks;

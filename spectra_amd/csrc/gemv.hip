@@ -25,7 +25,8 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   const int S = (int)((k + 2047) / 2048);
   // 8 waves per workgroup (two per SIMD): the setup work is per element, the stream per wave
   int G = 8 / S;
-  const int64_t want = (n + 255) / 256;  // rows per workgroup for ~one workgroup per CU
+  const int ncu = device_cu_count();
+  const int64_t want = (n + ncu - 1) / ncu;  // rows per workgroup for ~one workgroup per CU
   if (G > want) G = (int)want;
   if (G < 1) G = 1;
   int rpw = (int)((want + G - 1) / G);
@@ -89,7 +90,7 @@ static bool plan_gemv(int64_t n, int64_t k, int m, bool outliers, bool csr, Gemv
   if (ocap > fit) ocap = fit;
   // grids beyond one workgroup per CU: keep two resident per CU when the staging still
   // covers a useful share of the entries (the rest are read in the per-row phase)
-  if (pl->grid > 256 && mt == 1 && off < 81920) {
+  if (pl->grid > ncu && mt == 1 && off < 81920) {
     const int fit2 = (int)((81920 - off) / (uint32_t)(mt * 4));
     if (fit2 >= 256 && ocap > fit2) ocap = fit2;
   }

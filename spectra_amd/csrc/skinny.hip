@@ -560,7 +560,8 @@ struct SkinnyPlan {
 static bool plan_skinny(int64_t n, int64_t k, SkinnyPlan* pl) {
   const int nchunks = (int)(k / 128);
   const int64_t tiles = (n + 15) / 16;
-  int T = (int)((tiles + 255) / 256);
+  const int ncu = device_cu_count();
+  int T = (int)((tiles + ncu - 1) / ncu);
   T = T <= 1 ? 1 : (T <= 2 ? 2 : 4);
   const int cpw_max = T == 1 ? 8 : (T == 2 ? 6 : 4);
   const int nrounds = (nchunks + 8 * cpw_max - 1) / (8 * cpw_max);

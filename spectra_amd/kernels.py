@@ -444,7 +444,11 @@ def attend_decode(qkv: torch.Tensor, pos: torch.Tensor, cos: Optional[torch.Tens
     """Decode attention of the fused-QKV row ``qkv`` [(heads + 2 kv_heads) * d] of the token at
     position ``pos`` (int64 [1] on the device): rotates q and k (``cos``/``sin`` fp32 [L, d/2],
     None = no rotation), appends k and v to the caches [kv, L, d], attends over [0, pos];
-    returns fp16 [heads, d].  ``workspace`` (uint8, span partials) defaults to a fresh buffer."""
+    returns fp16 [heads, d].  ``workspace`` (uint8, ``attend_workspace_bytes`` or more): the
+    merge's per-KV-head arrival counters at its start, then the span partials.  It must be
+    zero before its first use; every complete call leaves the counters at zero, so one
+    workspace serves later calls of any shape that fits it, but overlapping calls on one
+    workspace race.  Default: a fresh zeroed buffer."""
     _need_f16(qkv, "qkv")
     _need_f16(k_cache, "k_cache")
     _need_f16(v_cache, "v_cache")
@@ -629,7 +633,8 @@ def attend_decode_q4(qkv: torch.Tensor, pos: torch.Tensor, cos: torch.Tensor, si
                      workspace: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``attend_decode`` over a 4-bit cache: ``k4`` / ``v4`` = (codes [kv, L, d/2], scales
     [kv, L, d/32], zeros [kv, L, d/32]) hold every position; ``k_window`` / ``v_window``
-    [kv, W, d] fp16 rings hold the last W positions (slot = position % W)."""
+    [kv, W, d] fp16 rings hold the last W positions (slot = position % W).  ``workspace``:
+    as for ``attend_decode`` (zero before its first use, counters first, no overlapping calls)."""
     _need_f16(qkv, "qkv")
     _need_f16(k_window, "k_window")
     _need_f16(v_window, "v_window")

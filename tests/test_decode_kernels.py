@@ -121,6 +121,29 @@ def test_attend_decode(hip, heads, kv, hd, L, rope):
         assert err <= 2e-3 * vc.abs().max().item(), (p, err)
 
 
+def test_attend_workspace_shared_across_shapes(hip):
+    """One zeroed workspace serves calls of different shapes in turn (the arrival counters sit
+    at its start whatever the shape, and every call leaves them at zero): max_seq 1100 then
+    100 then 700, head_dim 128 then 64, each against the fp32 reference."""
+    heads, kv = 8, 2
+    ws = torch.zeros(max(K.attend_workspace_bytes(heads, hd, L) for hd, L in ((128, 1100), (64, 700))),
+                     device="cuda", dtype=torch.uint8)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for hd, L, p in ((128, 1100, 1000), (64, 100, 70), (128, 700, 650), (64, 700, 3), (128, 1100, 1099)):
+        case(hd=hd, L=L, pos=p)
+        kc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+        vc = torch.randn(kv, L, hd, device="cuda", generator=g).half()
+        qkv = torch.randn((heads + 2 * kv) * hd, device="cuda", generator=g).half()
+        out = K.attend_decode(qkv, torch.tensor([p], device="cuda"), None, None, heads, kv, kc, vc, ws)
+        q = qkv[: heads * hd].reshape(heads, hd).float()
+        kk = kc[:, : p + 1, :].float().repeat_interleave(heads // kv, dim=0)  # [heads, n, hd]
+        vv = vc[:, : p + 1, :].float().repeat_interleave(heads // kv, dim=0)
+        sc = (kk @ q[:, :, None])[:, :, 0] / math.sqrt(hd)
+        ref = (torch.softmax(sc, -1)[:, None, :] @ vv)[:, 0, :]
+        assert (out.float() - ref).abs().max().item() <= 2e-3 * vc.abs().max().item()
+    assert int(ws[: heads * 256].view(torch.int32).abs().sum()) == 0  # counters left at zero
+
+
 @pytest.mark.parametrize("L", [600, 1100])
 def test_attend_decode_ignores_rows_past_position(hip, L):
     """Cache rows past the position may hold anything (here NaN): the output and the rows

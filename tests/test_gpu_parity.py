@@ -285,6 +285,79 @@ def test_format_b_gemv_shapes(hip, n, k):
     check_y(y.unsqueeze(0), y_ref, torch.float16)
 
 
+def _stream_operands(seed, n, k, had, marlin):
+    """Format B operands with 0.5% outliers plus one row holding an outlier in every fourth
+    column (far more entries than a lane group has lanes)."""
+    rng = np.random.default_rng(seed)
+    w = rand_np(rng, (n, k), 0.02)
+    mask = rng.random((n, k)) < 0.005
+    mask[5, ::4] = True
+    w[mask] = (rng.standard_normal(mask.sum()) * 0.2).astype(np.float16)
+    q = O.nf4_quantize(w, "float16", 64, 0, mask, marlin)
+    return q, rng
+
+
+@pytest.mark.parametrize("k,had,marlin,act,bias", [
+    (5120, 128, True, "float16", True),    # K / 1024 = 5: no row-owning plan
+    (6144, 128, False, "bfloat16", False),
+    (5120, 0, False, "float16", False),
+    (1024, 16, True, "float16", True),     # Hadamard blocks the row-owning kernel does not take
+    (1024, 32, False, "bfloat16", True),
+    (1024, 64, True, "bfloat16", False),
+    (1024, 256, False, "float16", False),
+    (1024, 512, True, "float16", True),
+])
+def test_stream_gemv_shapes(hip, k, had, marlin, act, bias):
+    """One-row shapes served by the streaming GEMV kernel (the M=1 NF4 shapes the row-owning
+    kernel's plan does not cover): fp16 / bf16 activations, both nibble orders, Hadamard
+    blocks 16-512, bias, and a row with more CSR entries than lanes, against the oracle."""
+    case(k=k, had=had, marlin=marlin, act=act, bias=bias)
+    n = 700
+    q, rng = _stream_operands(k + had + marlin, n, k, had, marlin)
+    rd = act if act == "float16" else "float32"
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], marlin, rd, q["rowptr"], q["col"], q["val"])
+    x = O.round_to(rand_np(rng, (1, k), 1.0, np.float32), act)
+    b = rand_np(rng, (n,), 0.1) if bias else None
+    y_ref = O.linear_ref(x, act, w_eff, rd, hadamard_block=had, bias=b)
+    y = K.fused_w4a16_gemv_hdsq(cuda(x, TDT[act]), cuda(q["packed"]), cuda(q["absmax"]), None,
+                                bias=cuda(b) if bias else None, outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]),
+                                marlin_layout=marlin, codebook="nf4", group_size=64, hadamard_block=had,
+                                outlier_rowptr=cuda(q["rowptr"]))
+    check_y(y, y_ref, TDT[act])
+
+
+@pytest.mark.parametrize("k,had,marlin,prologue", [(6144, 128, True, "rmsnorm"), (5120, 128, False, "rmsnorm"),
+                                                   (5120, 128, True, "silu_mul"), (1024, 64, False, "silu_mul")])
+def test_stream_gemv_prologues(hip, k, had, marlin, prologue):
+    """The streaming GEMV kernel's fused prologues (RMSNorm of the residual stream, SiLU-mul of
+    a fused gate_up row) and residual epilogue against the oracle: RMSNorm in fp64, the SiLU-mul
+    activations taken from the separate kernel (the prologue is bit-identical to it); the
+    residual add bit-identical to the separate fp16 add."""
+    case(k=k, had=had, marlin=marlin, prologue=prologue)
+    n = 900
+    q, rng = _stream_operands(k + had, n, k, had, marlin)
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], marlin, "float16", q["rowptr"], q["col"], q["val"])
+    ops = K.QWeightOperands(cuda(q["packed"]), cuda(q["absmax"]), None, k, codebook="nf4", group_size=64,
+                            hadamard_block=had, marlin_layout=marlin, outlier_idx=cuda(q["col"]),
+                            outlier_w=cuda(q["val"]), outlier_rowptr=cuda(q["rowptr"]))
+    if prologue == "rmsnorm":
+        h = (rng.standard_normal((1, k)) * 3).astype(np.float16)
+        nw = (rng.random(k) + 0.5).astype(np.float16)
+        y = K.w4a16_gemv_fused(ops, cuda(h), prologue="rmsnorm", norm_weight=cuda(nw), eps=1e-5)
+        hf = h.astype(np.float64)
+        x_eff = (hf / np.sqrt((hf * hf).mean() + 1e-5) * nw.astype(np.float64)).astype(np.float32)
+        check_y(y, O.linear_ref(x_eff, "float32", w_eff, "float16", hadamard_block=had), torch.float16)
+        return
+    gu = cuda((rng.standard_normal((1, 2 * k)) * 2).astype(np.float16))
+    act = K.silu_mul(gu)
+    y = K.w4a16_gemv_fused(ops, gu, prologue="silu_mul")
+    check_y(y, O.linear_ref(host(act), "float16", w_eff, "float16", hadamard_block=had), torch.float16)
+    res = cuda((rng.standard_normal((1, n)) * 4).astype(np.float16))
+    expect = res + y
+    out = K.w4a16_gemv_fused(ops, gu, prologue="silu_mul", residual=res, out=res)
+    assert out.data_ptr() == res.data_ptr() and torch.equal(res, expect)
+
+
 @pytest.mark.parametrize("act", ["float16", "bfloat16"])
 @pytest.mark.parametrize("m", [5, 16, 64, 130])
 def test_format_b_gemm(hip, act, m):
