@@ -396,6 +396,8 @@ def main():
     }
     detail = {"qkv_gemv_us": round(t_qkv * 1e6, 3), "qkv_gemv_GBps": round(b_qkv / t_qkv / 1e9, 1),
               "down_gemv_us": round(t_down * 1e6, 3), "down_gemv_GBps": round(achieved, 1)}
+    del g_down, g_qkv
+    detail.update(ceilings(lib, dev, args.pool_gb, {"qkv": (b_qkv, t_qkv), "down": (b_down, t_down)}))
     if not args.no_detail:
         detail.update(secondary(lib, dev, args.pool_gb))
     result["detail"] = detail
@@ -413,6 +415,44 @@ def main():
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
+
+
+def ceilings(lib, dev, pool_gb: float, gemvs: dict) -> dict:
+    """The floor and ceiling of a one-launch stream on this GPU, timed like the GEMVs (a graph
+    of 100 launches, HIP events on the replay stream), with the GEMVs' launch geometry (256
+    workgroups of 1024 threads): an empty kernel (the fixed cost of a launch), and a plain
+    streaming read of each GEMV's algorithmic bytes with its load pattern, rotating over a
+    buffer larger than the Infinity Cache.  ``gemvs``: name -> (bytes, seconds per launch)."""
+    grid, block, nl = 256, 1024, 100
+
+    class Call:
+        def __init__(self, fn, *args):
+            self.fn, self.args = fn, args
+
+        def __call__(self, stream):
+            L.check(self.fn.__name__, self.fn(*self.args, stream))
+
+    empty = Call(lib.spectra_measure_empty, grid, block)
+    t_empty = time_graph(graph_of([empty] * nl)) / nl
+    out = {"launch_floor_us": round(t_empty * 1e6, 3)}
+    buf = torch.empty(int(pool_gb * 1e9) // 256 * 256, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(block, dtype=torch.int32, device=dev)
+    for name, (nbytes, t_gemv) in gemvs.items():
+        b16 = (nbytes + 15) // 16 * 16
+        slot = (b16 + 4095) // 4096 * 4096
+        copies = buf.numel() // slot
+        calls = [Call(lib.spectra_measure_read, buf.data_ptr() + (i % copies) * slot, b16, grid, block,
+                      sink.data_ptr()) for i in range(nl)]
+        t_read = time_graph(graph_of(calls)) / nl
+        out[f"read_ceiling_{name}_us"] = round(t_read * 1e6, 3)
+        out[f"read_ceiling_{name}_GBps"] = round(nbytes / t_read / 1e9, 1)
+        out[f"{name}_gemv_over_read_ceiling"] = round(t_gemv / t_read, 3)
+    out["ceiling_note"] = (f"launch floor: an empty kernel of {grid} x {block} threads; read ceiling: a plain "
+                           "16-byte-per-thread streaming read of the GEMV's algorithmic bytes with its load pattern "
+                           f"and geometry, rotating over {buf.numel() / 1e9:.2f} GB; both in a graph of {nl} "
+                           "launches, as the GEMVs are timed")
+    del buf
+    return out
 
 
 COPY_BYTES = 16 << 20  # plain copy of known size: FETCH_SIZE / WRITE_SIZE scale factors

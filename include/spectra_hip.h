@@ -338,6 +338,18 @@ int spectra_greedy_next(const void* logits, int64_t n, int64_t* token, int64_t* 
 int spectra_greedy_finish(void* argmax_key, int64_t* token, int64_t* history, int64_t hist_len, int64_t* pos,
                           spectra_stream_t stream);
 
+/* Measurement only (no counterpart in the reference): the fixed cost of one launch and
+ * the time of a plain HBM stream, the floor and ceiling a one-launch GEMV is held against.
+ * spectra_measure_empty: a kernel that does nothing, grid x block threads.
+ * spectra_measure_read: reads `bytes` (a positive multiple of 16) at src (16-byte aligned)
+ * with the GEMV's load pattern -- workgroup b reads the b-th contiguous slice, each thread
+ * issues every 16-byte non-temporal load of its share before the first use -- and stores
+ * nothing unless the XOR of all it read equals a fixed value (sink: block uint32 words,
+ * 4-byte aligned).  block a multiple of 64 up to 1024; at most 16 loads per thread. */
+int spectra_measure_empty(int32_t grid, int32_t block, spectra_stream_t stream);
+int spectra_measure_read(const void* src, size_t bytes, int32_t grid, int32_t block, void* sink,
+                         spectra_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

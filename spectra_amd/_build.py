@@ -16,7 +16,7 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(PKG, "_obj")
 LIB = os.path.join(PKG, "libspectra_hip.so")
-SOURCES = ["api.hip", "quant.hip", "dequant.hip", "gemv.hip", "gemv_f16.hip", "gemv_bf16.hip", "gemv_stream_f16.hip", "gemv_stream_bf16.hip", "gemv_rows_plain.hip", "gemv_rows_pro.hip", "gemm.hip", "skinny.hip", "outliers.hip", "decode.hip"]
+SOURCES = ["api.hip", "quant.hip", "dequant.hip", "gemv.hip", "gemv_f16.hip", "gemv_bf16.hip", "gemv_stream_f16.hip", "gemv_stream_bf16.hip", "gemv_rows_plain.hip", "gemv_rows_pro.hip", "gemm.hip", "skinny.hip", "outliers.hip", "decode.hip", "measure.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

@@ -91,6 +91,8 @@ SIGNATURES = {
     "spectra_kv4_dequantize": (c_int32, [c_void_p, c_void_p, c_void_p, c_int64, c_int32, c_void_p, c_void_p]),
     "spectra_attend_decode_q4": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32,
                                            c_int32] + [c_void_p] * 8 + [c_void_p, c_size_t, c_void_p, c_void_p]),
+    "spectra_measure_empty": (c_int32, [c_int32, c_int32, c_void_p]),
+    "spectra_measure_read": (c_int32, [c_void_p, c_size_t, c_int32, c_int32, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -95,6 +95,12 @@ def test_entry_points_reject_bad_arguments():
                                         None) == L.ERR_INVALID
     assert "group_size=32" in lib.spectra_last_error().decode()
     assert lib.spectra_fwht_rows(0x1000, 96, L.F32, 2, 96, 96, 0x2000, 96, L.F32, None) == L.ERR_INVALID
+    # measurement kernels: geometry, alignment and size checks before any launch
+    assert lib.spectra_measure_empty(0, 64, None) == L.ERR_INVALID
+    assert lib.spectra_measure_read(0x1008, 1024, 4, 64, 0x2000, None) == L.ERR_INVALID  # unaligned source
+    assert lib.spectra_measure_read(0x1000, 1000, 4, 64, 0x2000, None) == L.ERR_INVALID  # not a multiple of 16
+    assert lib.spectra_measure_read(0x1000, 1024, 4, 100, 0x2000, None) == L.ERR_INVALID  # block not of whole waves
+    assert lib.spectra_measure_read(0x1000, 1 << 30, 1, 64, 0x2000, None) == L.ERR_UNSUPPORTED  # > 16 loads/thread
 
 
 def test_decode_kernels_reject_bad_arguments():
