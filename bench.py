@@ -602,7 +602,8 @@ def secondary(lib, dev, pool_gb: float) -> dict:
 def host_overhead(lib, dev, n: int = 3000) -> dict:
     """Host time to issue one eager M=1 down_proj call (cfg2 shape), measured as the issue
     rate of ``n`` back-to-back calls: the C-ABI entry point through ctypes, the functional
-    API (fused_w4a16_gemv_hdsq, cached descriptor) and the module (SpectraFusedLinear).
+    API (fused_w4a16_gemv_hdsq, cached descriptor), the module (SpectraFusedLinear, one
+    call of the registered operator) and the operator called directly.
     Whichever exceeds the kernel's own time bounds an eager caller."""
     from spectra_amd.engine import SpectraFusedLinear
     q = synth_nf4(3072, 8192, seed=32)
@@ -632,6 +633,8 @@ def host_overhead(lib, dev, n: int = 3000) -> dict:
                    x, q.packed, q.absmax, None, outlier_idx=col, outlier_w=val, marlin_layout=True,
                    out=y, **q.kernel_kwargs())), 2),
                "eager_m1_issue_us_module": round(issue(lambda: lin(x)), 2)}
+        args = lin._op_args  # bound by the module's first call
+        out["eager_m1_issue_us_torch_op"] = round(issue(lambda: torch.ops.spectra_hip.w4a16_linear(x, *args)), 2)
     out["eager_note"] = ("host issue time per eager M=1 down_proj call (3000 back-to-back calls); the kernel itself "
                          "takes down_gemv_us, so above that an eager caller is host-bound and a HIP graph is the remedy")
     return out

@@ -1,6 +1,7 @@
-"""Builds libspectra_hip.so in-tree with hipcc for gfx950 (no torch headers needed).
+"""Builds libspectra_hip.so in-tree with hipcc for gfx950 (no torch headers needed), then the
+thin PyTorch extension _spectra_torch.so over its C ABI (torch.ops.spectra_hip.*).
 
-    python -m spectra_amd._build            # compile + link
+    python -m spectra_amd._build            # compile + link both
 """
 from __future__ import annotations
 
@@ -16,6 +17,8 @@ CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 OBJDIR = os.path.join(PKG, "_obj")
 LIB = os.path.join(PKG, "libspectra_hip.so")
+TORCH_OPS_LIB = os.path.join(PKG, "_spectra_torch.so")
+TORCH_OPS_SOURCE = "torch_ops.cpp"
 SOURCES = ["api.hip", "quant.hip", "dequant.hip", "gemv.hip", "gemv_f16.hip", "gemv_bf16.hip", "gemv_stream_f16.hip", "gemv_stream_bf16.hip", "gemv_rows_plain.hip", "gemv_rows_pro.hip", "gemm.hip", "skinny.hip", "outliers.hip", "decode.hip", "measure.hip"]
 ARCH = "gfx950"
 
@@ -46,6 +49,32 @@ def _compile(src: str) -> str:
     return obj
 
 
+def build_torch_ops(verbose: bool = True) -> str:
+    """The operator registration (csrc/torch_ops.cpp): host C++ only, compiled with the host
+    compiler against the installed torch's headers and linked to libspectra_hip.so, which it
+    finds next to itself (rpath $ORIGIN)."""
+    import torch
+
+    tdir = os.path.dirname(os.path.abspath(torch.__file__))
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler (g++) for the torch operator library")
+    tmp = TORCH_OPS_LIB + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           f"-I{tdir}/include", f"-I{tdir}/include/torch/csrc/api/include", f"-I{INCLUDE}", "-I/opt/rocm/include",
+           os.path.join(CSRC, TORCH_OPS_SOURCE),
+           f"-L{tdir}/lib", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", f"-L{PKG}", "-lspectra_hip",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tdir}/lib", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"torch operator library failed to build:\n{r.stderr[-8000:]}")
+    os.replace(tmp, TORCH_OPS_LIB)
+    if verbose:
+        print(f"built {TORCH_OPS_LIB}")
+    return TORCH_OPS_LIB
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(OBJDIR, exist_ok=True)
     jobs = min(len(SOURCES), max(1, min(8, os.cpu_count() or 1)))
@@ -59,6 +88,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_torch_ops(verbose)
     return LIB
 
 

@@ -12,6 +12,7 @@ from ctypes import c_int32, c_int64, c_size_t, c_void_p, c_char_p
 
 _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libspectra_hip.so")
+TORCH_OPS_PATH = os.path.join(_PKG, "_spectra_torch.so")
 
 # spectra_status_t / dtype / format / outlier enums (include/spectra_hip.h)
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_WORKSPACE = 0, -1, -2, -3, -4
@@ -124,6 +125,25 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             fn.argtypes = args
         _lib = lib
         return lib
+
+
+_ops_loaded = False
+
+
+def load_torch_ops(path: str = TORCH_OPS_PATH):
+    """Register torch.ops.spectra_hip (the operator library built beside libspectra_hip.so)
+    once and return the namespace; raise (never fall back) when it is unavailable."""
+    global _ops_loaded
+    import torch
+
+    if not _ops_loaded:
+        with _lock:
+            if not _ops_loaded:
+                if not os.path.exists(path):
+                    raise RuntimeError(f"{path} is not built; run `python -m spectra_amd._build`")
+                torch.ops.load_library(path)
+                _ops_loaded = True
+    return torch.ops.spectra_hip
 
 
 def check(fn_name: str, status: int) -> None:

@@ -322,6 +322,7 @@ static int rows_launch(const spectra_qweight_t* w, const RowsPlan& pl, const voi
   p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_sc = pl.off_sc; p.off_ss = pl.off_ss;
   p.off_bias = pl.off_bias; p.off_res = pl.off_res;
   p.wr = pl.WR;
+  p.W = pl.W;
   const gemv_rows_fn fn = rows_fn(pl.G, pl.SPR, pl.RPG, pl.XC, pl.split, act_dtype == SPECTRA_BF16, kpro);
   const int st = ensure_lds_limit((const void*)fn, true);
   if (st != SPECTRA_OK) return st;

@@ -72,6 +72,7 @@ struct RowsParams {
   int cpr;             // 16-byte absmax chunks per row (K / block / 8)
   int cmagic;          // ceil(65536 / cpr): t / cpr == (t * cmagic) >> 16 for t < 1024
   int wr;              // row waves (waves wr .. W-1 are producers when split)
+  int W;               // waves per workgroup (blockDim.x / 64, passed so the kernel reads no implicit argument)
   uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res;
 };
 
@@ -486,7 +487,7 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
   constexpr int NS = SPR * RPG;
   constexpr int NP = NS <= 4 ? NS : NS <= 8 ? 2 : 0;  // slots decoded before the activations are ready
   const int tid = threadIdx.x;
-  const int W = (int)(blockDim.x >> 6);
+  const int W = p.W;  // == blockDim.x / 64; blockDim would pull in the 256-byte implicit-argument block
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int np = SPLIT ? W - p.wr : W;  // producer waves
   // producers are waves 0 .. np - 1 (dispatched first), row waves np .. W - 1
@@ -505,7 +506,7 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
   c.grow0 = c.gi * RPG;  // this group's first row inside the workgroup
   // every argument the issue phase needs, fetched in one round trip before the first load
   asm volatile("" ::"s"(p.x), "s"(p.packed), "s"(p.ldp), "s"(p.absmax), "s"(p.lda), "s"(p.csr), "s"(p.rowptr),
-               "s"(p.bias), "s"(p.res), "s"(p.bias_dt), "s"(p.nchunk), "s"(p.cpr), "s"(p.cmagic), "s"(p.wr));
+               "s"(p.bias), "s"(p.res), "s"(p.bias_dt), "s"(p.nchunk), "s"(p.cpr), "s"(p.cmagic), "s"(p.wr), "s"(p.W));
   // [0]: LUT rows built, [1]: producers done
   uint32_t* counter = (uint32_t*)(smem + kRowsCounterOff);
   const int rwave = SPLIT ? wave - np : wave;  // row-wave index

@@ -16,6 +16,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
+from . import _lib as L
 from .kernels import (GEMV_MAX_M, QWeightOperands, argmax_slots, attend_decode, attend_decode_q4,
                       attend_workspace_bytes, greedy_finish, greedy_next, kv4_quantize, rmsnorm, rope_append, silu_mul,
                       w4_embedding, w4a16_gemv_fused, w4a16_linear)
@@ -59,6 +60,7 @@ class SpectraFusedLinear(nn.Module):
         else:
             self.register_parameter("bias", None)
         self._ops: Optional[QWeightOperands] = None
+        self._op_args: Optional[tuple] = None
 
     def set_weights(self, packed_w: torch.Tensor, scales: torch.Tensor, zeros: Optional[torch.Tensor],
                     bias: Optional[torch.Tensor] = None, outlier_idx: Optional[torch.Tensor] = None,
@@ -83,6 +85,7 @@ class SpectraFusedLinear(nn.Module):
             self.outlier_weight = outlier_weight
             self.outlier_rowptr = outlier_rowptr
         self._ops = None
+        self._op_args = None
 
     def _operands(self) -> QWeightOperands:
         if self._ops is None:
@@ -97,17 +100,29 @@ class SpectraFusedLinear(nn.Module):
 
     def _apply(self, fn, *args, **kwargs):  # device/dtype moves invalidate the descriptor
         self._ops = None
+        self._op_args = None
         return super()._apply(fn, *args, **kwargs)
 
-    # outside any torch.compile trace, as the reference marks it (engine.py:90): the library
-    # call is opaque to the compiler
+    # validation and conversion of the operands (host reads of the outlier tensors) happen
+    # once, eagerly, outside any torch.compile trace
     @torch.compiler.disable
+    def _bind(self) -> tuple:
+        L.load_torch_ops()
+        args = self._operands().op_args
+        if args is None:
+            raise RuntimeError("operands built without holding their tensors cannot feed the operator")
+        self._op_args = args
+        return args
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        total_tokens = x.numel() // self.in_features
-        if total_tokens == 0:
-            return x.new_empty(x.shape[:-1] + (self.out_features,))
-        y = w4a16_linear(self._operands(), x.reshape(total_tokens, self.in_features))
-        return y.reshape(x.shape[:-1] + (self.out_features,)).to(x.dtype)
+        """One call of the registered operator torch.ops.spectra_hip.w4a16_linear: GEMV
+        family for one row, small-batch / GEMM families for more (engine.py:90-124).  The
+        operator has a schema and a shape function, so torch.compile traces through it where
+        the reference marks forward @torch.compiler.disable (engine.py:90)."""
+        args = self._op_args
+        if args is None:
+            args = self._bind()
+        return torch.ops.spectra_hip.w4a16_linear.default(x, *args)
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, codebook={self.codebook}, "

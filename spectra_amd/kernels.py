@@ -91,6 +91,17 @@ def validate_outliers(n: int, k: int, *, rowptr: Optional[torch.Tensor] = None, 
             raise ValueError(f"outlier column indices must lie in [0, K={k})")
 
 
+def layout_word(codebook: str, group_size: int, hadamard_block: int, marlin_layout: bool) -> int:
+    """The weight-layout argument of torch.ops.spectra_hip.w4a16_linear: bit 0 the codebook
+    (1 = NF4, 0 = Format A), bit 1 the Marlin nibble order, bits 2-13 the group / block size,
+    bits 14-25 the Hadamard block (0 = none)."""
+    if codebook not in ("asym", "nf4"):
+        raise ValueError(f"codebook must be 'asym' or 'nf4', got {codebook!r}")
+    if not (0 < group_size < 4096 and 0 <= hadamard_block < 4096):
+        raise ValueError(f"group_size {group_size} / hadamard_block {hadamard_block} out of range")
+    return (codebook == "nf4") | (bool(marlin_layout) << 1) | (group_size << 2) | (hadamard_block << 14)
+
+
 class QWeightOperands:
     """Validated device operands of one quantized weight + its C descriptor.
 
@@ -179,6 +190,16 @@ class QWeightOperands:
             keep.append(b)
         self.desc = w
         self.keep = keep if hold_inputs else [t for t in keep if id(t) not in inputs]
+        # the same operands as the arguments after x of torch.ops.spectra_hip.w4a16_linear
+        # (validated above; the operator trusts them); only when the caller's tensors are held
+        self.op_args = None
+        if hold_inputs:
+            csr = w.outlier_kind == L.OUTLIERS_CSR
+            cols = w.outlier_kind == L.OUTLIERS_COLUMNS
+            self.op_args = (packed, scales, zeros if fmt == L.FMT_ASYM_G32 else None,
+                            col if csr else idx if cols else None, val if csr else ow if cols else None,
+                            rp if csr else None, b if bias is not None else None,
+                            layout_word(codebook, gs, int(hadamard_block), bool(marlin_layout)))
         self.n, self.k, self.device = n, k, dev
 
     def ptr(self):
