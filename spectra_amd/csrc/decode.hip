@@ -271,11 +271,20 @@ __device__ __forceinline__ float load_dev(const float* p) {
 // Arrival of a span workgroup, and the merge by the last one of its KV head: every thread's
 // partial stores have completed before the workgroup counts itself in (one device-scope
 // atomic on the head's counter, 256 bytes apart per head); the workgroup that brings the
-// count to nspan merges the G heads' spans exactly as a separate merge kernel would (16
-// spans' loads in flight, m = -inf marks an empty span) and leaves the counter at 0.
-template <int G, int HD>
+// count to nspan merges the G (<= 8) heads' spans exactly as a separate merge kernel would
+// and leaves the counter at 0.  Spans are merged in batches of 16 (one batch up to 1024
+// positions), every load of a batch in flight at once: lane (j, u) of the first 16 G
+// threads (16-lane rows: j = tid / 16, u = tid % 16) loads (m, l) of head j, span u of the
+// batch and, with 16-lane reductions, keeps the head's running maximum and sum of
+// exponentials and turns the batch into weights exp(m - M) (m = -inf marks an empty span,
+// weight 0) in LDS; every thread loads the V sums of its outputs (o, o + 256, ...) and folds
+// them in with those weights.
+template <int HD>
 __device__ __forceinline__ void attend_arrive_merge(const float* part, uint32_t* counter, uint16_t* out, int kh,
-                                                    int nspan, int tid, int* last_l) {
+                                                    int G, int nspan, int tid, int* last_l) {
+  constexpr int B = 16, GM = 8, O = (GM * HD + kDecThreads - 1) / kDecThreads;
+  __shared__ __align__(16) float fw[GM][B + 4];  // the batch's span weights per head, then the rescale
+  __shared__ float hl_s[GM];
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0)
@@ -284,39 +293,74 @@ __device__ __forceinline__ void attend_arrive_merge(const float* part, uint32_t*
   __syncthreads();
   if (!*last_l) return;
   if (tid == 0) __hip_atomic_store(counter + kh * 64, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  constexpr int B = 16;
-  for (int o = tid; o < G * HD; o += kDecThreads) {
-    const int j = o / HD, d = o - j * HD;
-    const int h = kh * G + j;
-    const float* ph = part + (int64_t)h * nspan * (HD + 2);
-    float m = -INFINITY, l = 0.0f, a = 0.0f;
-    for (int s0 = 0; s0 < nspan; s0 += B) {
-      float mv[B], lv[B], av[B];
+  const int total = G * HD;
+  const float* ph0 = part + (int64_t)kh * G * nspan * (HD + 2);  // head j, span s: + (j nspan + s)(HD + 2)
+  const int lane = tid & 63;
+  const int wj = tid / B, wu = tid % B;
+  const bool wrow = wj < G;  // a weight lane (whole 16-lane rows)
+  float hm = -INFINITY, hl = 0.0f;  // weight lanes: the head's running max and sum
+  float a[O];
 #pragma unroll
-      for (int u = 0; u < B; ++u) {
-        const bool ok = s0 + u < nspan;
-        const float* pp = ph + (int64_t)(ok ? s0 + u : 0) * (HD + 2);
-        mv[u] = ok ? load_dev(pp + HD) : -INFINITY;
-        lv[u] = load_dev(pp + HD + 1);
-        av[u] = load_dev(pp + d);
-      }
-      float mb = m;
-#pragma unroll
-      for (int u = 0; u < B; ++u) mb = fmaxf(mb, mv[u]);
-      if (mb == -INFINITY) continue;  // nothing yet
-      const float r = __expf(m - mb);  // rescale what came before (0 when m = -inf)
-      l *= r;
-      a *= r;
-#pragma unroll
-      for (int u = 0; u < B; ++u) {
-        if (mv[u] == -INFINITY) continue;  // empty span: its V sums were never written
-        const float f = __expf(mv[u] - mb);
-        l += lv[u] * f;
-        a += av[u] * f;
-      }
-      m = mb;
+  for (int q = 0; q < O; ++q) a[q] = 0.0f;
+  for (int s0 = 0; s0 < nspan; s0 += B) {
+    float wmv = -INFINITY, wlv = 0.0f;
+    if (wrow && s0 + wu < nspan) {
+      const float* pp = ph0 + ((int64_t)wj * nspan + s0 + wu) * (HD + 2);
+      wmv = load_dev(pp + HD);
+      wlv = load_dev(pp + HD + 1);
     }
-    out[(int64_t)h * HD + d] = f2h(a / l);
+    float av[O][B];
+#pragma unroll
+    for (int q = 0; q < O; ++q) {
+      const int o = tid + q * kDecThreads;
+      const int oc = o < total ? o : 0;
+      const int j = oc / HD, d = oc - j * HD;
+      const float* pj = ph0 + (int64_t)j * nspan * (HD + 2) + d;
+#pragma unroll
+      for (int u = 0; u < B; ++u) av[q][u] = load_dev(pj + (int64_t)(s0 + u < nspan ? s0 + u : 0) * (HD + 2));
+    }
+    if (wrow) {
+      float mb = wmv;
+      mb = fmaxf(mb, lane_xor<1>(mb, lane));
+      mb = fmaxf(mb, lane_xor<2>(mb, lane));
+      mb = fmaxf(mb, lane_xor<4>(mb, lane));
+      mb = fmaxf(mb, lane_xor<8>(mb, lane));
+      mb = fmaxf(mb, hm);
+      const float r = mb == -INFINITY ? 1.0f : __expf(hm - mb);  // rescale of what came before (0 if nothing)
+      const float f = wmv == -INFINITY ? 0.0f : __expf(wmv - mb);  // empty span: weight 0
+      float lb = wlv * f;
+      lb += lane_xor<1>(lb, lane);
+      lb += lane_xor<2>(lb, lane);
+      lb += lane_xor<4>(lb, lane);
+      lb += lane_xor<8>(lb, lane);
+      hl = hl * r + lb;
+      hm = mb;
+      fw[wj][wu] = f;
+      if (wu == 0) fw[wj][B] = r;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < O; ++q) {
+      const int o = tid + q * kDecThreads;
+      if (o < total) {
+        const int j = o / HD;
+        float t = a[q] * fw[j][B];
+#pragma unroll
+        for (int u = 0; u < B; ++u) {
+          const float f = fw[j][u];
+          t = f == 0.0f ? t : t + av[q][u] * f;  // an empty span's V sums were never written
+        }
+        a[q] = t;
+      }
+    }
+    __syncthreads();  // (the weights are consumed before the next batch's)
+  }
+  if (wrow && wu == 0) hl_s[wj] = hl;
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < O; ++q) {
+    const int o = tid + q * kDecThreads;
+    if (o < total) out[(int64_t)kh * G * HD + o] = f2h(a[q] / hl_s[o / HD]);
   }
 }
 
@@ -377,7 +421,7 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
       store_dev(pbase + (int64_t)tid * nspan * (HD + 2) + HD, -INFINITY);
       store_dev(pbase + (int64_t)tid * nspan * (HD + 2) + HD + 1, 0.0f);
     }
-    attend_arrive_merge<G, HD>(part, counter, out, kh, nspan, tid, &last_l);  // (waits for the span's loads)
+    attend_arrive_merge<HD>(part, counter, out, kh, G, nspan, tid, &last_l);  // (waits for the span's loads)
     return;
   }
   const bool upper = dg * 8 >= H2;
@@ -542,7 +586,232 @@ __global__ void __launch_bounds__(kDecThreads) attend_kernel(const uint16_t* __r
     store_dev(pbase + (int64_t)j * nspan * (HD + 2) + d,
               (wsum[0][j][d] + wsum[1][j][d]) + (wsum[2][j][d] + wsum[3][j][d]));
   }
-  attend_arrive_merge<G, HD>(part, counter, out, kh, nspan, tid, &last_l);
+  attend_arrive_merge<HD>(part, counter, out, kh, G, nspan, tid, &last_l);
+}
+
+// MFMA decode attention on the fp16 cache (head_dim 64, 128 or 256, at most 8 query heads
+// per KV head).  Same grid, spans, partials and merge as attend_kernel; inside a span
+// workgroup wave w takes positions t0 + 16 w .. + 15 and lane (i, g) = (lane & 15, lane >> 4):
+//   * holds the 16-byte chunks 32 c + 8 g .. + 7 (c < head_dim / 32) of position t0 + 16 w + i
+//     for K and V, and of query head i for q (zero for i >= G): the A and B operands of
+//     v_mfma_f32_16x16x32_f16, so scores = K q^T is head_dim / 32 MFMAs;
+//   * ends the score MFMAs with the scores of positions 4 g + r (r < 4) for head i -- exactly
+//     the A operand of v_mfma_f32_16x16x16_f16 for P V, so the wave's softmax piece (max and
+//     sum per head over its 16 positions) feeds P V without moving;
+//   * reads the V operand (4 positions x 1 dim) from the wave's V tile, staged in LDS.
+// The rotated query heads and new key are computed once per workgroup (one thread per 8
+// rotation pairs of a row) into LDS.  The four waves' pieces are combined (log-sum-exp)
+// through LDS into the span's partials.  Rows past the position are masked: scores by
+// select, V rows zeroed before they reach the MFMA (a cache row past the position may hold
+// anything, NaN included).
+typedef _Float16 ah8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 ah4_t __attribute__((ext_vector_type(4)));
+typedef float af4_t __attribute__((ext_vector_type(4)));
+constexpr int kMfmaMaxGroup = 8;  // query heads per KV head served by attend_mfma_kernel
+
+template <int HD, bool ROPE>
+__global__ void __launch_bounds__(kDecThreads) attend_mfma_kernel(const uint16_t* __restrict__ qkv,
+                                                                   const int64_t* __restrict__ pos_p,
+                                                                   const float* __restrict__ cos_t,
+                                                                   const float* __restrict__ sin_t, int heads,
+                                                                   int kv_heads, float scale, const KvCache kvc,
+                                                                   float* __restrict__ part,
+                                                                   uint32_t* __restrict__ counter,
+                                                                   uint16_t* __restrict__ out) {
+  constexpr int KI = HD / 32;  // 32-dim blocks (score MFMAs; 16-byte chunks per lane and row)
+  constexpr int DB = HD / 16;  // 16-dim blocks (P V MFMAs)
+  constexpr int VS = HD + 8;   // LDS row stride (halves) of the V tiles and the rotated rows
+  constexpr int GM = kMfmaMaxGroup;
+  constexpr int RB = HD / 16;  // rotation work items per row (8 pairs (d, d + HD / 2) each)
+  static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim 64, 128 or 256");
+  // the V tiles [wave][16][VS] (fp16), then, once every wave is past its P V, the per-wave
+  // V sums [wave][GM][HD] (fp32) in the same bytes
+  __shared__ __align__(16) uint8_t lds[4 * 16 * VS * 2];
+  static_assert(4 * GM * HD * 4 <= 4 * 16 * VS * 2, "per-wave V sums fit the V tiles");
+  __shared__ __align__(16) uint16_t qs[GM + 1][VS];  // rotated query heads, then the new key
+  __shared__ float wm[4][16], wl[4][16];              // per-wave max and sum of exponentials
+  __shared__ int last_l;
+  // every kernel argument in one round trip, before the first load
+  asm volatile("" ::"s"(qkv), "s"(pos_p), "s"(cos_t), "s"(sin_t), "s"(heads), "s"(kv_heads), "s"(scale),
+               "s"(kvc.k), "s"(kvc.v), "s"(kvc.lmax), "s"(part), "s"(counter), "s"(out));
+  const int G = heads / kv_heads;
+  const int lmax = kvc.lmax;
+  const int kh = blockIdx.x, sp = blockIdx.y, nspan = gridDim.y, tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, i16 = lane & 15, g4 = lane >> 4;
+  const int t0 = sp * kSpanMax;
+  const int tp = t0 + 16 * wave + i16;  // the position of this lane's K / V chunks
+  // rotation item of this lane: row i (< G: query head, G: the new key), pair block
+  // b = RBW w + g (pairs (d, d + HD / 2), d = 8 b .. + 7); its query / key halves load first,
+  // so that waiting for them waits for no K / V chunk
+  constexpr int RBW = RB / 4;  // pair blocks per wave
+  const bool ritem = g4 < RBW && i16 <= G;
+  const int rblk = RBW * wave + g4;
+  uint4 rlo = make_uint4(0, 0, 0, 0), rhi = rlo;
+  if (ritem) {
+    const uint32_t o = (uint32_t)((i16 < G ? kh * G + i16 : heads + kh) * HD) * 2u + 16u * rblk;
+    rlo = load_at<uint4>(qkv, o);
+    rhi = load_at<uint4>(qkv, o + (uint32_t)HD);
+  }
+  // ---- K / V chunks at addresses independent of the position (rows clamped into the cache)
+  const uint16_t* kbase = kvc.k + (int64_t)kh * lmax * HD;
+  const uint16_t* vbase = kvc.v + (int64_t)kh * lmax * HD;
+  uint4 kr[KI], vr[KI];
+  {
+    const uint32_t o = (uint32_t)(min(tp, lmax - 1) * HD + 8 * g4) * 2u;
+#pragma unroll
+    for (int c = 0; c < KI; ++c) {
+      kr[c] = load_at<uint4>(kbase, o + 64u * c);
+      vr[c] = load_at<uint4>(vbase, o + 64u * c);
+    }
+  }
+  asm volatile("" ::: "memory");  // the K / V chunks are requested here, not sunk behind the position
+  // the position: a scalar load (it waits for no vector load)
+  const int64_t pos = *(const __attribute__((address_space(4))) int64_t*)pos_p;
+  const bool outside = pos < 0 || pos >= lmax;
+  const int n = outside ? 0 : (int)min((int64_t)kSpanMax, pos + 1 - t0);  // uniform
+  float* pbase = part + ((int64_t)kh * G * nspan + sp) * (HD + 2);     // head j: + j * nspan * (HD + 2)
+  if (n <= 0) {  // span past the position: an empty piece for the merge
+    if (tid < G) {
+      store_dev(pbase + (int64_t)tid * nspan * (HD + 2) + HD, -INFINITY);
+      store_dev(pbase + (int64_t)tid * nspan * (HD + 2) + HD + 1, 0.0f);
+    }
+    attend_arrive_merge<HD>(part, counter, out, kh, G, nspan, tid, &last_l);
+    return;
+  }
+  // ---- rotation: the cos / sin of the position for the wave's pair blocks (scalar loads:
+  //      they wait for no vector load), the rope_append arithmetic, into LDS
+  if constexpr (ROPE) {
+    typedef const __attribute__((address_space(4))) float* cfp_t;
+    const cfp_t ct = (cfp_t)(cos_t + pos * (HD / 2) + 8 * RBW * wave);
+    const cfp_t st = (cfp_t)(sin_t + pos * (HD / 2) + 8 * RBW * wave);
+    float cw[8 * RBW], sw[8 * RBW];
+#pragma unroll
+    for (int e = 0; e < 8 * RBW; ++e) {
+      cw[e] = ct[e];
+      sw[e] = st[e];
+    }
+    if (ritem) {
+      float cs[8], sn[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float cv = cw[e], sv = sw[e];
+#pragma unroll
+        for (int b = 1; b < RBW; ++b) {
+          cv = g4 == b ? cw[8 * b + e] : cv;
+          sv = g4 == b ? sw[8 * b + e] : sv;
+        }
+        cs[e] = cv;
+        sn[e] = sv;
+      }
+      const uint4 lo = rope_chunk(rlo, rhi, cs, sn, false), hi = rope_chunk(rhi, rlo, cs, sn, true);
+      rlo = lo;
+      rhi = hi;
+    }
+  }
+  if (ritem) {
+    *(uint4*)&qs[i16][8 * rblk] = rlo;
+    *(uint4*)&qs[i16][HD / 2 + 8 * rblk] = rhi;
+  }
+  const bool mine = tp == pos;  // the lanes of the new token's row
+  uint4 vn[KI];
+  if (mine) {
+    const uint16_t* vrow = qkv + (int64_t)(heads + kv_heads + kh) * HD;
+#pragma unroll
+    for (int c = 0; c < KI; ++c) vn[c] = load_at<uint4>(vrow, 16u * (4 * c + g4));
+  }
+  __syncthreads();
+  // ---- the new token: appended to the caches, and taken from registers
+  if (mine) {
+    const uint32_t o = (uint32_t)(pos * HD + 8 * g4) * 2u;
+#pragma unroll
+    for (int c = 0; c < KI; ++c) {
+      kr[c] = *(const uint4*)&qs[G][32 * c + 8 * g4];
+      vr[c] = vn[c];
+      *(uint4*)((uint8_t*)kvc.k + (int64_t)kh * lmax * HD * 2 + o + 64u * c) = kr[c];
+      *(uint4*)((uint8_t*)kvc.v + (int64_t)kh * lmax * HD * 2 + o + 64u * c) = vr[c];
+    }
+  }
+  // ---- this wave's V tile, rows past the position zeroed
+  uint16_t* vt = (uint16_t*)lds + wave * 16 * VS;
+  {
+    const bool vok = tp - t0 < n;
+#pragma unroll
+    for (int c = 0; c < KI; ++c)
+      *(uint4*)(vt + i16 * VS + 32 * c + 8 * g4) = vok ? vr[c] : make_uint4(0, 0, 0, 0);
+  }
+  // ---- scores: D[position 4 g + r][head i]
+  af4_t sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < KI; ++c) {
+    const uint4 qc = i16 < G ? *(const uint4*)&qs[i16][32 * c + 8 * g4] : make_uint4(0, 0, 0, 0);
+    sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(ah8_t, kr[c]), __builtin_bit_cast(ah8_t, qc), sc,
+                                                0, 0, 0);
+  }
+  // ---- the wave's softmax piece for head i over its 16 positions
+  const int pb = 16 * wave + 4 * g4;  // span-relative position of row r = pb + r
+  float e[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    e[r] = pb + r < n ? sc[r] * scale : -INFINITY;
+    mx = fmaxf(mx, e[r]);
+  }
+  mx = fmaxf(mx, lane_xor<16>(mx, lane));
+  mx = fmaxf(mx, lane_xor<32>(mx, lane));
+  float l = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    e[r] = pb + r < n ? __expf(e[r] - mx) : 0.0f;  // (no valid row: mx = -inf, every e 0)
+    l += e[r];
+  }
+  l += lane_xor<16>(l, lane);
+  l += lane_xor<32>(l, lane);
+  // ---- P V: D[head 4 g + r][dim 16 b + i]
+  const ah4_t pa = {(_Float16)e[0], (_Float16)e[1], (_Float16)e[2], (_Float16)e[3]};
+  af4_t acc[DB];
+  const uint16_t* vrd = vt + (4 * g4) * VS + i16;
+#pragma unroll
+  for (int b = 0; b < DB; ++b) {
+    const ah4_t vb = {__builtin_bit_cast(_Float16, vrd[16 * b]), __builtin_bit_cast(_Float16, vrd[VS + 16 * b]),
+                      __builtin_bit_cast(_Float16, vrd[2 * VS + 16 * b]),
+                      __builtin_bit_cast(_Float16, vrd[3 * VS + 16 * b])};
+    acc[b] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb, af4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+  }
+  // ---- the four waves' pieces -> the span's partials: each wave's V sums (unscaled) and
+  //      softmax piece to LDS, then per output the log-sum-exp combination in wave order
+  if (g4 == 0) {
+    wm[wave][i16] = mx;
+    wl[wave][i16] = l;
+  }
+  __syncthreads();  // (every wave is also past its V tile)
+  float* ws = (float*)lds;  // [wave][GM][HD]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * g4 + r;
+    if (h < G) {
+#pragma unroll
+      for (int b = 0; b < DB; ++b) ws[(wave * GM + h) * HD + 16 * b + i16] = acc[b][r];
+    }
+  }
+  __syncthreads();
+  for (int o = tid; o < G * HD; o += kDecThreads) {
+    const int j = o / HD, d = o - j * HD;
+    const float m4 = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+    float a = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) a += wm[w][j] == -INFINITY ? 0.0f : ws[(w * GM + j) * HD + d] * __expf(wm[w][j] - m4);
+    store_dev(pbase + (int64_t)j * nspan * (HD + 2) + d, a);
+  }
+  if (tid < G) {
+    const int j = tid;
+    const float m4 = fmaxf(fmaxf(wm[0][j], wm[1][j]), fmaxf(wm[2][j], wm[3][j]));
+    float lt = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) lt += wm[w][j] == -INFINITY ? 0.0f : wl[w][j] * __expf(wm[w][j] - m4);
+    store_dev(pbase + (int64_t)j * nspan * (HD + 2) + HD, m4);
+    store_dev(pbase + (int64_t)j * nspan * (HD + 2) + HD + 1, lt);
+  }
+  attend_arrive_merge<HD>(part, counter, out, kh, G, nspan, tid, &last_l);
 }
 
 // grid (ceil(rows * d / 8 / 256), heads): one lane per 8 values (groups of 32 = 4 lanes)
@@ -821,6 +1090,11 @@ static int attend_launch(const void* qkv, const int64_t* pos, const float* cos_t
   const int g = heads / kv_heads;
   attend_fn fn;
   if (q4) fn = cos_t ? pick_attend_hd<true, true>(head_dim, g) : nullptr;
+  else if (g <= kMfmaMaxGroup && head_dim >= 64)  // the MFMA kernel
+    fn = cos_t ? (head_dim == 64 ? attend_mfma_kernel<64, true> : head_dim == 128 ? attend_mfma_kernel<128, true>
+                                                                                 : attend_mfma_kernel<256, true>)
+               : (head_dim == 64 ? attend_mfma_kernel<64, false> : head_dim == 128 ? attend_mfma_kernel<128, false>
+                                                                                  : attend_mfma_kernel<256, false>);
   else fn = cos_t ? pick_attend_hd<true, false>(head_dim, g) : pick_attend_hd<false, false>(head_dim, g);
   if (fn == nullptr)
     return fail(SPECTRA_ERR_UNSUPPORTED, "decode attention serves 1, 2, 3, 4, 6 or 8 query heads per KV head "
