@@ -123,7 +123,10 @@ def test_decode_kernels_reject_bad_arguments():
     assert lib.spectra_attend_decode_q4(*args, 4, 2, 16, 64, 16, p, p, p, p, p, p, p, p, p, 1 << 20, p,
                                         None) == L.ERR_INVALID
     assert "head_dim" in lib.spectra_last_error().decode()
-    assert lib.spectra_attend_decode(*args, 40, 8, 128, 1024, p, p, p, 1 << 24, p, None) == L.ERR_UNSUPPORTED
+    # 10 query heads per KV head: past both kernels (the MFMA kernel serves up to 8 at head_dim
+    # >= 64, the other 1, 2, 3, 4, 6 or 8)
+    assert lib.spectra_attend_decode(*args, 80, 8, 128, 1024, p, p, p, 1 << 24, p, None) == L.ERR_UNSUPPORTED
+    assert lib.spectra_attend_decode(*args, 20, 4, 32, 1024, p, p, p, 1 << 24, p, None) == L.ERR_UNSUPPORTED
     assert lib.spectra_attend_decode(*args, 24, 8, 96, 1024, p, p, p, 1 << 24, p, None) == L.ERR_INVALID
     assert lib.spectra_attend_decode(p, p, p, None, 24, 8, 128, 1024, p, p, p, 1 << 24, p, None) == L.ERR_INVALID
     assert lib.spectra_silu_mul(p, 100, 1, 64, p, None) == L.ERR_INVALID
