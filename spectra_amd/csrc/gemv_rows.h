@@ -578,7 +578,10 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
     rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
     build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, W, c.lane);
     rows_rotate<XC, BF, PRO>(p, c, smem, wave, W, tid, pr);
-    __syncthreads();  // --- LUT, activation pairs, scales
+    // --- LUT, activation pairs, scales: this wave's LDS writes complete, then the barrier.
+    //     (__syncthreads would also wait for every outstanding global load, the weight
+    //     runs included, and so hold the decode back until the whole stream has landed.)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     if (wave * RW >= c.Rw) {  // a wave without rows (it only helped with the activations)
       __builtin_amdgcn_s_waitcnt(0);  // its dummy loads land before it ends
       return;

@@ -86,7 +86,8 @@ def _tables(L, hd):
 
 @pytest.mark.parametrize("heads,kv,hd,L", [(24, 8, 128, 768), (4, 4, 64, 1000), (8, 2, 256, 130), (6, 3, 64, 64),
                                            (32, 4, 128, 300), (12, 2, 64, 200), (24, 8, 128, 1100),
-                                           (4, 2, 16, 128), (4, 2, 16, 70), (8, 4, 32, 150)])
+                                           (4, 2, 16, 128), (4, 2, 16, 70), (8, 4, 32, 150),
+                                           (20, 4, 64, 300), (14, 2, 128, 200), (16, 2, 256, 200)])
 @pytest.mark.parametrize("rope", [True, False])
 def test_attend_decode(hip, heads, kv, hd, L, rope):
     g = torch.Generator(device="cuda").manual_seed(heads * L + rope)
