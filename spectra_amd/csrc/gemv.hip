@@ -6,6 +6,7 @@
 
 #include "gemv_kernel.h"
 #include "gemv_rows_inst.h"
+#include "gemv_rows_lm.h"
 #include "gemv_stream.h"
 
 namespace spectra {
@@ -282,6 +283,84 @@ static bool plan_rows(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block,
   return off <= 163840;
 }
 
+// The multi-pass row kernel (gemv_rows_lm.h): one workgroup per CU of 8 waves, R = ceil(N /
+// CUs) rows each, streamed in passes of 8 x RW rows; for the shapes whose rows outgrow the
+// row kernel's plan (the lm_head) and for the fused greedy pick.
+struct LmPlan {
+  int G, SPR, R, W, grid;
+  uint32_t off_xp, off_xsc, off_ss, lds_bytes;
+};
+
+static bool rows_lm_serves(const spectra_qweight_t* w, int m, int act_dtype, int kpro,
+                           const spectra_gemv_fusion_t* fu, LmPlan* pl) {
+  if (m != 1 || w->format != SPECTRA_FMT_NF4 || w->group_size < 32 || w->group_size > 1024) return false;
+  if (w->hadamard_block != 0 && w->hadamard_block != 128) return false;
+  if (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS) return false;
+  if (w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz >= (int64_t(1) << 29)) return false;
+  if (w->bias != nullptr || (fu != nullptr && fu->residual != nullptr)) return false;
+  if (kpro != kProNone && kpro != kProRms) return false;
+  if (kpro != kProNone && act_dtype != SPECTRA_F16) return false;
+  const int64_t k = w->k;
+  if (k % 1024 != 0) return false;
+  const int P = (int)(k / 1024);
+  const int G = P % 2 == 0 ? 64 : 32;
+  const int SPR = P * 32 / G;
+  if (gemv_rows_lm_pick(G, SPR, act_dtype == SPECTRA_BF16, kpro) == nullptr) return false;
+  const int ncu = device_cu_count();
+  const int64_t R = (w->n + ncu - 1) / ncu;
+  if (R * w->packed_stride >= (int64_t(1) << 31) || R * w->scales_stride * 2 >= (int64_t(1) << 31)) return false;
+  pl->G = G; pl->SPR = SPR; pl->R = (int)R; pl->W = kLmWaves;
+  pl->grid = (int)((w->n + R - 1) / R);
+  uint32_t off = kLutBytes;
+  pl->off_xp = off;
+  off = align16(off + (uint32_t)(k * 2));
+  pl->off_xsc = off;
+  off = align16(off + (uint32_t)(k / 128 * 4));
+  pl->off_ss = off;
+  off = align16(off + (uint32_t)(kMaxWaves * 4));
+  pl->lds_bytes = off;
+  return off <= 163840;
+}
+
+static int rows_lm_launch(const spectra_qweight_t* w, const LmPlan& pl, const void* x, int act_dtype, void* out,
+                          hipStream_t stream, const spectra_gemv_fusion_t* fu, int kpro) {
+  RowsParams p{};
+  p.packed = w->packed; p.ldp = w->packed_stride;
+  p.absmax = w->scales; p.lda = w->scales_stride;
+  const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
+  p.rowptr = csr ? w->csr_rowptr : nullptr;
+  p.ccol = csr ? w->csr_col : nullptr;
+  p.cval = csr ? w->csr_val : nullptr;
+  p.csr = csr ? 1 : 0;
+  p.csr_nnz = csr ? (int)w->csr_nnz : 0;
+  p.bias = nullptr;
+  p.x = x; p.out = out;
+  p.nw = fu ? fu->norm_weight : nullptr;
+  p.res = nullptr;
+  p.eps = fu ? fu->eps : 0.0f;
+  p.had = w->hadamard_block;
+  p.out_scale = w->hadamard_block ? (float)(1.0 / std::sqrt((double)w->hadamard_block)) : 1.0f;
+  p.n = (int)w->n; p.k = (int)w->k;
+  p.R = 0;  // the producers stage no block scales: the row waves read them with the runs
+  p.nchunk = (int)(w->k / 512);
+  int gs = 0;
+  while ((1 << gs) < w->group_size) ++gs;
+  p.gshift = gs;
+  p.marlin = w->marlin_layout ? 1 : 0;
+  p.cpr = (int)(w->k / w->group_size / 8);
+  p.cmagic = p.cpr > 0 ? (65536 + p.cpr - 1) / p.cpr : 0;
+  p.off_xp = pl.off_xp; p.off_xsc = pl.off_xsc; p.off_ss = pl.off_ss;
+  p.wr = 0;
+  p.W = pl.W;
+  unsigned long long* akey = fu != nullptr ? (unsigned long long*)fu->argmax_key : nullptr;
+  const gemv_rows_lm_fn fn = gemv_rows_lm_pick(pl.G, pl.SPR, act_dtype == SPECTRA_BF16, kpro);
+  const int st = ensure_lds_limit((const void*)fn, true);
+  if (st != SPECTRA_OK) return st;
+  hipLaunchKernelGGL(fn, dim3(pl.grid), dim3(64 * pl.W), pl.lds_bytes, stream, p, pl.R, akey);
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
 static bool rows_serves(const spectra_qweight_t* w, int m, int act_dtype, int kpro, RowsPlan* pl) {
   if (m != 1 || w->format != SPECTRA_FMT_NF4 || w->group_size < 32) return false;
   if (w->hadamard_block != 0 && w->hadamard_block != 128) return false;
@@ -375,10 +454,12 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
                     "CSR columns must be 16-byte and values 8-byte aligned (nnz < 2^31)");
   // the kernels pair each format with its own outlier kind and scale scheme: Format B
   // (NF4, blocks >= 64, CSR outliers), Format A (groups of 32, dense outlier columns)
-  // (the greedy pick rides on the epilogue of the kernel below only)
+  // (the greedy pick rides on the epilogues of the multi-pass row kernel and the multi-row kernel)
   const bool pick = fu != nullptr && fu->argmax_key != nullptr;
   RowsPlan rp;
   if (!pick && rows_serves(w, m, act_dtype, kpro, &rp)) return rows_launch(w, rp, x, act_dtype, out, stream, fu, kpro);
+  LmPlan lp;
+  if (rows_lm_serves(w, m, act_dtype, kpro, fu, &lp)) return rows_lm_launch(w, lp, x, act_dtype, out, stream, fu, kpro);
   StreamPlan sp;
   if (!pick && stream_serves(w, m, &sp)) return stream_launch(w, sp, x, act_dtype, out, stream, fu, kpro);
   if (w->format == SPECTRA_FMT_NF4 && w->group_size < 64)

@@ -384,29 +384,41 @@ __device__ __forceinline__ void rows_decode(const uint4& w, uint32_t lanebits, u
   }
 }
 
-// one slot's dot product with the rotated activations of its run, scaled into the row's sum
-template <int G, int SPR>
-__device__ __forceinline__ float rows_dot(const RowsParams& p, const RowsCtx& c, const uint8_t* smem, int s, int j,
-                                          const uint32_t (&dec)[16]) {
+// the rotated activations of one run (lane li of chunk-slot c: run c * G + li): 16 dwords of
+// fp16 pairs and the run's 128-block scale, read once and shared by the group's RPG rows
+struct XRun {
+  uint32_t xpair[16];
+  float xs;
+  int q;
+};
+
+template <int G>
+__device__ __forceinline__ XRun rows_xrun(const RowsParams& p, const RowsCtx& c, const uint8_t* smem, int ch) {
   const int Q = c.Q;
   const uint4* xp4 = (const uint4*)(smem + p.off_xp);
   const float* xsc = (const float*)(smem + p.off_xsc);
-  const float* scf = (const float*)(smem + p.off_sc);
-  const int q = (s % SPR) * G + c.li;
-  uint32_t xpair[16];
+  XRun r;
+  r.q = ch * G + c.li;
 #pragma unroll
   for (int cc = 0; cc < 4; ++cc) {
-    const uint4 a = xp4[cc * Q + q];
-    xpair[4 * cc] = a.x; xpair[4 * cc + 1] = a.y; xpair[4 * cc + 2] = a.z; xpair[4 * cc + 3] = a.w;
+    const uint4 a = xp4[cc * Q + r.q];
+    r.xpair[4 * cc] = a.x; r.xpair[4 * cc + 1] = a.y; r.xpair[4 * cc + 2] = a.z; r.xpair[4 * cc + 3] = a.w;
   }
-  const float xs = xsc[q >> 2];
+  r.xs = xsc[r.q >> 2];
+  return r;
+}
+
+// one slot's dot product with the rotated activations of its run, scaled into the row's sum
+__device__ __forceinline__ float rows_dot(const RowsParams& p, const RowsCtx& c, const uint8_t* smem, const XRun& x,
+                                          int j, const uint32_t (&dec)[16]) {
+  const float* scf = (const float*)(smem + p.off_sc);
   const int rowc = min(c.grow0 + j, c.Rw - 1);
-  const float am = scf[rowc * (c.K >> p.gshift) + (q >> (p.gshift - 5))];
+  const float am = scf[rowc * (c.K >> p.gshift) + (x.q >> (p.gshift - 5))];
   float d = 0.0f;
 #pragma unroll
   for (int b = 0; b < 16; ++b)
-    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, dec[b]), __builtin_bit_cast(f16x2_t, xpair[b]), d, false);
-  return d * (am * xs);
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, dec[b]), __builtin_bit_cast(f16x2_t, x.xpair[b]), d, false);
+  return d * (am * x.xs);
 }
 
 // the row waves' work once the weights are issued: the first NP slots are decoded as they
@@ -429,13 +441,22 @@ __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& 
 #pragma unroll
   for (int s = 0; s < NP; ++s) rows_decode(r.wq[s], lanebits, pre[s]);
   wait_x();
+  // chunk-slot major: each run's activations are read once for the group's RPG rows (slot
+  // s = j * SPR + ch); every row still sums its chunk-slots in order
 #pragma unroll
-  for (int s = 0; s < NP; ++s) acc[s / SPR] += rows_dot<G, SPR>(p, c, smem, s, s / SPR, pre[s]);
+  for (int ch = 0; ch < SPR; ++ch) {
+    const XRun xr = rows_xrun<G>(p, c, smem, ch);
 #pragma unroll
-  for (int s = NP; s < NS; ++s) {
-    uint32_t dec[16];
-    rows_decode(r.wq[s], lanebits, dec);
-    acc[s / SPR] += rows_dot<G, SPR>(p, c, smem, s, s / SPR, dec);
+    for (int j = 0; j < RPG; ++j) {
+      const int s = j * SPR + ch;
+      if (s < NP) {
+        acc[j] += rows_dot(p, c, smem, xr, j, pre[s < NP ? s : 0]);
+      } else {
+        uint32_t dec[16];
+        rows_decode(r.wq[s], lanebits, dec);
+        acc[j] += rows_dot(p, c, smem, xr, j, dec);
+      }
+    }
   }
   // outliers: entry value x rotated activation, into the row's lanes
   if (p.csr) {
