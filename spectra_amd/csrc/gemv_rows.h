@@ -117,10 +117,10 @@ struct RowsCtx {
   int tid, lane, wave, W, K, Q, r0, Rw, gi, li, grow0;
 };
 
-// producer loads: the workgroup's block scales (one 16-byte chunk per producer thread below
-// R * cpr), bias and residual (producer threads below Rw), then the activation chunks
-// pw + np i (lane (i, g) = (lane & 15, lane >> 4) holds elements 32 i + 8 g .. + 7 of the
-// chunk, the MFMA A operand; chunks past the last read chunk 0)
+// producer loads: the activation chunks pw + np i (lane (i, g) = (lane & 15, lane >> 4)
+// holds elements 32 i + 8 g .. + 7 of the chunk, the MFMA A operand; chunks past the last
+// read chunk 0), then the workgroup's block scales (one 16-byte chunk per producer thread
+// below R * cpr), bias and residual (producer threads below Rw)
 template <int XC, int PRO>
 struct ProducerRegs {
   uint4 scv;
@@ -132,6 +132,17 @@ struct ProducerRegs {
 template <int XC, int PRO>
 __device__ __forceinline__ void rows_producer_loads(const RowsParams& p, const RowsCtx& c, int pw, int np, int ptid,
                                                     ProducerRegs<XC, PRO>& r) {
+  // the activation chunks first: the rotation waits for them, and a wait counts every load
+  // issued before the one it waits for (the block scales below come from HBM, cold)
+  const uint32_t xlo = 64u * (uint32_t)(c.lane & 15) + 16u * (uint32_t)(c.lane >> 4);
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int ch = pw + np * i;
+    const uint32_t o = (ch < p.nchunk ? (uint32_t)ch * 1024u : 0u) + xlo;
+    r.xr[i] = load_at<uint4>(p.x, o);
+    if constexpr (PRO == kProSiluMul) r.xu[i] = load_at<uint4>(p.x, o + 2u * (uint32_t)c.K);
+    if constexpr (PRO == kProRms) r.nwr[i] = load_at<uint4>(p.nw, o);
+  }
   const int srow = (ptid * p.cmagic) >> 16;  // ptid / cpr
   if (pw * 64 < p.R * p.cpr) {
     const int sr = srow < c.Rw ? srow : 0;
@@ -145,15 +156,6 @@ __device__ __forceinline__ void rows_producer_loads(const RowsParams& p, const R
       else r.bias_raw = load_at<uint16_t>((const uint16_t*)p.bias + c.r0, 2u * ti);
     }
     if (p.res != nullptr) r.res_raw = load_at<uint16_t>((const uint16_t*)p.res + c.r0, 2u * ti);
-  }
-  const uint32_t xlo = 64u * (uint32_t)(c.lane & 15) + 16u * (uint32_t)(c.lane >> 4);
-#pragma unroll
-  for (int i = 0; i < XC; ++i) {
-    const int ch = pw + np * i;
-    const uint32_t o = (ch < p.nchunk ? (uint32_t)ch * 1024u : 0u) + xlo;
-    r.xr[i] = load_at<uint4>(p.x, o);
-    if constexpr (PRO == kProSiluMul) r.xu[i] = load_at<uint4>(p.x, o + 2u * (uint32_t)c.K);
-    if constexpr (PRO == kProRms) r.nwr[i] = load_at<uint4>(p.nw, o);
   }
 }
 
