@@ -326,6 +326,63 @@ def test_stream_gemv_shapes(hip, k, had, marlin, act, bias):
     check_y(y, y_ref, TDT[act])
 
 
+@pytest.mark.parametrize("n,k,had,marlin,act,prologue", [
+    (40000, 3072, 128, True, "float16", None),      # lane groups of 32, passes of 32 rows
+    (45000, 4096, 0, False, "bfloat16", None),      # lane groups of 64, passes of 16 rows
+    (41000, 2048, 128, True, "float16", "rmsnorm"),
+])
+def test_multipass_gemv_shapes(hip, n, k, had, marlin, act, prologue):
+    """One-row shapes with more rows per CU (150-180) than the row-owning plan holds, served
+    by the multi-pass row kernel (the lm_head's): passes with the next pass's loads in flight,
+    partial last passes, the last workgroup's shorter row range, a row with more CSR entries
+    than lanes, and its greedy pick.  The operands come from the GPU quantizer; its codes and
+    the GPU dequant are pinned bit for bit to the oracle on sampled rows (pass and workgroup
+    boundaries, the dense-outlier row), then y is checked against the oracle product on that
+    W_eff."""
+    case(n=n, k=k, had=had, marlin=marlin, act=act, prologue=prologue)
+    g = torch.Generator().manual_seed(n + k)
+    w = (torch.randn(n, k, generator=g) * 0.02).half()
+    mask = torch.rand(n, k, generator=g) < 0.005
+    mask[5, ::4] = True
+    w[mask] = (torch.randn(int(mask.sum()), generator=g) * 0.2).half()
+    q = C.quantize_nf4(w.cuda(), 64, 0, mask.cuda(), marlin)
+    rd = act if act == "float16" else "float32"
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    R = -(-n // ncu)
+    pr = 32 if (k // 1024) % 2 else 16  # rows per pass: 8 waves x 2 rows x (64 / lanes per group)
+    rows = sorted({0, 5, pr - 1, pr, R - 1, R, R + pr, (n // R) * R - 1, (n // R) * R, n - 1})
+    rows = np.array([r for r in rows if r < n])
+    sub = O.nf4_quantize(w.numpy()[rows], "float16", 64, 0, mask.numpy()[rows], marlin)
+    assert np.array_equal(host(q.packed)[rows], sub["packed"]) and np.array_equal(host(q.absmax)[rows], sub["absmax"])
+    w_eff_t = K.w4_dequant(q.packed, q.absmax, None, out_dtype=TDT[rd], codebook="nf4", marlin_layout=marlin,
+                           outlier_idx=q.col, outlier_w=q.val, outlier_rowptr=q.rowptr)
+    w_eff = host(w_eff_t)
+    del w_eff_t
+    ref_rows = O.nf4_dequant(sub["packed"], sub["absmax"], marlin, rd, sub["rowptr"], sub["col"], sub["val"])
+    assert np.array_equal(w_eff[rows], ref_rows)
+    ops = K.QWeightOperands(q.packed, q.absmax, None, k, codebook="nf4", group_size=64, hadamard_block=had,
+                            marlin_layout=marlin, outlier_idx=q.col, outlier_w=q.val, outlier_rowptr=q.rowptr)
+    slots = K.argmax_slots()
+    token = torch.zeros(1, dtype=torch.int64, device="cuda")
+    rng = np.random.default_rng(n)
+    if prologue == "rmsnorm":
+        h = (rng.standard_normal((1, k)) * 3).astype(np.float16)
+        nw = (rng.random(k) + 0.5).astype(np.float16)
+        y = K.w4a16_gemv_fused(ops, cuda(h), prologue="rmsnorm", norm_weight=cuda(nw), eps=1e-5, argmax_key=slots)
+        hf = h.astype(np.float64)
+        x, xdt = (hf / np.sqrt((hf * hf).mean() + 1e-5) * nw.astype(np.float64)).astype(np.float32), "float32"
+    else:
+        x, xdt = O.round_to(rand_np(rng, (1, k), 1.0, np.float32), act), act
+        if act == "float16":
+            y = K.w4a16_gemv_fused(ops, cuda(x, TDT[act]), argmax_key=slots)
+        else:  # (the fused entry's pick takes fp16 activations)
+            y = K.w4a16_linear(ops, cuda(x, TDT[act]))
+    check_y(y, O.linear_ref(x, xdt, w_eff, rd, hadamard_block=had), TDT[act])
+    if act == "float16":
+        K.greedy_finish(slots, token)
+        assert int(token) == int(torch.argmax(y.float().reshape(-1)))
+
+
 @pytest.mark.parametrize("k,had,marlin,prologue", [(6144, 128, True, "rmsnorm"), (5120, 128, False, "rmsnorm"),
                                                    (5120, 128, True, "silu_mul"), (1024, 64, False, "silu_mul")])
 def test_stream_gemv_prologues(hip, k, had, marlin, prologue):
