@@ -145,10 +145,15 @@ int spectra_w4a16_gemv_fused(const spectra_qweight_t* w, const void* x, int64_t 
 
 /*
  * Batched / prefill GEMM family (any M >= 1, MFMA):
- *   out = FWHT_hb(a) . W_eff^T + bias,   fp16 MFMA operands, fp32 accumulation.
+ *   out = FWHT_hb(a) . W_eff^T + bias,   fp32 accumulation.
  * a: act_dtype [m, K] row stride lda; out: act_dtype [m, N] row stride ldo.
- * workspace: device scratch of at least spectra_w4a16_gemm_workspace() bytes
- * (may be NULL when that size is 0).  Replaces kernels.py:333-389.
+ * 2 <= m <= 16: small-batch stream; otherwise the hand-written GEMM (fp16 operands); from
+ * m >= 1024, when the workspace holds it, W_eff dequantized into the workspace in act_dtype
+ * and one hipBLASLt GEMM on it (the reference kernel's operand rounding).
+ * workspace: device scratch of spectra_w4a16_gemm_workspace() bytes, which serves every
+ * family (from m >= 1024 it includes N*K*2 + m*K*2 bytes + 32 MiB for the library path); a
+ * smaller one that holds the hand-written GEMM's buffers runs that GEMM.  May be NULL when
+ * the size is 0.  Replaces kernels.py:333-389.
  */
 size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64_t m, int32_t act_dtype);
 int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int64_t lda, int64_t m,

@@ -105,6 +105,7 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
                 int64_t ldo, hipStream_t stream, const spectra_gemv_fusion_t* fusion);
 int gemv_plan_grid(const spectra_qweight_t* w, int m);
 int skinny_supported(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m);
+size_t gemm_workspace_min(const spectra_qweight_t* w, int64_t m);
 }
 
 extern "C" const char* spectra_version(void) { return "spectra_hip 0.1.0 gfx950"; }
@@ -153,7 +154,9 @@ extern "C" int spectra_w4a16_linear_noalloc(const spectra_qweight_t* w, const vo
   int st = spectra::validate_qweight(w);
   if (st != SPECTRA_OK) return st;
   SPECTRA_REQUIRE(m >= 1, "m must be >= 1");
-  const size_t need = m >= 2 ? spectra_w4a16_gemm_workspace(w, m, act_dtype) : 0;
+  // the MFMA families' buffers (at m >= 1024 the library path, whose workspace holds the
+  // whole dequantized weight, is not taken from the scratch)
+  const size_t need = m >= 2 ? spectra::gemm_workspace_min(w, m) : 0;
   if (need > (size_t)SPECTRA_NOALLOC_SCRATCH_BYTES)
     return spectra::fail(SPECTRA_ERR_WORKSPACE,
                          "this call needs " + std::to_string(need) + " bytes of workspace, more than the " +

@@ -50,6 +50,118 @@ __global__ void __launch_bounds__(kDqThreads) scatter_csr_kernel(spectra_qweight
     store_elem(out, row * ldo + w.csr_col[e], out_dt, h2f(w.csr_val[e]));
 }
 
+// f2bf without a branch (same bits: round to nearest even, NaN quieted)
+__device__ __forceinline__ uint32_t f2bf_sel(float f) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : r;
+}
+
+// Row dequant at HBM rate (the prefill path materialises whole weights with it).  One wave per
+// (row, segment of kDqSegChunks 32-element runs); in a pass over a block of 64 kE elements
+// lane l owns the kE consecutive outputs kE l .. kE l + kE - 1 (kE = 8 for 16-bit, 4 for
+// fp32 outputs), so every store instruction of the wave writes 1 KB contiguously.  In both
+// nibble orders the 16 bytes of run c hold elements 32 c .. 32 c + 31 under one scale (group
+// size a multiple of 32): with the marlin pairs (k, k + 16) a lane reads kE bytes and takes
+// their low (first half of the run) or high nibbles, in the natural order kE / 2 bytes and
+// both nibbles.  All of a segment's loads are issued before the first decode.  The NF4 codes
+// come from a 16-entry LDS table.  Same values and roundings as dequant_kernel.  After the
+// segment's dense stores have completed (the wave waits on its store counter; the fence keeps
+// the compiler from moving stores across), the same wave stores the row's outliers that fall
+// in its segment over them, so they land last.
+constexpr int kDqSegChunks = 128;  // 4096 elements
+
+template <int kOut, bool kMarlin>
+struct DqShape {
+  static constexpr int kE = kOut == SPECTRA_F32 ? 4 : 8;   // outputs per lane per pass
+  static constexpr int kPasses = kDqSegChunks * 32 / (64 * kE);
+  static constexpr int kBytes = kMarlin ? kE : kE / 2;      // packed bytes per lane per pass
+};
+
+template <int kBytes>
+__device__ __forceinline__ uint64_t load_bytes(const uint8_t* p) {
+  if (kBytes == 8) return *(const uint64_t*)p;
+  if (kBytes == 4) return *(const uint32_t*)p;
+  return *(const uint16_t*)p;
+}
+
+// kOut: SPECTRA_F16, SPECTRA_BF16 or SPECTRA_F32
+template <bool kAsym, int kOut, bool kMarlin>
+__global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweight_t w, void* __restrict__ out,
+                                                                   int64_t ldo, int out_dt, int nseg) {
+  typedef DqShape<kOut, kMarlin> S;
+  __shared__ float code[16];
+  if (threadIdx.x < 16) code[threadIdx.x] = nf4_code_f32((int)threadIdx.x);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = (int64_t)blockIdx.x * (kDqThreads / 64) + (threadIdx.x >> 6);
+  const int64_t row = wid / nseg;
+  if (row >= w.n) return;
+  const int nch = (int)(w.k >> 5);
+  const int c0 = (int)(wid - row * nseg) * kDqSegChunks;
+  const int e_end = 32 * (min(nch, c0 + kDqSegChunks) - c0);  // elements of this segment
+  const int gch = kAsym ? 1 : w.group_size >> 5;              // runs per scale group
+  const uint8_t* prow = w.packed + row * w.packed_stride + 16 * (int64_t)c0;
+  uint64_t qb[S::kPasses];
+#pragma unroll
+  for (int b = 0; b < S::kPasses; ++b) {
+    const int o = 64 * S::kE * b + S::kE * lane;  // first element of the lane's outputs
+    const int e0 = o & 31;
+    if (o < e_end)
+      qb[b] = load_bytes<S::kBytes>(prow + 16 * (o >> 5) + (kMarlin ? (e0 & 15) : (e0 >> 1)));
+  }
+#pragma unroll
+  for (int b = 0; b < S::kPasses; ++b) {
+    const int o = 64 * S::kE * b + S::kE * lane;
+    if (o >= e_end) break;
+    const int c = c0 + (o >> 5), e0 = o & 31;
+    const float s = h2f(w.scales[row * w.scales_stride + c / gch]);
+    const float z = kAsym ? (float)w.zeros[row * w.zeros_stride + c] : 0.0f;
+    float v[S::kE];
+#pragma unroll
+    for (int i = 0; i < S::kE; ++i) {
+      // nibble of output e0 + i: marlin -> byte (e0 & 15) + i, high half when e0 >= 16;
+      // natural -> byte e0 / 2 + i / 2, high nibble for odd i
+      const int bit = kMarlin ? 8 * i : 8 * (i >> 1);
+      const uint32_t byte = (uint32_t)(qb[b] >> bit) & 0xffu;
+      const uint32_t q = kMarlin ? (e0 >= 16 ? byte >> 4 : byte & 15u) : ((i & 1) ? byte >> 4 : byte & 15u);
+      v[i] = kAsym ? ((float)q - z) * s : code[q] * s;
+      if (kOut == SPECTRA_F16) {
+        // the product is rounded to fp32 first, then to fp16 (the compiler would otherwise fold
+        // the product and the conversion into one v_fma_mixlo_f16)
+        asm volatile("" : "+v"(v[i]));
+      }
+    }
+    if (kOut == SPECTRA_F32) {
+      *(float4*)((float*)out + row * ldo + 32 * (int64_t)c0 + o) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint32_t p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        p[i] = kOut == SPECTRA_BF16 ? f2bf_sel(v[2 * i]) | (f2bf_sel(v[2 * i + 1]) << 16)
+                                    : (uint32_t)f2h(v[2 * i]) | ((uint32_t)f2h(v[2 * i + 1]) << 16);
+      *(uint4*)((uint16_t*)out + row * ldo + 32 * (int64_t)c0 + o) = make_uint4(p[0], p[1], p[2], p[3]);
+    }
+  }
+  const int64_t k0 = 32 * (int64_t)c0, k1 = k0 + e_end;
+  if (w.outlier_kind == SPECTRA_OUTLIERS_COLUMNS) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int j = lane; j < w.num_outliers; j += 64) {
+      const int64_t col = w.outlier_idx[j];
+      if (col >= k0 && col < k1)
+        store_elem(out, row * ldo + col, out_dt, load_elem(w.outlier_w, row * w.outlier_w_stride + j, w.outlier_w_dtype));
+    }
+  } else if (w.outlier_kind == SPECTRA_OUTLIERS_CSR) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int e = w.csr_rowptr[row] + lane; e < w.csr_rowptr[row + 1]; e += 64) {
+      const int col = w.csr_col[e];
+      if (col >= k0 && col < k1) store_elem(out, row * ldo + col, out_dt, h2f(w.csr_val[e]));
+    }
+  }
+}
+
 // Embedding gather (engine.py:127-212, SpectraFusedEmbedding.forward): row ids[b] of
 // W_eff, bit-identical to the same row of spectra_w4_dequant.  One workgroup per id: the
 // dense values first, then (after the barrier) the row's outlier columns / CSR entries.
@@ -115,6 +227,30 @@ extern "C" int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t
   SPECTRA_REQUIRE(ldo >= w->k, "out row stride smaller than K");
   SPECTRA_REQUIRE(out_dtype >= SPECTRA_F16 && out_dtype <= SPECTRA_F32, "bad out dtype");
   const hipStream_t s = (hipStream_t)stream;
+  const int esz = out_dtype == SPECTRA_F32 ? 4 : 2;
+  const bool asym = w->format == SPECTRA_FMT_ASYM_G32;
+  if (w->k % 32 == 0 && (asym || w->group_size % 32 == 0) && (reinterpret_cast<uintptr_t>(w->packed) % 16) == 0 &&
+      w->packed_stride % 16 == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0 && (ldo * esz) % 16 == 0) {
+    // [asym][out dtype][marlin]
+    static const void* const kerns[2][3][2] = {
+        {{(const void*)dequant_rows_kernel<false, SPECTRA_F16, false>, (const void*)dequant_rows_kernel<false, SPECTRA_F16, true>},
+         {(const void*)dequant_rows_kernel<false, SPECTRA_BF16, false>, (const void*)dequant_rows_kernel<false, SPECTRA_BF16, true>},
+         {(const void*)dequant_rows_kernel<false, SPECTRA_F32, false>, (const void*)dequant_rows_kernel<false, SPECTRA_F32, true>}},
+        {{(const void*)dequant_rows_kernel<true, SPECTRA_F16, false>, (const void*)dequant_rows_kernel<true, SPECTRA_F16, true>},
+         {(const void*)dequant_rows_kernel<true, SPECTRA_BF16, false>, (const void*)dequant_rows_kernel<true, SPECTRA_BF16, true>},
+         {(const void*)dequant_rows_kernel<true, SPECTRA_F32, false>, (const void*)dequant_rows_kernel<true, SPECTRA_F32, true>}}};
+    const int oi = out_dtype == SPECTRA_F16 ? 0 : out_dtype == SPECTRA_BF16 ? 1 : 2;
+    const void* kern = kerns[asym ? 1 : 0][oi][w->marlin_layout ? 1 : 0];
+    spectra_qweight_t wc = *w;
+    int odt = (int)out_dtype;
+    int nseg = (int)((w->k / 32 + kDqSegChunks - 1) / kDqSegChunks);
+    void* args[] = {(void*)&wc, (void*)&out, (void*)&ldo, (void*)&odt, (void*)&nseg};
+    const int64_t waves = w->n * nseg, per_block = kDqThreads / 64;
+    SPECTRA_HIP_CHECK(hipLaunchKernel(kern, dim3((unsigned)((waves + per_block - 1) / per_block)), dim3(kDqThreads),
+                                      args, 0, s));
+    SPECTRA_HIP_CHECK(hipGetLastError());
+    return SPECTRA_OK;
+  }
   const int64_t work = w->n * (w->k / 2);
   hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((work + kDqThreads - 1) / kDqThreads)), dim3(kDqThreads), 0, s,
                      *w, out, ldo, (int)out_dtype);

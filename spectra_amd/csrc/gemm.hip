@@ -59,11 +59,13 @@ __device__ __forceinline__ int tile_swz(int r) {
 // written in packed-byte pair order.
 constexpr int kPrepMaxU = 16;  // K <= 256 * 8 * 16 = 32768
 
+// raw_dt >= 0 (the library-GEMM path): no scale (F = 0), the rotated row rounded to raw_dt
+// (SPECTRA_F16 or SPECTRA_BF16), the compute dtype of the reference's GEMM; marlin must be 0.
 template <int kPrepU>
 __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __restrict__ a, int64_t lda, int dt,
                                                                   int k, int log_had, float div, int marlin, int vec,
                                                                   uint16_t* __restrict__ a16,
-                                                                  int32_t* __restrict__ fexp) {
+                                                                  int32_t* __restrict__ fexp, int raw_dt) {
   extern __shared__ float fs[];  // [k] fp32 (the 1024-block stage), then [k] fp16 (pair-order write)
   __shared__ float wmax[kPrepThreads / 64];
   const int64_t row = blockIdx.x;
@@ -153,6 +155,7 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
   const int E = eb == 0 ? -126 : eb - 127;
   int F = bits == 0 ? 0 : 14 - E;  // max |x_rot| * 2^F in [2^14, 2^15): exact scaling, no overflow
   F = F < -126 ? -126 : (F > 126 ? 126 : F);
+  if (raw_dt >= 0) F = 0;
   const float f2 = __builtin_bit_cast(float, (uint32_t)(F + 127) << 23);
   // output scale: 2^F / sqrt(block) (one rounding), with the lane's butterfly sign
   const float f = sgn * (log_had > 0 ? f2 / div : f2);
@@ -191,12 +194,38 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
         uint32_t d[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          d[e] = (uint32_t)f2h(v[u][2 * e] * f) | ((uint32_t)f2h(v[u][2 * e + 1] * f) << 16);
+          d[e] = raw_dt >= 0 ? (uint32_t)from_f32_16(v[u][2 * e] * f, raw_dt) |
+                                   ((uint32_t)from_f32_16(v[u][2 * e + 1] * f, raw_dt) << 16)
+                             : (uint32_t)f2h(v[u][2 * e] * f) | ((uint32_t)f2h(v[u][2 * e + 1] * f) << 16);
         *(uint4*)(a16 + row * k + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
       }
     }
   }
   if (tid == 0) fexp[row] = F;
+}
+
+// the activation prep of the library-GEMM path: every row rotated (natural order) and
+// rounded to the activation dtype dt, unscaled
+int gemm_prep_rotate(const void* a, int64_t lda, int64_t m, int dt, int k, int had, uint16_t* a16, int32_t* fexp,
+                     hipStream_t s) {
+  int log_had = 0;
+  while (had > 1 && (1 << log_had) < had) ++log_had;
+  const float div = had > 1 ? (float)std::sqrt((double)had) : 1.0f;
+  const int64_t n8 = k / 8;
+  const int pu = n8 <= 256 ? 1 : n8 <= 512 ? 2 : n8 <= 1024 ? 4 : n8 <= 2048 ? 8 : 16;
+  const void* prep = pu == 1 ? (const void*)gemm_prep_kernel<1> : pu == 2 ? (const void*)gemm_prep_kernel<2>
+                   : pu == 4 ? (const void*)gemm_prep_kernel<4> : pu == 8 ? (const void*)gemm_prep_kernel<8>
+                             : (const void*)gemm_prep_kernel<16>;
+  int st = ensure_lds_limit(prep);
+  if (st != SPECTRA_OK) return st;
+  const int vec = (reinterpret_cast<uintptr_t>(a) % 16) == 0 && lda % 8 == 0;
+  const int marl = 0, raw_dt = dt;
+  const size_t prep_lds = (size_t)k * (had > 512 ? 4 : 2);
+  void* pargs[] = {(void*)&a, (void*)&lda, (void*)&dt, (void*)&k, (void*)&log_had, (void*)&div, (void*)&marl,
+                   (void*)&vec, (void*)&a16, (void*)&fexp, (void*)&raw_dt};
+  SPECTRA_HIP_CHECK(hipLaunchKernel(prep, dim3((unsigned)m), dim3(kPrepThreads), pargs, prep_lds, s));
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
 }
 
 // ---------------------------------------------------------------------------
@@ -687,6 +716,11 @@ static int64_t outlier_entries(const spectra_qweight_t* w) {
   return 0;
 }
 
+// prefill.hip: the library GEMM path (m >= 1024)
+size_t prefill_workspace(const spectra_qweight_t* w, int64_t m, int act_dtype);
+int prefill_launch(const spectra_qweight_t* w, const void* a, int64_t lda, int64_t m, int act_dtype, void* out,
+                   int64_t ldo, void* workspace, size_t workspace_bytes, hipStream_t s);
+
 // skinny.hip: the small-batch MFMA family (2 <= m <= 16)
 size_t skinny_workspace(const spectra_qweight_t* w, int64_t m);
 int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m, int act_dtype, void* out,
@@ -696,8 +730,10 @@ int skinny_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_
 
 using namespace spectra;
 
-extern "C" size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64_t m, int32_t act_dtype) {
-  (void)act_dtype;
+namespace spectra {
+// the MFMA families' own buffers: every call of the GEMM entry runs with this much (the
+// library path of m >= 1024 needs more and runs only when the workspace holds it)
+size_t gemm_workspace_min(const spectra_qweight_t* w, int64_t m) {
   if (w == nullptr || m <= 0) return 0;
   const GemmPlan g = plan_gemm(m, w->n, w->k);
   size_t gemm = align256((size_t)m * (size_t)w->k * 2) + align256((size_t)m * 4) +
@@ -708,6 +744,13 @@ extern "C" size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64
             align256((size_t)nent * 4);
   const size_t small = skinny_workspace(w, m);
   return gemm > small ? gemm : small;
+}
+}  // namespace spectra
+
+extern "C" size_t spectra_w4a16_gemm_workspace(const spectra_qweight_t* w, int64_t m, int32_t act_dtype) {
+  if (w == nullptr || m <= 0) return 0;
+  const size_t need = gemm_workspace_min(w, m), lib = prefill_workspace(w, m, act_dtype);
+  return need > lib ? need : lib;
 }
 
 extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int64_t lda, int64_t m,
@@ -726,14 +769,19 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   if (w->hadamard_block > 1024) return fail(SPECTRA_ERR_UNSUPPORTED, "the GEMM family serves hadamard_block <= 1024");
   SPECTRA_REQUIRE((reinterpret_cast<uintptr_t>(w->packed) % 16) == 0 && w->packed_stride % 16 == 0,
                   "packed weights must be 16-byte aligned with a row stride multiple of 16");
-  const size_t need = spectra_w4a16_gemm_workspace(w, m, act_dtype);
+  const size_t need = gemm_workspace_min(w, m);
   if (workspace == nullptr || workspace_bytes < need)
-    return fail(SPECTRA_ERR_WORKSPACE, "workspace missing or smaller than spectra_w4a16_gemm_workspace()");
+    return fail(SPECTRA_ERR_WORKSPACE, "workspace missing or smaller than the GEMM family needs "
+                                       "(spectra_w4a16_gemm_workspace() bytes serve every family)");
   SPECTRA_REQUIRE((reinterpret_cast<uintptr_t>(workspace) % 256) == 0, "workspace must be 256-byte aligned");
   const hipStream_t s = (hipStream_t)stream;
   if (m >= 2 && m <= 16) {  // HBM-bound small batches: the MFMA stream family when it serves the operands
     const int sst = skinny_launch(w, a, lda, m, act_dtype, out, ldo, workspace, workspace_bytes, s);
     if (sst != SPECTRA_ERR_UNSUPPORTED) return sst;
+  }
+  if (m >= 1024) {  // prompt sizes: dequantized weights on the matrix-core library GEMM
+    const int pst = prefill_launch(w, a, lda, m, act_dtype, out, ldo, workspace, workspace_bytes, s);
+    if (pst != SPECTRA_ERR_UNSUPPORTED) return pst;
   }
   uint16_t* a16 = (uint16_t*)workspace;
   int32_t* fexp = (int32_t*)((uint8_t*)workspace + align256((size_t)m * w->k * 2));
@@ -752,8 +800,9 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
   const int vec = (reinterpret_cast<uintptr_t>(a) % 16) == 0 && lda % 8 == 0;
   const int kk32 = (int)w->k, marl = w->marlin_layout ? 1 : 0;
   const size_t prep_lds = (size_t)w->k * (had > 512 ? 4 : 2);
+  const int scaled = -1;  // per-row power-of-two scale, fp16
   void* pargs[] = {(void*)&a, (void*)&lda, (void*)&act_dtype, (void*)&kk32, (void*)&log_had, (void*)&div,
-                   (void*)&marl, (void*)&vec, (void*)&a16, (void*)&fexp};
+                   (void*)&marl, (void*)&vec, (void*)&a16, (void*)&fexp, (void*)&scaled};
   SPECTRA_HIP_CHECK(hipLaunchKernel(prep, dim3((unsigned)m), dim3(kPrepThreads), pargs, prep_lds, s));
   SPECTRA_HIP_CHECK(hipGetLastError());
 

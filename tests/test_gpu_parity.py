@@ -22,6 +22,7 @@ import pytest
 import torch
 
 import oracle as O
+from spectra_amd import _lib as L
 from spectra_amd import compressor as C
 from spectra_amd import kernels as K
 from spectra_amd.engine import SpectraFusedEmbedding, SpectraFusedLinear
@@ -162,6 +163,64 @@ def test_dequant_format_b_bitexact(hip, out_dt):
         assert np.array_equal(host(w), g["w_eff16"])
     if out_dt == "bfloat16":
         assert np.array_equal(host(w), g["w_effbf"])
+
+
+@pytest.mark.parametrize("out_dt", ["float16", "bfloat16", "float32"])
+def test_dequant_every_code_and_scale(hip, out_dt):
+    """Every NF4 code under every finite fp16 absmax (63488 blocks of 64, each holding the 16
+    codes four times), dequantized by the row kernel: bit-exact against the oracle's fp32
+    product and its rounding to the output dtype (one rounding to fp32, then one to 16 bits)."""
+    case(out_dt=out_dt)
+    bits = np.arange(65536, dtype=np.uint32)
+    finite = bits[((bits >> 10) & 0x1F) != 0x1F].astype(np.uint16)  # 63488 patterns
+    n, k = 248, 16384
+    absmax = finite.view(np.float16).reshape(n, k // 64)
+    codes = (np.arange(k) % 16).astype(np.uint8)
+    packed = np.tile((codes[0::2] | (codes[1::2] << 4)).astype(np.uint8), (n, 1))  # natural nibble order
+    ref = O.nf4_dequant(packed, absmax, False, out_dt)
+    ops = K.QWeightOperands(cuda(packed), cuda(absmax), None, k, codebook="nf4", group_size=64, marlin_layout=False)
+    out = torch.empty((n, k), dtype=TDT[out_dt], device="cuda")
+    L.check("spectra_w4_dequant", lib_dequant(ops, out, k, out_dt))
+    got = host(out)
+    if out_dt == "float32":
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    else:
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def lib_dequant(ops, out, ldo, out_dt):
+    return L.load().spectra_w4_dequant(ops.ptr(), out.data_ptr(), ldo, K._DT[TDT[out_dt]], K._stream(out.device))
+
+
+@pytest.mark.parametrize("fmt,marlin,out_dt", [
+    ("nf4", False, "float16"), ("nf4", True, "bfloat16"), ("nf4", False, "float32"),
+    ("asym", True, "bfloat16"), ("asym", False, "float32"), ("asym", True, "float16"),
+])
+def test_dequant_row_and_general_kernels(hip, fmt, marlin, out_dt):
+    """spectra_w4_dequant runs the row kernel (a 16-byte chunk of packed bytes per lane, the
+    row's outliers stored over it afterwards) when rows and output are 16-byte aligned, and
+    the general kernel otherwise (here an output row stride of K + 1): both bit-exact against
+    the oracle, CSR and column outliers included.  K = 5120 spans two of the row kernel's
+    4096-element segments (the second one partial), each storing its own outliers."""
+    case(fmt=fmt, marlin=marlin, out_dt=out_dt)
+    n, k = 200, 5120
+    if fmt == "nf4":
+        q, _ = _format_b(11, n, k, 0, ratio=0.01, marlin=marlin)
+        ref = O.nf4_dequant(q["packed"], q["absmax"], marlin, out_dt, q["rowptr"], q["col"], q["val"])
+        ops = K.QWeightOperands(cuda(q["packed"]), cuda(q["absmax"]), None, k, codebook="nf4", group_size=64,
+                                marlin_layout=marlin, outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]),
+                                outlier_rowptr=cuda(q["rowptr"]))
+    else:
+        packed, scales, z, idx, ow, _ = _format_a(12, n, k, 16)
+        ref = O.apply_outlier_columns(O.dequant_group32(packed, scales, z, marlin, out_dt), idx, ow, out_dt)
+        ops = K.QWeightOperands(cuda(packed), cuda(scales), cuda(z), k, codebook="asym", marlin_layout=marlin,
+                                outlier_idx=cuda(idx), outlier_w=cuda(ow))
+    lib = L.load()
+    for ldo in (k, k + 1):
+        out = torch.full((n, ldo), float("nan"), dtype=TDT[out_dt], device="cuda")
+        L.check("spectra_w4_dequant", lib.spectra_w4_dequant(ops.ptr(), out.data_ptr(), ldo, K._DT[TDT[out_dt]],
+                                                             K._stream(out.device)))
+        assert np.array_equal(host(out[:, :k].contiguous()), ref), f"ldo={ldo}"
 
 
 # ---------------------------------------------------------------------------
@@ -431,6 +490,50 @@ def test_format_b_gemm(hip, act, m):
     check_y(y, y_ref, TDT[act])
 
 
+@pytest.mark.parametrize("act,bias_dt,ldo_pad", [
+    ("float16", "float16", 0),    # the library GEMM, bias in its epilogue
+    ("float16", "float32", 0),
+    ("bfloat16", "bfloat16", 0),
+    ("bfloat16", "float32", 0),
+    ("float16", "float16", 3),    # row stride not a multiple of 8: served by the MFMA family
+])
+def test_prefill_library_path(hip, act, bias_dt, ldo_pad):
+    """M >= 1024 runs the dequantized weights on the library GEMM, with the reference's
+    operands (kernels.py:238-242): W_eff and the rotated activations in the activations'
+    dtype, fp32 accumulation, the output in that dtype.  Against the oracle with the same
+    operand rounding, with bias, one row 300 times larger than the others (on the library
+    path; the strided output runs on the MFMA family, whose in-kernel decode and outlier
+    terms are held to the fp32-operand bar of its own tests, so its rows stay unit-scale)."""
+    case(act=act, bias_dt=bias_dt, ldo_pad=ldo_pad)
+    m, n, k = 1100, 520, 2048
+    q, rng = _format_b(7 + ldo_pad, n, k, 128, ratio=0.01)
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, act, q["rowptr"], q["col"], q["val"])
+    x = rand_np(rng, (m, k), 1.0, np.float32)
+    if ldo_pad == 0:
+        x[7] *= 300.0
+    x = O.round_to(x, act)
+    b = O.round_to((rng.standard_normal(n) * 0.5).astype(np.float32), bias_dt)
+    y_ref = O.linear_ref(x, act, w_eff, act, hadamard_block=128, bias=b, bias_dtype=bias_dt, round_x_to=act)
+    ops = K.QWeightOperands(cuda(q["packed"]), cuda(q["absmax"]), None, k, codebook="nf4", group_size=64,
+                            hadamard_block=128, marlin_layout=True, outlier_idx=cuda(q["col"]),
+                            outlier_w=cuda(q["val"]), outlier_rowptr=cuda(q["rowptr"]), bias=cuda(b, TDT[bias_dt]))
+    y = torch.full((m, n + ldo_pad), float("nan"), dtype=TDT[act], device="cuda")[:, :n]
+    K._run_linear(ops, cuda(x, TDT[act]), y, "gemm")
+    check_y(y, y_ref, TDT[act])
+
+
+def test_prefill_library_path_format_a(hip):
+    """The library path on a Format A weight (groups of 32, dense outlier columns)."""
+    case(m=1024, n=384, k=1536)
+    packed, scales, z, idx, ow, w_deq = _format_a(31, 384, 1536, 16)
+    rng = np.random.default_rng(32)
+    x = O.round_to(rand_np(rng, (1024, 1536), 1.0, np.float32), "float16")
+    y_ref = O.linear_ref(x, "float16", w_deq, "float16")
+    y = K.batched_w4a16_gemm(cuda(x), cuda(packed), cuda(scales), cuda(z), outlier_idx=cuda(idx), outlier_w=cuda(ow),
+                             marlin_layout=True)
+    check_y(y, y_ref, torch.float16)
+
+
 @pytest.mark.parametrize("act", ["float16", "bfloat16"])
 @pytest.mark.parametrize("m", [2, 3, 5, 8, 13, 16])
 @pytest.mark.parametrize("n,k,had,marlin", [
@@ -639,7 +742,10 @@ def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
 ])
 def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     """cfg4 shape class: fp32 torch reference on the GPU built from the bit-exact dequant
-    and FWHT kernels (0.5% CSR outliers, bf16 activations)."""
+    and FWHT kernels (0.5% CSR outliers, bf16 activations).  Below 1024 rows the MFMA family
+    (fp16 operands, per-row scale) is held to the fp32 operands; from 1024 rows the library
+    GEMM computes on bf16 operands like the reference's kernel (kernels.py:238-242), and the
+    reference product takes W_eff and the rotated activations rounded to bf16."""
     case(m=m, k=k, n=n)
     g = torch.Generator().manual_seed(4)
     w = (torch.randn(n, k, generator=g) * 0.02).half()
@@ -655,10 +761,12 @@ def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     # the reference's operands are the oracle's on sampled rows: quantized codes, CSR and W_eff
     # (float32 and bf16) bit for bit, and the rotated activations
     w_eff = _sampled_rows_bitexact(q, w, mask.view(n, k), "float32")
-    _sampled_rows_bitexact(q, w, mask.view(n, k), "bfloat16")
+    w_bf = _sampled_rows_bitexact(q, w, mask.view(n, k), "bfloat16")
     x_rot = K.fwht_rows(x, 128, out_dtype=torch.float32)
     xr = np.array([0, m // 2, m - 1])
     assert np.array_equal(host(x_rot)[xr], O.rotate_blocks(O.to_f32(host(x)[xr], "bfloat16"), 128))
+    if m >= 1024:
+        w_eff, x_rot = w_bf.float(), x_rot.bfloat16().float()
     y_t = (x_rot @ w_eff.float().T).double().cpu().numpy()
     check_y(y, y_t, torch.bfloat16)
 

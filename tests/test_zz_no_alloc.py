@@ -88,6 +88,26 @@ def test_noalloc_format_a(hip):
         assert torch.equal(got, ref)
 
 
+def test_noalloc_prompt_rows_on_the_mfma_family(hip):
+    """From 1024 rows the full workspace query includes the library GEMM path's dequantized
+    weight (here 16 MiB, beyond the scratch); the no-allocation entry counts only the MFMA
+    family's buffers (about 1.3 MiB here), so the call runs from the scratch on that family:
+    against the workspace entry (the library path, the same fp16 operands) within 1e-2."""
+    lib = hip
+    n, k, m = 16384, 512, 1024
+    case(n=n, k=k, m=m, fmt="nf4")
+    ops = _nf4_operands(n, k, 16)
+    assert lib.spectra_w4a16_gemm_workspace(ops.ptr(), m, L.F16) > 8 << 20
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(17)).half().cuda()
+    ref = torch.empty(m, n, dtype=torch.float16, device="cuda")
+    got = torch.full((m, n), float("nan"), dtype=torch.float16, device="cuda")
+    _with_workspace(lib, ops, x, ref)
+    L.check("spectra_w4a16_linear_noalloc", _noalloc(lib, ops, x, got))
+    torch.cuda.synchronize()
+    err = (got.float() - ref.float()).abs().max().item()
+    assert err <= 1e-2, f"max-abs {err}"
+
+
 def test_noalloc_rejects_workspace_beyond_scratch(hip):
     lib = hip
     n, k, m = 1024, 4096, 2048  # the prefill GEMM needs > 8 MiB of workspace at this m
