@@ -715,10 +715,13 @@ def _decode_run(dev, kv_bits: int) -> dict:
 
 
 def _time_eager(fn, iters: int = 20) -> float:
+    """Per-call GPU time of ``fn`` at steady state: one untimed call is queued before the
+    start event, so the host's issue latency after the synchronisation is not timed."""
     for _ in range(3):
         fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
     e0.record()
     for _ in range(iters):
         fn()

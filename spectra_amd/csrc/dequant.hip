@@ -3,6 +3,8 @@
 //             engine.py:185-206), then outlier columns := round_out(outlier_w)
 //             (tests/test_kernels.py:38-39, engine.py:209-210)
 //   Format B: round_out(fp32(NF4[q]) * fp32(absmax)), then CSR positions := round_out(val)
+#include <algorithm>
+
 #include "common.h"
 
 namespace spectra {
@@ -58,7 +60,8 @@ __device__ __forceinline__ uint32_t f2bf_sel(float f) {
 }
 
 // Row dequant at HBM rate (the prefill path materialises whole weights with it).  One wave per
-// (row, segment of kDqSegChunks 32-element runs); in a pass over a block of 64 kE elements
+// (row, segment of segc 32-element runs, segc <= kDqSegChunks a whole number of passes chosen by
+// the host so that the grid holds about kDqWaves waves); in a pass over a block of 64 kE elements
 // lane l owns the kE consecutive outputs kE l .. kE l + kE - 1 (kE = 8 for 16-bit, 4 for
 // fp32 outputs), so every store instruction of the wave writes 1 KB contiguously.  In both
 // nibble orders the 16 bytes of run c hold elements 32 c .. 32 c + 31 under one scale (group
@@ -69,7 +72,9 @@ __device__ __forceinline__ uint32_t f2bf_sel(float f) {
 // segment's dense stores have completed (the wave waits on its store counter; the fence keeps
 // the compiler from moving stores across), the same wave stores the row's outliers that fall
 // in its segment over them, so they land last.
-constexpr int kDqSegChunks = 128;  // 4096 elements
+constexpr int kDqSegChunks = 224;  // at most 7168 elements per segment
+constexpr int64_t kDqWaves = 12288;  // 48 waves per CU on 256 CUs
+constexpr int kDqPre = 2;            // outlier entries preloaded per lane
 
 template <int kOut, bool kMarlin>
 struct DqShape {
@@ -88,7 +93,7 @@ __device__ __forceinline__ uint64_t load_bytes(const uint8_t* p) {
 // kOut: SPECTRA_F16, SPECTRA_BF16 or SPECTRA_F32
 template <bool kAsym, int kOut, bool kMarlin>
 __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweight_t w, void* __restrict__ out,
-                                                                   int64_t ldo, int out_dt, int nseg) {
+                                                                   int64_t ldo, int out_dt, int nseg, int segc) {
   typedef DqShape<kOut, kMarlin> S;
   __shared__ float code[16];
   if (threadIdx.x < 16) code[threadIdx.x] = nf4_code_f32((int)threadIdx.x);
@@ -98,8 +103,8 @@ __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweigh
   const int64_t row = wid / nseg;
   if (row >= w.n) return;
   const int nch = (int)(w.k >> 5);
-  const int c0 = (int)(wid - row * nseg) * kDqSegChunks;
-  const int e_end = 32 * (min(nch, c0 + kDqSegChunks) - c0);  // elements of this segment
+  const int c0 = (int)(wid - row * nseg) * segc;
+  const int e_end = 32 * (min(nch, c0 + segc) - c0);  // elements of this segment
   const int gch = kAsym ? 1 : w.group_size >> 5;              // runs per scale group
   const uint8_t* prow = w.packed + row * w.packed_stride + 16 * (int64_t)c0;
   uint64_t qb[S::kPasses];
@@ -109,6 +114,32 @@ __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweigh
     const int e0 = o & 31;
     if (o < e_end)
       qb[b] = load_bytes<S::kBytes>(prow + 16 * (o >> 5) + (kMarlin ? (e0 & 15) : (e0 >> 1)));
+  }
+  // the first kDqPre * 64 outlier entries of the row (column, value), loaded with the weights so
+  // that the tail below only filters and stores them
+  int64_t ocol[kDqPre];
+  float oval[kDqPre];
+  int64_t e_beg = 0, e_lim = 0;  // entries of the row (CSR: [rowptr[row], rowptr[row + 1]))
+  if (w.outlier_kind == SPECTRA_OUTLIERS_CSR) {
+    e_beg = w.csr_rowptr[row];
+    e_lim = w.csr_rowptr[row + 1];
+  } else if (w.outlier_kind == SPECTRA_OUTLIERS_COLUMNS) {
+    e_lim = w.num_outliers;
+  }
+#pragma unroll
+  for (int t = 0; t < kDqPre; ++t) {
+    const int64_t e = e_beg + lane + 64 * t;
+    ocol[t] = -1;
+    oval[t] = 0.0f;
+    if (e < e_lim) {
+      if (w.outlier_kind == SPECTRA_OUTLIERS_CSR) {
+        ocol[t] = w.csr_col[e];
+        oval[t] = h2f(w.csr_val[e]);
+      } else {
+        ocol[t] = w.outlier_idx[e];
+        oval[t] = load_elem(w.outlier_w, row * w.outlier_w_stride + e, w.outlier_w_dtype);
+      }
+    }
   }
 #pragma unroll
   for (int b = 0; b < S::kPasses; ++b) {
@@ -144,20 +175,19 @@ __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweigh
     }
   }
   const int64_t k0 = 32 * (int64_t)c0, k1 = k0 + e_end;
-  if (w.outlier_kind == SPECTRA_OUTLIERS_COLUMNS) {
+  if (e_lim > e_beg) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0);
-    for (int j = lane; j < w.num_outliers; j += 64) {
-      const int64_t col = w.outlier_idx[j];
+#pragma unroll
+    for (int t = 0; t < kDqPre; ++t)
+      if (ocol[t] >= k0 && ocol[t] < k1) store_elem(out, row * ldo + ocol[t], out_dt, oval[t]);
+    for (int64_t e = e_beg + 64 * kDqPre + lane; e < e_lim; e += 64) {  // rows with more entries
+      const int64_t col = w.outlier_kind == SPECTRA_OUTLIERS_CSR ? (int64_t)w.csr_col[e] : w.outlier_idx[e];
       if (col >= k0 && col < k1)
-        store_elem(out, row * ldo + col, out_dt, load_elem(w.outlier_w, row * w.outlier_w_stride + j, w.outlier_w_dtype));
-    }
-  } else if (w.outlier_kind == SPECTRA_OUTLIERS_CSR) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);
-    for (int e = w.csr_rowptr[row] + lane; e < w.csr_rowptr[row + 1]; e += 64) {
-      const int col = w.csr_col[e];
-      if (col >= k0 && col < k1) store_elem(out, row * ldo + col, out_dt, h2f(w.csr_val[e]));
+        store_elem(out, row * ldo + col, out_dt,
+                   w.outlier_kind == SPECTRA_OUTLIERS_CSR
+                       ? h2f(w.csr_val[e])
+                       : load_elem(w.outlier_w, row * w.outlier_w_stride + e, w.outlier_w_dtype));
     }
   }
 }
@@ -243,8 +273,14 @@ extern "C" int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t
     const void* kern = kerns[asym ? 1 : 0][oi][w->marlin_layout ? 1 : 0];
     spectra_qweight_t wc = *w;
     int odt = (int)out_dtype;
-    int nseg = (int)((w->k / 32 + kDqSegChunks - 1) / kDqSegChunks);
-    void* args[] = {(void*)&wc, (void*)&out, (void*)&ldo, (void*)&odt, (void*)&nseg};
+    // segments of whole passes (16 runs for 16-bit outputs, 8 for fp32): enough of them for
+    // about kDqWaves waves, none longer than kDqSegChunks runs
+    const int64_t nch = w->k / 32, unit = esz == 4 ? 8 : 16;
+    int64_t ns = std::min((nch + unit - 1) / unit, std::max<int64_t>(1, (kDqWaves + w->n - 1) / w->n));
+    int64_t sc = ((nch + ns - 1) / ns + unit - 1) / unit * unit;
+    sc = std::min<int64_t>(sc, kDqSegChunks);
+    int nseg = (int)((nch + sc - 1) / sc), segc = (int)sc;
+    void* args[] = {(void*)&wc, (void*)&out, (void*)&ldo, (void*)&odt, (void*)&nseg, (void*)&segc};
     const int64_t waves = w->n * nseg, per_block = kDqThreads / 64;
     SPECTRA_HIP_CHECK(hipLaunchKernel(kern, dim3((unsigned)((waves + per_block - 1) / per_block)), dim3(kDqThreads),
                                       args, 0, s));

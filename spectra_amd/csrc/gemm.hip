@@ -61,6 +61,9 @@ constexpr int kPrepMaxU = 16;  // K <= 256 * 8 * 16 = 32768
 
 // raw_dt >= 0 (the library-GEMM path): no scale (F = 0), the rotated row rounded to raw_dt
 // (SPECTRA_F16 or SPECTRA_BF16), the compute dtype of the reference's GEMM; marlin must be 0.
+// With no row-wide scale to find, blockIdx.y then picks a segment of kPrepThreads * 8 * kPrepU
+// elements of the row (a multiple of every Hadamard block size), so a long row spreads over
+// several workgroups; the scaled mode runs with gridDim.y = 1 (the whole row).
 template <int kPrepU>
 __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __restrict__ a, int64_t lda, int dt,
                                                                   int k, int log_had, float div, int marlin, int vec,
@@ -70,14 +73,15 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
   __shared__ float wmax[kPrepThreads / 64];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
-  const int n8 = k >> 3;
+  const int64_t seg0 = (int64_t)blockIdx.y * (kPrepThreads * 8 * kPrepU);  // first element
+  const int n8 = (int)min((int64_t)k - seg0, (int64_t)kPrepThreads * 8 * kPrepU) >> 3;
   float v[kPrepU][8];
 #pragma unroll
   for (int u = 0; u < kPrepU; ++u) {
     const int c = tid + u * kPrepThreads;
     if (c < n8) {
       if (vec) {
-        const uint4 q = ((const uint4*)((const uint16_t*)a + row * lda))[c];
+        const uint4 q = ((const uint4*)((const uint16_t*)a + row * lda + seg0))[c];
         const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -86,7 +90,7 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
         }
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[u][e] = load_elem(a, row * lda + 8 * c + e, dt);
+        for (int e = 0; e < 8; ++e) v[u][e] = load_elem(a, row * lda + seg0 + 8 * c + e, dt);
       }
     } else {
 #pragma unroll
@@ -183,7 +187,7 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
         uint32_t d[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) d[i] = (uint32_t)run[j0 + i] | ((uint32_t)run[j0 + i + 16] << 16);
-        *(uint4*)(a16 + row * k + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
+        *(uint4*)(a16 + row * k + seg0 + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
       }
     }
   } else {  // byte j = (k 2j, k 2j + 1): pair order is the natural order
@@ -197,7 +201,7 @@ __global__ void __launch_bounds__(kPrepThreads) gemm_prep_kernel(const void* __r
           d[e] = raw_dt >= 0 ? (uint32_t)from_f32_16(v[u][2 * e] * f, raw_dt) |
                                    ((uint32_t)from_f32_16(v[u][2 * e + 1] * f, raw_dt) << 16)
                              : (uint32_t)f2h(v[u][2 * e] * f) | ((uint32_t)f2h(v[u][2 * e + 1] * f) << 16);
-        *(uint4*)(a16 + row * k + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
+        *(uint4*)(a16 + row * k + seg0 + 8 * c) = make_uint4(d[0], d[1], d[2], d[3]);
       }
     }
   }
@@ -211,19 +215,17 @@ int gemm_prep_rotate(const void* a, int64_t lda, int64_t m, int dt, int k, int h
   int log_had = 0;
   while (had > 1 && (1 << log_had) < had) ++log_had;
   const float div = had > 1 ? (float)std::sqrt((double)had) : 1.0f;
-  const int64_t n8 = k / 8;
-  const int pu = n8 <= 256 ? 1 : n8 <= 512 ? 2 : n8 <= 1024 ? 4 : n8 <= 2048 ? 8 : 16;
-  const void* prep = pu == 1 ? (const void*)gemm_prep_kernel<1> : pu == 2 ? (const void*)gemm_prep_kernel<2>
-                   : pu == 4 ? (const void*)gemm_prep_kernel<4> : pu == 8 ? (const void*)gemm_prep_kernel<8>
-                             : (const void*)gemm_prep_kernel<16>;
+  // segments of kPrepThreads * 8 * 2 = 4096 elements (two chunks of 8 per thread)
+  const void* prep = (const void*)gemm_prep_kernel<2>;
   int st = ensure_lds_limit(prep);
   if (st != SPECTRA_OK) return st;
   const int vec = (reinterpret_cast<uintptr_t>(a) % 16) == 0 && lda % 8 == 0;
   const int marl = 0, raw_dt = dt;
-  const size_t prep_lds = (size_t)k * (had > 512 ? 4 : 2);
+  const int seg = kPrepThreads * 8 * 2, nseg = (k + seg - 1) / seg;
+  const size_t prep_lds = (size_t)seg * (had > 512 ? 4 : 2);
   void* pargs[] = {(void*)&a, (void*)&lda, (void*)&dt, (void*)&k, (void*)&log_had, (void*)&div, (void*)&marl,
                    (void*)&vec, (void*)&a16, (void*)&fexp, (void*)&raw_dt};
-  SPECTRA_HIP_CHECK(hipLaunchKernel(prep, dim3((unsigned)m), dim3(kPrepThreads), pargs, prep_lds, s));
+  SPECTRA_HIP_CHECK(hipLaunchKernel(prep, dim3((unsigned)m, (unsigned)nseg), dim3(kPrepThreads), pargs, prep_lds, s));
   SPECTRA_HIP_CHECK(hipGetLastError());
   return SPECTRA_OK;
 }

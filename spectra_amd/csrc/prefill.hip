@@ -6,7 +6,9 @@
 // (fp16 or bf16, the activations' dtype: kernels.py:238-242, 347-348):
 //  * W_eff dequantized once per call into the compute dtype (the bit-exact dequant of
 //    spectra_w4_dequant, outliers included);
-//  * the activations rotated in fp32 and rounded to the compute dtype, unscaled;
+//  * the activations rotated in fp32 and rounded to the compute dtype, unscaled (without a
+//    rotation the GEMM reads them where they are, when 16-byte aligned with a row stride
+//    that is a multiple of 8);
 //  * one plain GEMM of hipBLASLt over the two (fp32 accumulation, host alpha 1 and beta 0),
 //    D in the compute dtype written straight to `out`, the bias added in its epilogue.
 // Per shape the heuristic's candidate algorithms are timed once (on an eager call; under
@@ -31,7 +33,7 @@ int gemm_prep_rotate(const void* a, int64_t lda, int64_t m, int dt, int k, int h
 
 constexpr int64_t kPrefillMinM = 1024;
 constexpr size_t kPrefillLtWorkspace = size_t(32) << 20;
-constexpr int kPrefillCandidates = 8;
+constexpr int kPrefillCandidates = 32;
 
 namespace {
 
@@ -43,8 +45,8 @@ struct LtPlan {
   bool timed = false;
 };
 
-// (device, m, n, k, ldo, compute dtype, bias dtype or -1)
-typedef std::tuple<int, int64_t, int64_t, int64_t, int64_t, int, int> PlanKey;
+// (device, m, n, k, ldo, compute dtype, bias dtype or -1, activation row stride)
+typedef std::tuple<int, int64_t, int64_t, int64_t, int64_t, int, int, int64_t> PlanKey;
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
@@ -63,8 +65,8 @@ hipDataType lt_type(int dt) { return dt == SPECTRA_BF16 ? HIP_R_16BF : dt == SPE
 
 // D (N x M column-major = out [m][ldo] row-major) = op(W) op(A) (+ bias per row of D, i.e.
 // per output column), W: K x N column-major (the [N][K] rows of W_eff), op T; A: K x M
-// column-major (the [M][K] rotated rows), op N.  Only candidates the heuristic marks valid
-// and that fit the workspace are kept.
+// column-major (the [M][K] rotated rows, row stride lda), op N.  Only candidates the
+// heuristic marks valid and that fit the workspace are kept.
 LtPlan* plan_for(hipblasLtHandle_t h, const PlanKey& key) {
   auto it = g_plans.find(key);
   if (it != g_plans.end()) return it->second.ncand > 0 ? &it->second : nullptr;
@@ -72,6 +74,7 @@ LtPlan* plan_for(hipblasLtHandle_t h, const PlanKey& key) {
   const int64_t m = std::get<1>(key), n = std::get<2>(key), k = std::get<3>(key), ldo = std::get<4>(key);
   const hipDataType dt = lt_type(std::get<5>(key));
   const int bias_dt = std::get<6>(key);
+  const int64_t lda = std::get<7>(key);
   bool ok = hipblasLtMatmulDescCreate(&pl.md, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS;
   const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
   ok = ok && hipblasLtMatmulDescSetAttribute(pl.md, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)) == HIPBLAS_STATUS_SUCCESS;
@@ -84,7 +87,7 @@ LtPlan* plan_for(hipblasLtHandle_t h, const PlanKey& key) {
              HIPBLAS_STATUS_SUCCESS;
   }
   ok = ok && hipblasLtMatrixLayoutCreate(&pl.la, dt, (uint64_t)k, (uint64_t)n, k) == HIPBLAS_STATUS_SUCCESS;
-  ok = ok && hipblasLtMatrixLayoutCreate(&pl.lb, dt, (uint64_t)k, (uint64_t)m, k) == HIPBLAS_STATUS_SUCCESS;
+  ok = ok && hipblasLtMatrixLayoutCreate(&pl.lb, dt, (uint64_t)k, (uint64_t)m, lda) == HIPBLAS_STATUS_SUCCESS;
   ok = ok && hipblasLtMatrixLayoutCreate(&pl.ld, dt, (uint64_t)n, (uint64_t)m, ldo) == HIPBLAS_STATUS_SUCCESS;
   hipblasLtMatmulPreference_t pref = nullptr;
   ok = ok && hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS;
@@ -149,17 +152,22 @@ int prefill_launch(const spectra_qweight_t* w, const void* a, int64_t lda, int64
   hipblasLtHandle_t h = handle_for(dev);
   if (h == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "prefill library path: no hipBLASLt handle");
   const int bias_dt = w->bias == nullptr ? -1 : w->bias_dtype;
-  const PlanKey key(dev, m, w->n, w->k, ldo, act_dtype, bias_dt);
+  // without a rotation the activations are the GEMM's operand as given
+  const bool direct_a = w->hadamard_block <= 1 && lda % 8 == 0 && (reinterpret_cast<uintptr_t>(a) % 16) == 0;
+  const PlanKey key(dev, m, w->n, w->k, ldo, act_dtype, bias_dt, direct_a ? lda : (int64_t)w->k);
   LtPlan* pl = plan_for(h, key);
   if (pl == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "prefill library path: no algorithm for the shape");
   uint8_t* ws = (uint8_t*)workspace;
   uint16_t* weff = (uint16_t*)(ws + L.weff);
-  uint16_t* a16 = (uint16_t*)(ws + L.a16);
+  const uint16_t* a16 = direct_a ? (const uint16_t*)a : (const uint16_t*)(ws + L.a16);
   // (1) W_eff [N][K] in the compute dtype (outliers included), (2) the rotated activations
   int st = spectra_w4_dequant(w, weff, w->k, act_dtype, s);
   if (st != SPECTRA_OK) return st;
-  st = gemm_prep_rotate(a, lda, m, act_dtype, (int)w->k, w->hadamard_block, a16, (int32_t*)(ws + L.fexp), s);
-  if (st != SPECTRA_OK) return st;
+  if (!direct_a) {
+    st = gemm_prep_rotate(a, lda, m, act_dtype, (int)w->k, w->hadamard_block, (uint16_t*)(ws + L.a16),
+                          (int32_t*)(ws + L.fexp), s);
+    if (st != SPECTRA_OK) return st;
+  }
   // (3) the GEMM
   if (bias_dt >= 0) {
     const void* bp = w->bias;

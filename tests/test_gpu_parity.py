@@ -192,26 +192,27 @@ def lib_dequant(ops, out, ldo, out_dt):
     return L.load().spectra_w4_dequant(ops.ptr(), out.data_ptr(), ldo, K._DT[TDT[out_dt]], K._stream(out.device))
 
 
-@pytest.mark.parametrize("fmt,marlin,out_dt", [
-    ("nf4", False, "float16"), ("nf4", True, "bfloat16"), ("nf4", False, "float32"),
-    ("asym", True, "bfloat16"), ("asym", False, "float32"), ("asym", True, "float16"),
+@pytest.mark.parametrize("fmt,marlin,out_dt,n_out", [
+    ("nf4", False, "float16", 0), ("nf4", True, "bfloat16", 0), ("nf4", False, "float32", 0),
+    ("asym", True, "bfloat16", 16), ("asym", False, "float32", 150), ("asym", True, "float16", 150),
 ])
-def test_dequant_row_and_general_kernels(hip, fmt, marlin, out_dt):
+def test_dequant_row_and_general_kernels(hip, fmt, marlin, out_dt, n_out):
     """spectra_w4_dequant runs the row kernel (a 16-byte chunk of packed bytes per lane, the
     row's outliers stored over it afterwards) when rows and output are 16-byte aligned, and
     the general kernel otherwise (here an output row stride of K + 1): both bit-exact against
-    the oracle, CSR and column outliers included.  K = 5120 spans two of the row kernel's
-    4096-element segments (the second one partial), each storing its own outliers."""
-    case(fmt=fmt, marlin=marlin, out_dt=out_dt)
-    n, k = 200, 5120
+    the oracle, CSR and column outliers included.  K = 8192 spans several of the row kernel's
+    segments, each storing its own outliers; 3% CSR outliers (about 245 a row) and 150 outlier
+    columns exceed the 128 entries a lane group preloads, so the remainder loop runs too."""
+    case(fmt=fmt, marlin=marlin, out_dt=out_dt, n_out=n_out)
+    n, k = 120, 8192
     if fmt == "nf4":
-        q, _ = _format_b(11, n, k, 0, ratio=0.01, marlin=marlin)
+        q, _ = _format_b(11, n, k, 0, ratio=0.03, marlin=marlin)
         ref = O.nf4_dequant(q["packed"], q["absmax"], marlin, out_dt, q["rowptr"], q["col"], q["val"])
         ops = K.QWeightOperands(cuda(q["packed"]), cuda(q["absmax"]), None, k, codebook="nf4", group_size=64,
                                 marlin_layout=marlin, outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]),
                                 outlier_rowptr=cuda(q["rowptr"]))
     else:
-        packed, scales, z, idx, ow, _ = _format_a(12, n, k, 16)
+        packed, scales, z, idx, ow, _ = _format_a(12, n, k, n_out)
         ref = O.apply_outlier_columns(O.dequant_group32(packed, scales, z, marlin, out_dt), idx, ow, out_dt)
         ops = K.QWeightOperands(cuda(packed), cuda(scales), cuda(z), k, codebook="asym", marlin_layout=marlin,
                                 outlier_idx=cuda(idx), outlier_w=cuda(ow))
