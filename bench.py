@@ -289,6 +289,8 @@ def main():
                     help="only run plain device copies of COPY_BYTES each (PMC traffic calibration)")
     ap.add_argument("--profile-gemm", action="store_true",
                     help="only run the cfg4 prefill GEMMs a few times (for rocprofv3 counter runs)")
+    ap.add_argument("--profile-gemm-handwritten", action="store_true",
+                    help="as --profile-gemm, on the hand-written MFMA GEMM instead of the library path")
     ap.add_argument("--profile-small-batch", action="store_true",
                     help="only run cfg3's M=16 small-batch calls (down_proj, gate_up) a few times (rocprofv3 runs)")
     ap.add_argument("--decode-e2e", action="store_true",
@@ -311,8 +313,8 @@ def main():
     if args.decode_e2e:
         print(json.dumps(decode_e2e(dev)), flush=True)
         return
-    if args.profile_gemm:
-        print(json.dumps(profile_gemm(dev)), flush=True)
+    if args.profile_gemm or args.profile_gemm_handwritten:
+        print(json.dumps(profile_gemm(lib, dev, "dispatch" if args.profile_gemm else "handwritten")), flush=True)
         return
     if args.profile_small_batch:
         print(json.dumps(profile_small_batch(L.load(), dev, args.pool_gb)), flush=True)
@@ -565,16 +567,16 @@ def secondary(lib, dev, pool_gb: float) -> dict:
         out[f"cfg3_down_m{m}_GBps"] = round(gemv_bytes(q3d, m) / t / 1e9, 1)
     del q3d, pool, pool_ops
     out.update(host_overhead(lib, dev))
-    # cfg4: prefill GEMM M=2048, (K,N) = (4096,14336) and (14336,4096), bf16
+    # cfg4: prefill GEMM M=2048, (K,N) = (4096,14336) and (14336,4096), bf16: the dispatching
+    # entry (the library path from 1024 rows) and the hand-written MFMA GEMM, whole calls
     for (kk, nn) in ((4096, 14336), (14336, 4096)):
-        q4 = synth_nf4(nn, kk, seed=40 + kk)
-        a = torch.randn(2048, kk, generator=torch.Generator().manual_seed(kk)).bfloat16().to(dev)
-        t = _time_eager(lambda: K.batched_w4a16_gemm(a, q4.packed, q4.absmax, None, outlier_idx=q4.col,
-                                                     outlier_w=q4.val, marlin_layout=True, **q4.kernel_kwargs()),
-                        iters=10)
-        out[f"cfg4_gemm_k{kk}_n{nn}_us"] = round(t * 1e6, 1)
-        out[f"cfg4_gemm_k{kk}_n{nn}_TFLOPs"] = round(2 * 2048 * kk * nn / t / 1e12, 1)
-        out[f"cfg4_gemm_k{kk}_n{nn}_mfma_frac"] = round(2 * 2048 * kk * nn / t / 1e12 / PEAK_FP16_TFLOPS, 4)
+        q4, a = cfg4_operands(dev, kk, nn)
+        for family, tag in (("dispatch", ""), ("handwritten", "_handwritten")):
+            t = _time_eager(cfg4_gemm(lib, dev, q4, a, family), iters=10)
+            out[f"cfg4_gemm_k{kk}_n{nn}{tag}_us"] = round(t * 1e6, 1)
+            out[f"cfg4_gemm_k{kk}_n{nn}{tag}_TFLOPs"] = round(2 * 2048 * kk * nn / t / 1e12, 1)
+            out[f"cfg4_gemm_k{kk}_n{nn}{tag}_mfma_frac"] = round(2 * 2048 * kk * nn / t / 1e12 / PEAK_FP16_TFLOPS,
+                                                                 4)
         del q4, a
     # cfg5 linear chain: 28 x (QKV, o_proj, gate_up, down) + lm_head GEMVs, distinct weights
     shapes = [(5120, 3072), (3072, 3072), (16384, 3072), (3072, 8192)]
@@ -640,16 +642,45 @@ def host_overhead(lib, dev, n: int = 3000) -> dict:
     return out
 
 
-def profile_gemm(dev, iters: int = 3) -> dict:
-    """cfg4's two prefill GEMMs (M=2048, bf16), ``iters`` launches each after a warm-up."""
+# the library path's own hipBLASLt workspace (spectra_amd/csrc/prefill.hip)
+PREFILL_LT_WORKSPACE = 32 << 20
+
+
+def cfg4_gemm(lib, dev, q4: C.NF4Weight, a: torch.Tensor, family: str):
+    """One cfg4 GEMM through the C ABI on preallocated buffers (bf16 activations and output).
+    family "dispatch": the workspace spectra_w4a16_gemm_workspace() asks for, so M >= 1024 runs
+    the library path; "handwritten": the same buffer declared PREFILL_LT_WORKSPACE + 1 bytes
+    short, which the library path does not fit, so the entry runs the hand-written MFMA GEMM
+    (it holds that GEMM's own buffers)."""
+    ops = operands(q4)
+    m, n = a.shape[0], q4.n
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    need = int(lib.spectra_w4a16_gemm_workspace(ctypes.byref(ops.desc), m, L.BF16))
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_bytes = need if family == "dispatch" else need - PREFILL_LT_WORKSPACE - 1
+    args = (ctypes.byref(ops.desc), a.data_ptr(), a.stride(0), m, L.BF16, out.data_ptr(), out.stride(0),
+            ws.data_ptr(), ws_bytes)
+
+    def call():
+        L.check("spectra_w4a16_gemm", lib.spectra_w4a16_gemm(*args, torch.cuda.current_stream().cuda_stream))
+    call.keep = (ops, out, ws)
+    return call
+
+
+def cfg4_operands(dev, kk: int, nn: int):
+    q4 = synth_nf4(nn, kk, seed=40 + kk)
+    a = torch.randn(2048, kk, generator=torch.Generator().manual_seed(kk)).bfloat16().to(dev)
+    return q4, a
+
+
+def profile_gemm(lib, dev, family: str = "dispatch", iters: int = 3) -> dict:
+    """cfg4's two prefill GEMMs (M=2048, bf16), ``iters`` launches each after a warm-up, on the
+    dispatching entry's path or on the hand-written GEMM (see cfg4_gemm)."""
     out = {}
     for kk, nn in ((4096, 14336), (14336, 4096)):
-        q4 = synth_nf4(nn, kk, seed=40 + kk)
-        a = torch.randn(2048, kk, generator=torch.Generator().manual_seed(kk)).bfloat16().to(dev)
-        fn = lambda: K.batched_w4a16_gemm(a, q4.packed, q4.absmax, None, outlier_idx=q4.col, outlier_w=q4.val,
-                                          marlin_layout=True, **q4.kernel_kwargs())
-        t = _time_eager(fn, iters)
-        out[f"cfg4_gemm_k{kk}_n{nn}_us"] = round(t * 1e6, 1)
+        q4, a = cfg4_operands(dev, kk, nn)
+        t = _time_eager(cfg4_gemm(lib, dev, q4, a, family), iters)
+        out[f"cfg4_gemm_k{kk}_n{nn}{'' if family == 'dispatch' else '_handwritten'}_us"] = round(t * 1e6, 1)
         del q4, a
     return out
 
