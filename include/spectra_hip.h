@@ -148,10 +148,10 @@ int spectra_w4a16_gemv_fused(const spectra_qweight_t* w, const void* x, int64_t 
  *   out = FWHT_hb(a) . W_eff^T + bias,   fp32 accumulation.
  * a: act_dtype [m, K] row stride lda; out: act_dtype [m, N] row stride ldo.
  * 2 <= m <= 16: small-batch stream; otherwise the hand-written GEMM (fp16 operands); from
- * m >= 1024, when the workspace holds it, W_eff dequantized into the workspace in act_dtype
+ * m >= 512, when the workspace holds it, W_eff dequantized into the workspace in act_dtype
  * and one hipBLASLt GEMM on it (the reference kernel's operand rounding).
  * workspace: device scratch of spectra_w4a16_gemm_workspace() bytes, which serves every
- * family (from m >= 1024 it includes N*K*2 + m*K*2 bytes + 32 MiB for the library path); a
+ * family (from m >= 512 it includes N*K*2 + m*K*2 bytes + 32 MiB for the library path); a
  * smaller one that holds the hand-written GEMM's buffers runs that GEMM.  May be NULL when
  * the size is 0.  Replaces kernels.py:333-389.
  */

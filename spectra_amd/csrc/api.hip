@@ -154,7 +154,7 @@ extern "C" int spectra_w4a16_linear_noalloc(const spectra_qweight_t* w, const vo
   int st = spectra::validate_qweight(w);
   if (st != SPECTRA_OK) return st;
   SPECTRA_REQUIRE(m >= 1, "m must be >= 1");
-  // the MFMA families' buffers (at m >= 1024 the library path, whose workspace holds the
+  // the MFMA families' buffers (at m >= 512 the library path, whose workspace holds the
   // whole dequantized weight, is not taken from the scratch)
   const size_t need = m >= 2 ? spectra::gemm_workspace_min(w, m) : 0;
   if (need > (size_t)SPECTRA_NOALLOC_SCRATCH_BYTES)

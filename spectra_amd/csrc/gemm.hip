@@ -718,7 +718,8 @@ static int64_t outlier_entries(const spectra_qweight_t* w) {
   return 0;
 }
 
-// prefill.hip: the library GEMM path (m >= 1024)
+// prefill.hip: the library GEMM path (m >= 512)
+constexpr int64_t kLibraryMinM = 512;
 size_t prefill_workspace(const spectra_qweight_t* w, int64_t m, int act_dtype);
 int prefill_launch(const spectra_qweight_t* w, const void* a, int64_t lda, int64_t m, int act_dtype, void* out,
                    int64_t ldo, void* workspace, size_t workspace_bytes, hipStream_t s);
@@ -734,7 +735,7 @@ using namespace spectra;
 
 namespace spectra {
 // the MFMA families' own buffers: every call of the GEMM entry runs with this much (the
-// library path of m >= 1024 needs more and runs only when the workspace holds it)
+// library path of m >= kLibraryMinM needs more and runs only when the workspace holds it)
 size_t gemm_workspace_min(const spectra_qweight_t* w, int64_t m) {
   if (w == nullptr || m <= 0) return 0;
   const GemmPlan g = plan_gemm(m, w->n, w->k);
@@ -781,7 +782,7 @@ extern "C" int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int
     const int sst = skinny_launch(w, a, lda, m, act_dtype, out, ldo, workspace, workspace_bytes, s);
     if (sst != SPECTRA_ERR_UNSUPPORTED) return sst;
   }
-  if (m >= 1024) {  // prompt sizes: dequantized weights on the matrix-core library GEMM
+  if (m >= kLibraryMinM) {  // prompt sizes: dequantized weights on the matrix-core library GEMM
     const int pst = prefill_launch(w, a, lda, m, act_dtype, out, ldo, workspace, workspace_bytes, s);
     if (pst != SPECTRA_ERR_UNSUPPORTED) return pst;
   }

@@ -31,7 +31,7 @@ namespace spectra {
 int gemm_prep_rotate(const void* a, int64_t lda, int64_t m, int dt, int k, int had, uint16_t* a16, int32_t* fexp,
                      hipStream_t s);
 
-constexpr int64_t kPrefillMinM = 1024;
+constexpr int64_t kPrefillMinM = 512;
 constexpr size_t kPrefillLtWorkspace = size_t(32) << 20;
 constexpr int kPrefillCandidates = 32;
 

@@ -33,6 +33,10 @@ __all__ = ["fused_w4a16_gemv_hdsq", "batched_w4a16_gemm", "w4a16_linear", "w4_de
            "kv4_dequantize", "attend_decode_q4", "validate_outliers"]
 
 GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA GEMM
+# rows from which the GEMM entry runs the prefill library path (W_eff dequantized in the
+# activations' dtype, one hipBLASLt GEMM) when the workspace holds it: kPrefillMinM in
+# csrc/prefill.hip
+PREFILL_LIBRARY_MIN_M = 512
 
 _DT = {torch.float16: L.F16, torch.bfloat16: L.BF16, torch.float32: L.F32}
 _TORCH_DT = {v: k for k, v in _DT.items()}

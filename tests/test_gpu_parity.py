@@ -499,7 +499,7 @@ def test_format_b_gemm(hip, act, m):
     ("float16", "float16", 3),    # row stride not a multiple of 8: served by the MFMA family
 ])
 def test_prefill_library_path(hip, act, bias_dt, ldo_pad):
-    """M >= 1024 runs the dequantized weights on the library GEMM, with the reference's
+    """From PREFILL_LIBRARY_MIN_M rows the dequantized weights run on the library GEMM, with the reference's
     operands (kernels.py:238-242): W_eff and the rotated activations in the activations'
     dtype, fp32 accumulation, the output in that dtype.  Against the oracle with the same
     operand rounding, with bias, one row 300 times larger than the others (on the library
@@ -736,17 +736,19 @@ def test_baseline_shapes(hip, name, n, k, had, ratio, ms):
 
 
 @pytest.mark.parametrize("m,k,n", [
-    (512, 4096, 14336),   # 256-wide tiles, K split in two
-    (2048, 4096, 14336),  # cfg4's first GEMM at full size: 448 tiles of 256 x 256, no K split
-    (2048, 14336, 4096),  # cfg4's second GEMM at full size: 256-wide tiles, K split in two
-    (512, 8192, 3072),    # 128-wide tiles, K split in four
+    (448, 4096, 14336),   # hand-written GEMM: 256-wide tiles, K split in two
+    (2048, 4096, 14336),  # cfg4's first GEMM at full size (library path)
+    (2048, 14336, 4096),  # cfg4's second GEMM at full size (library path)
+    (384, 8192, 3072),    # hand-written GEMM: 128-wide tiles, K split in five
+    (512, 8192, 3072),    # the library path's first row count
 ])
 def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     """cfg4 shape class: fp32 torch reference on the GPU built from the bit-exact dequant
-    and FWHT kernels (0.5% CSR outliers, bf16 activations).  Below 1024 rows the MFMA family
-    (fp16 operands, per-row scale) is held to the fp32 operands; from 1024 rows the library
-    GEMM computes on bf16 operands like the reference's kernel (kernels.py:238-242), and the
-    reference product takes W_eff and the rotated activations rounded to bf16."""
+    and FWHT kernels (0.5% CSR outliers, bf16 activations).  Below PREFILL_LIBRARY_MIN_M rows the
+    hand-written MFMA GEMM (fp16 operands, per-row scale) is held to the fp32 operands; from
+    there the library GEMM computes on bf16 operands like the reference's kernel
+    (kernels.py:238-242), and the reference product takes W_eff and the rotated activations
+    rounded to bf16."""
     case(m=m, k=k, n=n)
     g = torch.Generator().manual_seed(4)
     w = (torch.randn(n, k, generator=g) * 0.02).half()
@@ -766,7 +768,7 @@ def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     x_rot = K.fwht_rows(x, 128, out_dtype=torch.float32)
     xr = np.array([0, m // 2, m - 1])
     assert np.array_equal(host(x_rot)[xr], O.rotate_blocks(O.to_f32(host(x)[xr], "bfloat16"), 128))
-    if m >= 1024:
+    if m >= K.PREFILL_LIBRARY_MIN_M:
         w_eff, x_rot = w_bf.float(), x_rot.bfloat16().float()
     y_t = (x_rot @ w_eff.float().T).double().cpu().numpy()
     check_y(y, y_t, torch.bfloat16)

@@ -89,7 +89,7 @@ def test_noalloc_format_a(hip):
 
 
 def test_noalloc_prompt_rows_on_the_mfma_family(hip):
-    """From 1024 rows the full workspace query includes the library GEMM path's dequantized
+    """From 512 rows the full workspace query includes the library GEMM path's dequantized
     weight (here 16 MiB, beyond the scratch); the no-allocation entry counts only the MFMA
     family's buffers (about 1.3 MiB here), so the call runs from the scratch on that family:
     against the workspace entry (the library path, the same fp16 operands) within 1e-2."""
