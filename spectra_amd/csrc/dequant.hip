@@ -4,6 +4,7 @@
 //             (tests/test_kernels.py:38-39, engine.py:209-210)
 //   Format B: round_out(fp32(NF4[q]) * fp32(absmax)), then CSR positions := round_out(val)
 #include <algorithm>
+#include <cmath>
 
 #include "common.h"
 
@@ -90,12 +91,22 @@ __device__ __forceinline__ uint64_t load_bytes(const uint8_t* p) {
   return *(const uint16_t*)p;
 }
 
-// kOut: SPECTRA_F16, SPECTRA_BF16 or SPECTRA_F32
-template <bool kAsym, int kOut, bool kMarlin>
+// kOut: SPECTRA_F16, SPECTRA_BF16 or SPECTRA_F32.
+// kRot (16-bit outputs, K a multiple of 512, Hadamard blocks of 2 .. 512): the rows come out
+// rotated, W_eff H_b / sqrt(b) blockwise (the prefill library path's weights: with H_b
+// symmetric, x_rot . W_eff^T = x . (W_eff H_b / sqrt(b))^T).  Each pass of 512 elements then
+// goes through the wave's LDS slot: the dense values, the outliers that fall in the pass over
+// them, back into registers, then the transform (stages 1, 2, 4 in registers, 8 .. 256 across
+// the lanes of a block, as gemm_prep_kernel), the sign and 1 / sqrt(b) in one product, one
+// rounding to the output dtype.  There is no outlier tail.
+template <bool kAsym, int kOut, bool kMarlin, bool kRot>
 __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweight_t w, void* __restrict__ out,
-                                                                   int64_t ldo, int out_dt, int nseg, int segc) {
+                                                                   int64_t ldo, int out_dt, int nseg, int segc,
+                                                                   int log_had, float rot_scale) {
   typedef DqShape<kOut, kMarlin> S;
+  static_assert(!kRot || S::kE == 8, "the rotated rows are 16-bit outputs");
   __shared__ float code[16];
+  __shared__ __align__(16) float stage[kRot ? kDqThreads / 64 : 1][kRot ? 512 : 4];
   if (threadIdx.x < 16) code[threadIdx.x] = nf4_code_f32((int)threadIdx.x);
   __syncthreads();
   const int lane = threadIdx.x & 63;
@@ -157,10 +168,61 @@ __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweigh
       const uint32_t byte = (uint32_t)(qb[b] >> bit) & 0xffu;
       const uint32_t q = kMarlin ? (e0 >= 16 ? byte >> 4 : byte & 15u) : ((i & 1) ? byte >> 4 : byte & 15u);
       v[i] = kAsym ? ((float)q - z) * s : code[q] * s;
-      if (kOut == SPECTRA_F16) {
+      if (kOut == SPECTRA_F16 && !kRot) {
         // the product is rounded to fp32 first, then to fp16 (the compiler would otherwise fold
         // the product and the conversion into one v_fma_mixlo_f16)
         asm volatile("" : "+v"(v[i]));
+      }
+    }
+    if constexpr (kRot) {
+      // the pass's dense values and its outliers through the wave's LDS slot (one wave:
+      // in-order LDS, the wait and the memory clobber keep every read after every write)
+      float* st = stage[threadIdx.x >> 6];
+      const int64_t pk0 = 32 * (int64_t)c0 + 64 * S::kE * b;  // first column of the pass
+      *(float4*)&st[8 * lane] = make_float4(v[0], v[1], v[2], v[3]);
+      *(float4*)&st[8 * lane + 4] = make_float4(v[4], v[5], v[6], v[7]);
+#pragma unroll
+      for (int t = 0; t < kDqPre; ++t)
+        if (ocol[t] >= pk0 && ocol[t] < pk0 + 512) st[ocol[t] - pk0] = oval[t];
+      for (int64_t e = e_beg + 64 * kDqPre + lane; e < e_lim; e += 64) {  // rows with more entries
+        const int64_t col = w.outlier_kind == SPECTRA_OUTLIERS_CSR ? (int64_t)w.csr_col[e] : w.outlier_idx[e];
+        if (col >= pk0 && col < pk0 + 512)
+          st[col - pk0] = w.outlier_kind == SPECTRA_OUTLIERS_CSR
+                              ? h2f(w.csr_val[e])
+                              : load_elem(w.outlier_w, row * w.outlier_w_stride + e, w.outlier_w_dtype);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      float r[1][8];
+      const float4 ra = *(const float4*)&st[8 * lane], rb = *(const float4*)&st[8 * lane + 4];
+      r[0][0] = ra.x; r[0][1] = ra.y; r[0][2] = ra.z; r[0][3] = ra.w;
+      r[0][4] = rb.x; r[0][5] = rb.y; r[0][6] = rb.z; r[0][7] = rb.w;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot is rewritten by the next pass
+#pragma unroll
+      for (int lh = 0; lh < 3; ++lh) {
+        if (lh < log_had) {
+          const int h = 1 << lh;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if ((e & h) == 0) {
+              const float x0 = r[0][e], x1 = r[0][e | h];
+              r[0][e] = x0 + x1;
+              r[0][e | h] = x0 - x1;
+            }
+        }
+      }
+      float sgn = 1.0f;
+      auto side = [&](int lb) { const bool hi = (lane & lb) != 0; if (hi) sgn = -sgn; return hi ? -1.0f : 1.0f; };
+      if (log_had > 3) prep_fly<1>(r, side(1), lane);
+      if (log_had > 4) prep_fly<2>(r, side(2), lane);
+      if (log_had > 5) prep_fly<4>(r, side(4), lane);
+      if (log_had > 6) prep_fly<8>(r, side(8), lane);
+      if (log_had > 7) prep_fly<16>(r, side(16), lane);
+      if (log_had > 8) prep_fly<32>(r, side(32), lane);
+      const float f = sgn * rot_scale;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        v[i] = r[0][i] * f;
+        if (kOut == SPECTRA_F16) asm volatile("" : "+v"(v[i]));  // fp32, then fp16
       }
     }
     if (kOut == SPECTRA_F32) {
@@ -175,7 +237,7 @@ __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweigh
     }
   }
   const int64_t k0 = 32 * (int64_t)c0, k1 = k0 + e_end;
-  if (e_lim > e_beg) {
+  if (!kRot && e_lim > e_beg) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
@@ -249,6 +311,75 @@ extern "C" int spectra_w4_embedding(const spectra_qweight_t* w, const int64_t* i
   return SPECTRA_OK;
 }
 
+namespace spectra {
+
+// whether the row kernel serves the operands: 16-byte aligned rows of whole 32-element runs
+// under one scale each (rot_had > 0: the rotated rows, see kRot)
+bool dequant_rows_ok(const spectra_qweight_t* w, const void* out, int64_t ldo, int out_dtype, int rot_had) {
+  const int esz = out_dtype == SPECTRA_F32 ? 4 : 2;
+  const bool asym = w->format == SPECTRA_FMT_ASYM_G32;
+  if (!(w->k % 32 == 0 && (asym || w->group_size % 32 == 0) && (reinterpret_cast<uintptr_t>(w->packed) % 16) == 0 &&
+        w->packed_stride % 16 == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0 && (ldo * esz) % 16 == 0))
+    return false;
+  return rot_had == 0 || (esz == 2 && w->k % 512 == 0 && rot_had >= 2 && rot_had <= 512 && is_pow2(rot_had));
+}
+
+// the row kernel's launch; SPECTRA_ERR_UNSUPPORTED (nothing launched) where dequant_rows_ok fails
+static int launch_dequant_rows(const spectra_qweight_t* w, void* out, int64_t ldo, int out_dtype, int rot_had,
+                               hipStream_t s) {
+  if (!dequant_rows_ok(w, out, ldo, out_dtype, rot_had)) return SPECTRA_ERR_UNSUPPORTED;
+  const int esz = out_dtype == SPECTRA_F32 ? 4 : 2;
+  const bool asym = w->format == SPECTRA_FMT_ASYM_G32;
+  typedef const void* K;
+  // [rotated][asym][out dtype][marlin]
+  static const K kerns[2][2][3][2] = {
+      {{{(K)dequant_rows_kernel<false, SPECTRA_F16, false, false>, (K)dequant_rows_kernel<false, SPECTRA_F16, true, false>},
+        {(K)dequant_rows_kernel<false, SPECTRA_BF16, false, false>, (K)dequant_rows_kernel<false, SPECTRA_BF16, true, false>},
+        {(K)dequant_rows_kernel<false, SPECTRA_F32, false, false>, (K)dequant_rows_kernel<false, SPECTRA_F32, true, false>}},
+       {{(K)dequant_rows_kernel<true, SPECTRA_F16, false, false>, (K)dequant_rows_kernel<true, SPECTRA_F16, true, false>},
+        {(K)dequant_rows_kernel<true, SPECTRA_BF16, false, false>, (K)dequant_rows_kernel<true, SPECTRA_BF16, true, false>},
+        {(K)dequant_rows_kernel<true, SPECTRA_F32, false, false>, (K)dequant_rows_kernel<true, SPECTRA_F32, true, false>}}},
+      {{{(K)dequant_rows_kernel<false, SPECTRA_F16, false, true>, (K)dequant_rows_kernel<false, SPECTRA_F16, true, true>},
+        {(K)dequant_rows_kernel<false, SPECTRA_BF16, false, true>, (K)dequant_rows_kernel<false, SPECTRA_BF16, true, true>},
+        {nullptr, nullptr}},
+       {{(K)dequant_rows_kernel<true, SPECTRA_F16, false, true>, (K)dequant_rows_kernel<true, SPECTRA_F16, true, true>},
+        {(K)dequant_rows_kernel<true, SPECTRA_BF16, false, true>, (K)dequant_rows_kernel<true, SPECTRA_BF16, true, true>},
+        {nullptr, nullptr}}}};
+  const int oi = out_dtype == SPECTRA_F16 ? 0 : out_dtype == SPECTRA_BF16 ? 1 : 2;
+  const void* kern = kerns[rot_had > 0 ? 1 : 0][asym ? 1 : 0][oi][w->marlin_layout ? 1 : 0];
+  if (kern == nullptr) return SPECTRA_ERR_UNSUPPORTED;
+  spectra_qweight_t wc = *w;
+  int odt = out_dtype;
+  // segments of whole passes (16 runs for 16-bit outputs, 8 for fp32): enough of them for
+  // about kDqWaves waves, none longer than kDqSegChunks runs
+  const int64_t nch = w->k / 32, unit = esz == 4 ? 8 : 16;
+  int64_t ns = std::min((nch + unit - 1) / unit, std::max<int64_t>(1, (kDqWaves + w->n - 1) / w->n));
+  int64_t sc = ((nch + ns - 1) / ns + unit - 1) / unit * unit;
+  sc = std::min<int64_t>(sc, kDqSegChunks);
+  int nseg = (int)((nch + sc - 1) / sc), segc = (int)sc;
+  int log_had = 0;
+  while (rot_had > 1 && (1 << log_had) < rot_had) ++log_had;
+  const float div = rot_had > 1 ? (float)std::sqrt((double)rot_had) : 1.0f;
+  float rot_scale = 1.0f / div;  // the activation prep's 2^0 / sqrt(b)
+  void* args[] = {(void*)&wc, (void*)&out, (void*)&ldo, (void*)&odt, (void*)&nseg, (void*)&segc,
+                  (void*)&log_had, (void*)&rot_scale};
+  const int64_t waves = w->n * nseg, per_block = kDqThreads / 64;
+  SPECTRA_HIP_CHECK(hipLaunchKernel(kern, dim3((unsigned)((waves + per_block - 1) / per_block)), dim3(kDqThreads),
+                                    args, 0, s));
+  SPECTRA_HIP_CHECK(hipGetLastError());
+  return SPECTRA_OK;
+}
+
+// the prefill library path's weights: W_eff H_b / sqrt(b) rowwise in blocks of b = had, in the
+// 16-bit out_dtype, row stride K; SPECTRA_ERR_UNSUPPORTED (nothing launched) when the row
+// kernel does not serve the operands (then the activations are rotated instead)
+int w4_dequant_rotated(const spectra_qweight_t* w, void* out, int out_dtype, int had, hipStream_t s) {
+  if (out_dtype != SPECTRA_F16 && out_dtype != SPECTRA_BF16) return SPECTRA_ERR_UNSUPPORTED;
+  return launch_dequant_rows(w, out, w->k, out_dtype, had, s);
+}
+
+}  // namespace spectra
+
 extern "C" int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t ldo, int32_t out_dtype,
                                   spectra_stream_t stream) {
   int st = validate_qweight(w);
@@ -257,36 +388,8 @@ extern "C" int spectra_w4_dequant(const spectra_qweight_t* w, void* out, int64_t
   SPECTRA_REQUIRE(ldo >= w->k, "out row stride smaller than K");
   SPECTRA_REQUIRE(out_dtype >= SPECTRA_F16 && out_dtype <= SPECTRA_F32, "bad out dtype");
   const hipStream_t s = (hipStream_t)stream;
-  const int esz = out_dtype == SPECTRA_F32 ? 4 : 2;
-  const bool asym = w->format == SPECTRA_FMT_ASYM_G32;
-  if (w->k % 32 == 0 && (asym || w->group_size % 32 == 0) && (reinterpret_cast<uintptr_t>(w->packed) % 16) == 0 &&
-      w->packed_stride % 16 == 0 && (reinterpret_cast<uintptr_t>(out) % 16) == 0 && (ldo * esz) % 16 == 0) {
-    // [asym][out dtype][marlin]
-    static const void* const kerns[2][3][2] = {
-        {{(const void*)dequant_rows_kernel<false, SPECTRA_F16, false>, (const void*)dequant_rows_kernel<false, SPECTRA_F16, true>},
-         {(const void*)dequant_rows_kernel<false, SPECTRA_BF16, false>, (const void*)dequant_rows_kernel<false, SPECTRA_BF16, true>},
-         {(const void*)dequant_rows_kernel<false, SPECTRA_F32, false>, (const void*)dequant_rows_kernel<false, SPECTRA_F32, true>}},
-        {{(const void*)dequant_rows_kernel<true, SPECTRA_F16, false>, (const void*)dequant_rows_kernel<true, SPECTRA_F16, true>},
-         {(const void*)dequant_rows_kernel<true, SPECTRA_BF16, false>, (const void*)dequant_rows_kernel<true, SPECTRA_BF16, true>},
-         {(const void*)dequant_rows_kernel<true, SPECTRA_F32, false>, (const void*)dequant_rows_kernel<true, SPECTRA_F32, true>}}};
-    const int oi = out_dtype == SPECTRA_F16 ? 0 : out_dtype == SPECTRA_BF16 ? 1 : 2;
-    const void* kern = kerns[asym ? 1 : 0][oi][w->marlin_layout ? 1 : 0];
-    spectra_qweight_t wc = *w;
-    int odt = (int)out_dtype;
-    // segments of whole passes (16 runs for 16-bit outputs, 8 for fp32): enough of them for
-    // about kDqWaves waves, none longer than kDqSegChunks runs
-    const int64_t nch = w->k / 32, unit = esz == 4 ? 8 : 16;
-    int64_t ns = std::min((nch + unit - 1) / unit, std::max<int64_t>(1, (kDqWaves + w->n - 1) / w->n));
-    int64_t sc = ((nch + ns - 1) / ns + unit - 1) / unit * unit;
-    sc = std::min<int64_t>(sc, kDqSegChunks);
-    int nseg = (int)((nch + sc - 1) / sc), segc = (int)sc;
-    void* args[] = {(void*)&wc, (void*)&out, (void*)&ldo, (void*)&odt, (void*)&nseg, (void*)&segc};
-    const int64_t waves = w->n * nseg, per_block = kDqThreads / 64;
-    SPECTRA_HIP_CHECK(hipLaunchKernel(kern, dim3((unsigned)((waves + per_block - 1) / per_block)), dim3(kDqThreads),
-                                      args, 0, s));
-    SPECTRA_HIP_CHECK(hipGetLastError());
-    return SPECTRA_OK;
-  }
+  st = launch_dequant_rows(w, out, ldo, (int)out_dtype, 0, s);
+  if (st != SPECTRA_ERR_UNSUPPORTED) return st;
   const int64_t work = w->n * (w->k / 2);
   hipLaunchKernelGGL(dequant_kernel, dim3((unsigned)((work + kDqThreads - 1) / kDqThreads)), dim3(kDqThreads), 0, s,
                      *w, out, ldo, (int)out_dtype);

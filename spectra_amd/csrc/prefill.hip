@@ -6,9 +6,11 @@
 // (fp16 or bf16, the activations' dtype: kernels.py:238-242, 347-348):
 //  * W_eff dequantized once per call into the compute dtype (the bit-exact dequant of
 //    spectra_w4_dequant, outliers included);
-//  * the activations rotated in fp32 and rounded to the compute dtype, unscaled (without a
-//    rotation the GEMM reads them where they are, when 16-byte aligned with a row stride
-//    that is a multiple of 8);
+//  * the Hadamard rotation on the weights: with H_b symmetric, FWHT_b(a) / sqrt(b) . W_eff^T =
+//    a . (W_eff H_b / sqrt(b))^T, so the dequant writes the rotated rows (blocks up to 512,
+//    K a multiple of 512) and the GEMM reads the activations where they are (16-byte aligned,
+//    row stride a multiple of 8); otherwise the activations are rotated in fp32 and rounded
+//    to the compute dtype into the workspace (without a rotation they are read as given);
 //  * one plain GEMM of hipBLASLt over the two (fp32 accumulation, host alpha 1 and beta 0),
 //    D in the compute dtype written straight to `out`, the bias added in its epilogue.
 // Per shape the heuristic's candidate algorithms are timed once (on an eager call; under
@@ -30,6 +32,9 @@ namespace spectra {
 // gemm.hip: the rotation into the compute dtype (natural order, unscaled)
 int gemm_prep_rotate(const void* a, int64_t lda, int64_t m, int dt, int k, int had, uint16_t* a16, int32_t* fexp,
                      hipStream_t s);
+// dequant.hip: the row dequant's operand check and its rotated rows (W_eff H_b / sqrt(b))
+bool dequant_rows_ok(const spectra_qweight_t* w, const void* out, int64_t ldo, int out_dtype, int rot_had);
+int w4_dequant_rotated(const spectra_qweight_t* w, void* out, int out_dtype, int had, hipStream_t s);
 
 constexpr int64_t kPrefillMinM = 512;
 constexpr size_t kPrefillLtWorkspace = size_t(32) << 20;
@@ -152,16 +157,26 @@ int prefill_launch(const spectra_qweight_t* w, const void* a, int64_t lda, int64
   hipblasLtHandle_t h = handle_for(dev);
   if (h == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "prefill library path: no hipBLASLt handle");
   const int bias_dt = w->bias == nullptr ? -1 : w->bias_dtype;
-  // without a rotation the activations are the GEMM's operand as given
-  const bool direct_a = w->hadamard_block <= 1 && lda % 8 == 0 && (reinterpret_cast<uintptr_t>(a) % 16) == 0;
+  // the activations are the GEMM's operand as given when there is no rotation, or when the
+  // rotation goes onto the weights (the row dequant's rotated rows); otherwise the prep rotates
+  // them into the workspace.  The weights take it when the activations are the larger side
+  // (4 M >= N): the prep moves 4 M K bytes, the rotated rows add their transform's work to the
+  // N K weights (measured at cfg4: K = 14336, N = 4096 saves 17 us; K = 4096, N = 14336 runs
+  // 4-7 us slower than the prep)
+  const bool x_ok = lda % 8 == 0 && (reinterpret_cast<uintptr_t>(a) % 16) == 0;
+  const int had = w->hadamard_block;
+  const bool rot_w = x_ok && had > 1 && 4 * m >= w->n &&
+                     dequant_rows_ok(w, (const uint8_t*)workspace + L.weff, w->k, act_dtype, had);
+  const bool direct_a = x_ok && (had <= 1 || rot_w);
   const PlanKey key(dev, m, w->n, w->k, ldo, act_dtype, bias_dt, direct_a ? lda : (int64_t)w->k);
   LtPlan* pl = plan_for(h, key);
   if (pl == nullptr) return fail(SPECTRA_ERR_UNSUPPORTED, "prefill library path: no algorithm for the shape");
   uint8_t* ws = (uint8_t*)workspace;
   uint16_t* weff = (uint16_t*)(ws + L.weff);
   const uint16_t* a16 = direct_a ? (const uint16_t*)a : (const uint16_t*)(ws + L.a16);
-  // (1) W_eff [N][K] in the compute dtype (outliers included), (2) the rotated activations
-  int st = spectra_w4_dequant(w, weff, w->k, act_dtype, s);
+  // (1) W_eff [N][K] in the compute dtype (outliers included; rotated when rot_w), (2) the
+  // rotated activations
+  int st = rot_w ? w4_dequant_rotated(w, weff, act_dtype, had, s) : spectra_w4_dequant(w, weff, w->k, act_dtype, s);
   if (st != SPECTRA_OK) return st;
   if (!direct_a) {
     st = gemm_prep_rotate(a, lda, m, act_dtype, (int)w->k, w->hadamard_block, (uint16_t*)(ws + L.a16),

@@ -38,6 +38,16 @@ GEMV_MAX_M = 4  # rows served by the GEMV family; larger batches go to the MFMA 
 # csrc/prefill.hip
 PREFILL_LIBRARY_MIN_M = 512
 
+
+def prefill_rotates_weights(m: int, n: int, k: int, hadamard_block: int) -> bool:
+    """Whether the prefill library path puts the Hadamard rotation on the weights (W_eff H / sqrt(b)
+    from the row dequant, the activations read as given) rather than on the activations: its rule
+    in csrc/prefill.hip for 16-byte aligned activations with a row stride a multiple of 8 (as this
+    module passes them): m >= PREFILL_LIBRARY_MIN_M, 4 m >= n, K a multiple of 512, blocks of
+    2 .. 512."""
+    return (m >= PREFILL_LIBRARY_MIN_M and 4 * m >= n and k % 512 == 0 and 2 <= hadamard_block <= 512
+            and hadamard_block & (hadamard_block - 1) == 0)
+
 _DT = {torch.float16: L.F16, torch.bfloat16: L.BF16, torch.float32: L.F32}
 _TORCH_DT = {v: k for k, v in _DT.items()}
 

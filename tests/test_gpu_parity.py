@@ -491,30 +491,39 @@ def test_format_b_gemm(hip, act, m):
     check_y(y, y_ref, TDT[act])
 
 
-@pytest.mark.parametrize("act,bias_dt,ldo_pad", [
-    ("float16", "float16", 0),    # the library GEMM, bias in its epilogue
-    ("float16", "float32", 0),
-    ("bfloat16", "bfloat16", 0),
-    ("bfloat16", "float32", 0),
-    ("float16", "float16", 3),    # row stride not a multiple of 8: served by the MFMA family
+@pytest.mark.parametrize("act,bias_dt,ldo_pad,ratio", [
+    ("float16", "float16", 0, 0.01),    # the library GEMM, bias in its epilogue
+    ("float16", "float32", 0, 0.01),
+    ("bfloat16", "bfloat16", 0, 0.01),
+    ("bfloat16", "float32", 0, 0.01),
+    ("float16", "float16", 0, 0.08),    # ~160 outliers a row: more than a lane group preloads
+    ("float16", "float16", 3, 0.01),    # row stride not a multiple of 8: served by the MFMA family
 ])
-def test_prefill_library_path(hip, act, bias_dt, ldo_pad):
-    """From PREFILL_LIBRARY_MIN_M rows the dequantized weights run on the library GEMM, with the reference's
-    operands (kernels.py:238-242): W_eff and the rotated activations in the activations'
-    dtype, fp32 accumulation, the output in that dtype.  Against the oracle with the same
-    operand rounding, with bias, one row 300 times larger than the others (on the library
-    path; the strided output runs on the MFMA family, whose in-kernel decode and outlier
-    terms are held to the fp32-operand bar of its own tests, so its rows stay unit-scale)."""
-    case(act=act, bias_dt=bias_dt, ldo_pad=ldo_pad)
+def test_prefill_library_path(hip, act, bias_dt, ldo_pad, ratio):
+    """From PREFILL_LIBRARY_MIN_M rows the dequantized weights run on the library GEMM in the
+    activations' dtype (the reference kernel's operand type, kernels.py:238-242), fp32
+    accumulation, the output in that dtype.  The Hadamard rotation goes onto the weights there
+    (x_rot . W_eff^T = x . (W_eff H / sqrt(b))^T, H symmetric): the oracle's reference takes
+    the activations as given and the oracle's fp32 W_eff rotated blockwise and rounded to the
+    activations' dtype.  With bias, one row 300 times larger than the others (on the library
+    path; the strided output runs on the MFMA family, against rotated activations rounded
+    to its fp16 operands, its rows unit-scale)."""
+    case(act=act, bias_dt=bias_dt, ldo_pad=ldo_pad, ratio=ratio)
     m, n, k = 1100, 520, 2048
-    q, rng = _format_b(7 + ldo_pad, n, k, 128, ratio=0.01)
+    q, rng = _format_b(7 + ldo_pad, n, k, 128, ratio=ratio)
     w_eff = O.nf4_dequant(q["packed"], q["absmax"], True, act, q["rowptr"], q["col"], q["val"])
     x = rand_np(rng, (m, k), 1.0, np.float32)
     if ldo_pad == 0:
         x[7] *= 300.0
     x = O.round_to(x, act)
     b = O.round_to((rng.standard_normal(n) * 0.5).astype(np.float32), bias_dt)
-    y_ref = O.linear_ref(x, act, w_eff, act, hadamard_block=128, bias=b, bias_dtype=bias_dt, round_x_to=act)
+    if ldo_pad == 0:  # the library path, here with the rotation on the weights
+        assert K.prefill_rotates_weights(m, n, k, 128)
+        w_rot = O.round_to(O.rotate_blocks(O.nf4_dequant(q["packed"], q["absmax"], True, "float32", q["rowptr"],
+                                                         q["col"], q["val"]), 128), act)
+        y_ref = O.linear_ref(x, act, w_rot, act, bias=b, bias_dtype=bias_dt)
+    else:
+        y_ref = O.linear_ref(x, act, w_eff, act, hadamard_block=128, bias=b, bias_dtype=bias_dt, round_x_to=act)
     ops = K.QWeightOperands(cuda(q["packed"]), cuda(q["absmax"]), None, k, codebook="nf4", group_size=64,
                             hadamard_block=128, marlin_layout=True, outlier_idx=cuda(q["col"]),
                             outlier_w=cuda(q["val"]), outlier_rowptr=cuda(q["rowptr"]), bias=cuda(b, TDT[bias_dt]))
@@ -747,8 +756,10 @@ def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     and FWHT kernels (0.5% CSR outliers, bf16 activations).  Below PREFILL_LIBRARY_MIN_M rows the
     hand-written MFMA GEMM (fp16 operands, per-row scale) is held to the fp32 operands; from
     there the library GEMM computes on bf16 operands like the reference's kernel
-    (kernels.py:238-242), and the reference product takes W_eff and the rotated activations
-    rounded to bf16."""
+    (kernels.py:238-242).  With the rotation on the weights (prefill_rotates_weights) the
+    reference product takes the activations as given and the fp32 W_eff rotated blockwise (the
+    HIP FWHT, pinned to the oracle) and rounded to bf16; otherwise W_eff and the rotated
+    activations rounded to bf16."""
     case(m=m, k=k, n=n)
     g = torch.Generator().manual_seed(4)
     w = (torch.randn(n, k, generator=g) * 0.02).half()
@@ -768,7 +779,10 @@ def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     x_rot = K.fwht_rows(x, 128, out_dtype=torch.float32)
     xr = np.array([0, m // 2, m - 1])
     assert np.array_equal(host(x_rot)[xr], O.rotate_blocks(O.to_f32(host(x)[xr], "bfloat16"), 128))
-    if m >= K.PREFILL_LIBRARY_MIN_M:
+    if K.prefill_rotates_weights(m, n, k, 128):
+        w_eff = K.fwht_rows(w_eff.float(), 128, out_dtype=torch.float32).bfloat16()
+        x_rot = x.float()
+    elif m >= K.PREFILL_LIBRARY_MIN_M:
         w_eff, x_rot = w_bf.float(), x_rot.bfloat16().float()
     y_t = (x_rot @ w_eff.float().T).double().cpu().numpy()
     check_y(y, y_t, torch.bfloat16)
