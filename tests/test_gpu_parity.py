@@ -863,6 +863,42 @@ def test_determinism_and_graph_replay(hip):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("k,n", [(4096, 14336), (14336, 4096)])
+def test_prefill_library_path_graph_replay(hip, k, n):
+    """cfg4's two shapes through the module at M=2048, bf16: the prefill library path (a
+    Stream-K algorithm on the first shape, the rotated weights on the second).  Two eager calls
+    (the first times the candidates) agree bit for bit; then the call is captured in a graph
+    and replayed three times with eager work between the replays, each replay equal to the
+    eager output bit for bit."""
+    case(k=k, n=n)
+    g = torch.Generator().manual_seed(k)
+    w = (torch.randn(n, k, generator=g) * 0.02).half()
+    mask = torch.rand(n, k, generator=g) < 0.005
+    q = C.quantize_nf4(w.cuda(), 64, 128, mask.cuda(), True)
+    lin = SpectraFusedLinear(k, n, 64, codebook="nf4", hadamard_block=128).cuda()
+    lin.set_weights(q.packed, q.absmax, None, outlier_idx=q.col, outlier_weight=q.val, marlin_layout=True,
+                    outlier_rowptr=q.rowptr)
+    x = torch.randn(K.PREFILL_LIBRARY_MIN_M * 4, k, generator=g).bfloat16().cuda()
+    e = lin(x)
+    assert torch.equal(lin(x), e)  # bitwise deterministic
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            lin(x)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gy = lin(x)
+    for _ in range(3):
+        gy.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gy, e)
+        _ = lin(x)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 def test_functional_api_reuses_and_validates_descriptors(hip):
     """fused_w4a16_gemv_hdsq builds (and validates) a weight's descriptor once: a second call
     with the same tensors reuses it, an in-place write to an operand rebuilds and re-validates
