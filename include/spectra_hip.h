@@ -162,9 +162,10 @@ int spectra_w4a16_gemm(const spectra_qweight_t* w, const void* a, int64_t lda, i
 
 /*
  * Module dispatch (engine.py:90-124): m <= 4 -> GEMV family, else GEMM family; 2 <= m <= 4
- * rows of a shape whose GEMV plan needs more than one workgroup per CU go to the GEMM
- * entry's small-batch MFMA family instead, when it serves the operands and the workspace
- * is large enough (otherwise they stay on the GEMV family).
+ * rows of a shape that only the older multi-row GEMV kernels serve, with a plan of more
+ * than one workgroup per CU, go to the GEMM entry's small-batch MFMA family instead, when
+ * it serves the operands and the workspace is large enough (otherwise they stay on the
+ * GEMV family).
  * workspace as for spectra_w4a16_gemm (sized by spectra_w4a16_gemm_workspace).
  */
 int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, int64_t ldx, int64_t m,

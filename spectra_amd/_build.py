@@ -19,7 +19,7 @@ OBJDIR = os.path.join(PKG, "_obj")
 LIB = os.path.join(PKG, "libspectra_hip.so")
 TORCH_OPS_LIB = os.path.join(PKG, "_spectra_torch.so")
 TORCH_OPS_SOURCE = "torch_ops.cpp"
-SOURCES = ["api.hip", "quant.hip", "dequant.hip", "gemv.hip", "gemv_f16.hip", "gemv_bf16.hip", "gemv_stream_f16.hip", "gemv_stream_bf16.hip", "gemv_rows_plain.hip", "gemv_rows_pro.hip", "gemv_rows_lm.hip", "gemm.hip", "prefill.hip", "skinny.hip", "outliers.hip", "decode.hip", "measure.hip"]
+SOURCES = ["api.hip", "quant.hip", "dequant.hip", "gemv.hip", "gemv_f16.hip", "gemv_bf16.hip", "gemv_stream_f16.hip", "gemv_stream_bf16.hip", "gemv_rows_plain.hip", "gemv_rows_pro.hip", "gemv_rows_lm.hip", "gemv_rows_multi_f16.hip", "gemv_rows_multi_bf16.hip", "gemm.hip", "prefill.hip", "skinny.hip", "outliers.hip", "decode.hip", "measure.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [

@@ -172,11 +172,12 @@ extern "C" int spectra_w4a16_linear(const spectra_qweight_t* w, const void* x, i
                                     size_t workspace_bytes, spectra_stream_t stream) {
   // engine.py:94-124: single-token rows go to the GEMV family, everything else (and any
   // operand combination the GEMV family does not serve) to the GEMM family.
-  // 2..4 rows of a shape whose GEMV plan needs more than one workgroup per CU (the
-  // multi-row GEMV kernels hold more than 128 VGPRs, so a second round of workgroups runs
-  // behind the first) go to the small-batch MFMA family, which streams the weights in one
-  // round (N=16384, K=3072: 17.0 us against 21.8-23.9 us), when it serves the operands and
-  // the workspace holds its buffers.
+  // 2..4 rows: the row-owning GEMV (one workgroup per CU; K = 3072, 4096, 8192) where it
+  // plans the shape.  A shape only the older multi-row GEMV kernels serve, whose plan needs
+  // more than one workgroup per CU (they hold more than 128 VGPRs, so a second round of
+  // workgroups runs behind the first), goes to the small-batch MFMA family, which streams
+  // the weights in one round, when it serves the operands and the workspace holds its
+  // buffers.
   if (m >= 2 && m <= 4 && spectra::validate_qweight(w) == SPECTRA_OK &&
       spectra::gemv_plan_grid(w, (int)m) > spectra::device_cu_count() &&
       x != nullptr && spectra::skinny_supported(w, x, ldx, m) == SPECTRA_OK && workspace != nullptr &&

@@ -207,15 +207,17 @@ static int stream_launch(const spectra_qweight_t* w, const StreamPlan& pl, const
 }
 
 // ---------------------------------------------------------------------------
-// row-owning kernel plan (one activation row, NF4, Hadamard block 128 or none)
+// row-owning kernel plan (1 .. 4 activation rows, NF4, Hadamard block 128 or none)
 // ---------------------------------------------------------------------------
 struct RowsPlan {
-  int G, SPR, RPG, XC, W, WR, R, grid, nchunk, cpr;
+  int G, SPR, RPG, XC, W, WR, R, grid, nchunk, cpr, mr;
   bool split;
-  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res, lds_bytes;
+  uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res, xp_row, xsc_row, lds_bytes;
 };
 
-static gemv_rows_fn rows_fn(int g, int spr, int rpg, int xc, bool split, bool bf, int pro) {
+static gemv_rows_fn rows_fn(int g, int spr, int rpg, int xc, bool split, bool bf, int pro, int mr) {
+  if (mr > 1)
+    return bf ? gemv_rows_pick_multi_bf16(g, spr, rpg, xc, split, mr) : gemv_rows_pick_multi_f16(g, spr, rpg, xc, split, mr);
   return pro == kProNone ? gemv_rows_pick_plain(g, spr, rpg, xc, split, bf) : gemv_rows_pick_pro(g, spr, rpg, xc, split, pro);
 }
 
@@ -224,8 +226,11 @@ static gemv_rows_fn rows_fn(int g, int spr, int rpg, int xc, bool split, bool bf
 // row waves leave spare waves (up to 16 per workgroup) to produce the activations, each
 // rotating at most four 512-value chunks (measured: for down_proj 12 row waves with 4
 // producers beat 6 row waves of twice the rows with 10); otherwise every wave does both
-// jobs.
-static bool plan_rows(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block, int ncu, bool bf, int pro,
+// jobs.  Several activation rows (mr = 2 .. 4): every wave producing first, all rows'
+// chunks loaded up front (measured, down_proj M = 2 / 3 / 4: 7.8 / 9.1 / 10.4 us against
+// 7.9 / 9.3 / 10.8 with split producer waves and 9.0-9.5 / 11.3 / 13.0 with two rows per
+// group).
+static bool plan_rows(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block, int ncu, bool bf, int pro, int mr,
                       RowsPlan* pl) {
   if (k % 1024 != 0 || k > 14336 || ncu <= 0 || block < 32 || block > 1024) return false;
   if ((k / block) % 8 != 0 || (lda * 2) % 16 != 0) return false;  // absmax rows in whole 16-byte chunks
@@ -239,7 +244,7 @@ static bool plan_rows(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block,
   if (R * ldp >= (int64_t(1) << 31) || R * lda * 2 >= (int64_t(1) << 31)) return false;
   bool found = false;
   for (int pass = 0; pass < 2 && !found; ++pass) {
-    const bool split = pass == 0;
+    const bool split = mr > 1 ? pass == 1 : pass == 0;
     for (int RPG = 1; RPG <= 8 && !found; RPG *= 2) {
       if (SPR * RPG > nsmax) break;
       const int64_t NG = (R + RPG - 1) / RPG;
@@ -258,19 +263,22 @@ static bool plan_rows(int64_t n, int64_t k, int64_t ldp, int64_t lda, int block,
         XC = (nchunk + W - 1) / W;
         if (XC > 1 || R * cpr > 64 * W) continue;
       }
-      if (rows_fn(G, SPR, RPG, XC, split, bf, pro) == nullptr) continue;
+      if (rows_fn(G, SPR, RPG, XC, split, bf, pro, mr) == nullptr) continue;
       pl->G = G; pl->SPR = SPR; pl->RPG = RPG; pl->XC = XC; pl->W = W; pl->WR = (int)WR; pl->split = split;
       found = true;
     }
   }
   if (!found) return false;
-  pl->R = (int)R; pl->nchunk = nchunk; pl->cpr = cpr;
+  pl->R = (int)R; pl->nchunk = nchunk; pl->cpr = cpr; pl->mr = mr;
   pl->grid = (int)((n + R - 1) / R);
+  // each activation row's rotated pairs and block scales in a slot of its own
+  pl->xp_row = align16((uint32_t)(k * 2));
+  pl->xsc_row = align16((uint32_t)(k / 128 * 4));
   uint32_t off = kLutBytes;
   pl->off_xp = off;
-  off = align16(off + (uint32_t)(k * 2));
+  off += (uint32_t)mr * pl->xp_row;
   pl->off_xsc = off;
-  off = align16(off + (uint32_t)(k / 128 * 4));
+  off += (uint32_t)mr * pl->xsc_row;
   pl->off_sc = off;
   off = align16(off + (uint32_t)(R * (k / block) * 4));
   pl->off_ss = off;
@@ -361,19 +369,24 @@ static int rows_lm_launch(const spectra_qweight_t* w, const LmPlan& pl, const vo
   return SPECTRA_OK;
 }
 
-static bool rows_serves(const spectra_qweight_t* w, int m, int act_dtype, int kpro, RowsPlan* pl) {
-  if (m != 1 || w->format != SPECTRA_FMT_NF4 || w->group_size < 32) return false;
+// several rows (m = 2 .. 4): no prologue (each row would need its own norm)
+static bool rows_serves(const spectra_qweight_t* w, int m, int act_dtype, int kpro, const spectra_gemv_fusion_t* fu,
+                        RowsPlan* pl) {
+  if (m < 1 || m > 4 || w->format != SPECTRA_FMT_NF4 || w->group_size < 32) return false;
+  if (m > 1 && kpro != kProNone) return false;
+  if (m > 1 && fu != nullptr && fu->residual != nullptr && (int64_t)(m - 1) * fu->residual_stride + w->n >= (int64_t(1) << 31))
+    return false;  // the residual's byte offsets in 32 bits
   if (w->hadamard_block != 0 && w->hadamard_block != 128) return false;
   if (w->outlier_kind == SPECTRA_OUTLIERS_COLUMNS) return false;
   if (w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz >= (int64_t(1) << 29)) return false;
   if (!ptr_aligned(w->scales, 16)) return false;
   if (kpro != kProNone && act_dtype != SPECTRA_F16) return false;
   return plan_rows(w->n, w->k, w->packed_stride, w->scales_stride, w->group_size, device_cu_count(),
-                   act_dtype == SPECTRA_BF16, kpro, pl);
+                   act_dtype == SPECTRA_BF16, kpro, m, pl);
 }
 
-static int rows_launch(const spectra_qweight_t* w, const RowsPlan& pl, const void* x, int act_dtype, void* out,
-                       hipStream_t stream, const spectra_gemv_fusion_t* fu, int kpro) {
+static int rows_launch(const spectra_qweight_t* w, const RowsPlan& pl, const void* x, int64_t ldx, int act_dtype,
+                       void* out, int64_t ldo, hipStream_t stream, const spectra_gemv_fusion_t* fu, int kpro) {
   RowsParams p;
   p.packed = w->packed; p.ldp = w->packed_stride;
   p.absmax = w->scales; p.lda = w->scales_stride;
@@ -385,6 +398,9 @@ static int rows_launch(const spectra_qweight_t* w, const RowsPlan& pl, const voi
   p.csr_nnz = csr ? (int)w->csr_nnz : 0;
   p.bias = w->bias; p.bias_dt = w->bias_dtype;
   p.x = x; p.out = out;
+  p.ldx = ldx; p.ldo = ldo;
+  p.ldr = fu ? fu->residual_stride : 0;
+  p.xp_row = pl.xp_row; p.xsc_row = pl.xsc_row;
   p.nw = fu ? fu->norm_weight : nullptr;
   p.res = fu ? fu->residual : nullptr;
   p.eps = fu ? fu->eps : 0.0f;
@@ -402,7 +418,7 @@ static int rows_launch(const spectra_qweight_t* w, const RowsPlan& pl, const voi
   p.off_bias = pl.off_bias; p.off_res = pl.off_res;
   p.wr = pl.WR;
   p.W = pl.W;
-  const gemv_rows_fn fn = rows_fn(pl.G, pl.SPR, pl.RPG, pl.XC, pl.split, act_dtype == SPECTRA_BF16, kpro);
+  const gemv_rows_fn fn = rows_fn(pl.G, pl.SPR, pl.RPG, pl.XC, pl.split, act_dtype == SPECTRA_BF16, kpro, pl.mr);
   const int st = ensure_lds_limit((const void*)fn, true);
   if (st != SPECTRA_OK) return st;
   hipLaunchKernelGGL(fn, dim3(pl.grid), dim3(64 * pl.W), pl.lds_bytes, stream, p);
@@ -424,7 +440,7 @@ static bool stream_serves(const spectra_qweight_t* w, int m, StreamPlan* pl) {
 // the descriptor is already validated
 int gemv_plan_grid(const spectra_qweight_t* w, int m) {
   RowsPlan rp;
-  if (rows_serves(w, m, SPECTRA_F16, kProNone, &rp)) return rp.grid;
+  if (rows_serves(w, m, SPECTRA_F16, kProNone, nullptr, &rp)) return rp.grid;
   StreamPlan sp;
   if (stream_serves(w, m, &sp)) return sp.grid;
   const bool csr = w->outlier_kind == SPECTRA_OUTLIERS_CSR && w->csr_nnz > 0;
@@ -457,7 +473,8 @@ int gemv_launch(const spectra_qweight_t* w, const void* x, int64_t ldx, int m, i
   // (the greedy pick rides on the epilogues of the multi-pass row kernel and the multi-row kernel)
   const bool pick = fu != nullptr && fu->argmax_key != nullptr;
   RowsPlan rp;
-  if (!pick && rows_serves(w, m, act_dtype, kpro, &rp)) return rows_launch(w, rp, x, act_dtype, out, stream, fu, kpro);
+  if (!pick && rows_serves(w, m, act_dtype, kpro, fu, &rp))
+    return rows_launch(w, rp, x, ldx, act_dtype, out, ldo, stream, fu, kpro);
   LmPlan lp;
   if (rows_lm_serves(w, m, act_dtype, kpro, fu, &lp)) return rows_lm_launch(w, lp, x, act_dtype, out, stream, fu, kpro);
   StreamPlan sp;

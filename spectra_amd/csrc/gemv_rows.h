@@ -1,8 +1,11 @@
-// One-row decode GEMV for NF4 weights, rows owned by lane groups:
-//   out[0, :] = FWHT_128(x) . W_eff^T (+ CSR outliers, bias, residual), fp32 accumulation.
+// Decode GEMV for NF4 weights, rows owned by lane groups, one to four activation rows:
+//   out[m, :] = FWHT_128(x[m]) . W_eff^T (+ CSR outliers, bias, residual), fp32 accumulation.
 //
 // Replaces the reference's single-row Triton GEMV (kernels.py:16-184) for Format B operands
-// at M = 1 with a Hadamard block of 128 (or none), the decode hot path.  A launch is bound
+// at M = 1 with a Hadamard block of 128 (or none), the decode hot path, and its small-batch
+// path (kernels.py:191-389 at M = 2 .. 4, no prologue or residual): each weight slot is
+// decoded once for the MR rows, and each row's rotated activations get an LDS slot of
+// their own.  A launch is bound
 // by HBM, and what keeps it from the bound is work that cannot overlap the weight stream:
 // the rotated activations must exist before the first dot product, and every cross-wave
 // reduction after the last byte lands is on the critical path.  This design keeps both
@@ -74,10 +77,15 @@ struct RowsParams {
   int wr;              // row waves (waves wr .. W-1 are producers when split)
   int W;               // waves per workgroup (blockDim.x / 64, passed so the kernel reads no implicit argument)
   uint32_t off_xp, off_xsc, off_sc, off_ss, off_bias, off_res;
+  // several activation rows (MR > 1): row m of x at x + m ldx, of out at out + m ldo
+  // (elements); its rotated pairs and block scales at off_xp + m xp_row, off_xsc + m xsc_row
+  // (the residual's rows ldr apart, read by the row waves themselves)
+  int64_t ldx, ldo, ldr;
+  uint32_t xp_row, xsc_row;
 };
 
 constexpr int kRowsSpinLimit = 1 << 20;  // s_sleep rounds a row wave waits for the producers, at most
-// LDS byte offset of the producers' two counters: the unused upper half of the nibble-pair
+// LDS byte offset of the producers' counters (at most 5): the unused upper half of the nibble-pair
 // LUT's first 256-byte row (the 32 copies fill bytes 0..127 of each row), a constant so
 // that zeroing them waits for no kernel argument
 constexpr uint32_t kRowsCounterOff = 128;
@@ -129,20 +137,25 @@ struct ProducerRegs {
   uint4 xr[XC], xu[PRO == kProSiluMul ? XC : 1], nwr[PRO == kProRms ? XC : 1];
 };
 
+// the activation chunks of one row (x: its first element)
 template <int XC, int PRO>
-__device__ __forceinline__ void rows_producer_loads(const RowsParams& p, const RowsCtx& c, int pw, int np, int ptid,
-                                                    ProducerRegs<XC, PRO>& r) {
-  // the activation chunks first: the rotation waits for them, and a wait counts every load
-  // issued before the one it waits for (the block scales below come from HBM, cold)
+__device__ __forceinline__ void rows_producer_xloads(const RowsParams& p, const RowsCtx& c, const void* x, int pw,
+                                                     int np, ProducerRegs<XC, PRO>& r) {
   const uint32_t xlo = 64u * (uint32_t)(c.lane & 15) + 16u * (uint32_t)(c.lane >> 4);
 #pragma unroll
   for (int i = 0; i < XC; ++i) {
     const int ch = pw + np * i;
     const uint32_t o = (ch < p.nchunk ? (uint32_t)ch * 1024u : 0u) + xlo;
-    r.xr[i] = load_at<uint4>(p.x, o);
-    if constexpr (PRO == kProSiluMul) r.xu[i] = load_at<uint4>(p.x, o + 2u * (uint32_t)c.K);
+    r.xr[i] = load_at<uint4>(x, o);
+    if constexpr (PRO == kProSiluMul) r.xu[i] = load_at<uint4>(x, o + 2u * (uint32_t)c.K);
     if constexpr (PRO == kProRms) r.nwr[i] = load_at<uint4>(p.nw, o);
   }
+}
+
+// the workgroup's block scales, bias and residual (producer threads)
+template <int XC, int PRO>
+__device__ __forceinline__ void rows_producer_sloads(const RowsParams& p, const RowsCtx& c, int pw, int ptid,
+                                                     ProducerRegs<XC, PRO>& r) {
   const int srow = (ptid * p.cmagic) >> 16;  // ptid / cpr
   if (pw * 64 < p.R * p.cpr) {
     const int sr = srow < c.Rw ? srow : 0;
@@ -159,13 +172,24 @@ __device__ __forceinline__ void rows_producer_loads(const RowsParams& p, const R
   }
 }
 
+template <int XC, int PRO>
+__device__ __forceinline__ void rows_producer_loads(const RowsParams& p, const RowsCtx& c, int pw, int np, int ptid,
+                                                    ProducerRegs<XC, PRO>& r) {
+  // the activation chunks first: the rotation waits for them, and a wait counts every load
+  // issued before the one it waits for (the block scales below come from HBM, cold)
+  rows_producer_xloads<XC, PRO>(p, c, p.x, pw, np, r);
+  rows_producer_sloads<XC, PRO>(p, c, pw, ptid, r);
+}
+
 // producer work after the LUT: the rotated chunks as fp16 pairs with one power-of-two scale
 // per 128-block, block scales (fp32), bias, residual, RMSNorm partials
+// (activation row m: its pairs and scales into row m's LDS slots; row 0 also stages the block
+// scales, bias, residual and the RMSNorm partials)
 template <int XC, bool BF, int PRO>
 __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& c, uint8_t* smem, int pw, int np,
-                                             int ptid, const ProducerRegs<XC, PRO>& r) {
-  uint32_t* xpd = (uint32_t*)(smem + p.off_xp);  // [pair / 4][run][pair % 4] dwords
-  float* xsc = (float*)(smem + p.off_xsc);       // one scale per 128-block
+                                             int ptid, const ProducerRegs<XC, PRO>& r, int m = 0) {
+  uint32_t* xpd = (uint32_t*)(smem + p.off_xp + (uint32_t)m * p.xp_row);  // [pair / 4][run][pair % 4] dwords
+  float* xsc = (float*)(smem + p.off_xsc + (uint32_t)m * p.xsc_row);       // one scale per 128-block
   const int lane = c.lane, Q = c.Q;
   // B operands: column j of MFMA 1 / 2 is H_32 column (or unit column) pi1(j) / pi2(j),
   // the low / high position of packed pair j (marlin: j, j + 16; plain: 2 j, 2 j + 1)
@@ -266,6 +290,11 @@ __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& 
         const float t0 = d2[t][0] + d2[t][1], t1 = d2[t][0] - d2[t][1], t2 = d2[t][2] + d2[t][3], t3 = d2[t][2] - d2[t][3];
         hi[t][0] = t0 + t2; hi[t][1] = t1 + t3; hi[t][2] = t0 - t2; hi[t][3] = t1 - t3;
       } else {
+        // the MFMA results go straight into the inline asm below, whose reads the compiler's
+        // hazard padding does not cover (a VALU read of an MFMA result needs wait states the
+        // hardware does not insert): 16 wait states, tied to the results so that they sit
+        // between the MFMAs and the asm
+        asm volatile("s_nop 7\n\ts_nop 7" : "+v"(d1[t]), "+v"(d2[t]));
 #pragma unroll
         for (int q = 0; q < 4; ++q) { lo[t][q] = d1[t][q]; hi[t][q] = d2[t][q]; }
       }
@@ -317,6 +346,7 @@ __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& 
       if (jj == 0) xsc[blk] = bsc[t];
     }
   }
+  if (m != 0) return;
   if constexpr (PRO == kProRms) {  // per-producer sums of h^2, fixed order
     ssq = wave_sum(ssq);
     if (lane == 0) ((float*)(smem + p.off_ss))[pw] = ssq;
@@ -395,10 +425,11 @@ struct XRun {
 };
 
 template <int G>
-__device__ __forceinline__ XRun rows_xrun(const RowsParams& p, const RowsCtx& c, const uint8_t* smem, int ch) {
+__device__ __forceinline__ XRun rows_xrun(const RowsParams& p, const RowsCtx& c, const uint8_t* smem, int ch,
+                                          int m = 0) {
   const int Q = c.Q;
-  const uint4* xp4 = (const uint4*)(smem + p.off_xp);
-  const float* xsc = (const float*)(smem + p.off_xsc);
+  const uint4* xp4 = (const uint4*)(smem + p.off_xp + (uint32_t)m * p.xp_row);
+  const float* xsc = (const float*)(smem + p.off_xsc + (uint32_t)m * p.xsc_row);
   XRun r;
   r.q = ch * G + c.li;
 #pragma unroll
@@ -423,11 +454,21 @@ __device__ __forceinline__ float rows_dot(const RowsParams& p, const RowsCtx& c,
   return d * (am * x.xs);
 }
 
+// the same product without the block scale (several activation rows share it)
+__device__ __forceinline__ float rows_dot_raw(const XRun& x, const uint32_t (&dec)[16]) {
+  float d = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 16; ++b)
+    d = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, dec[b]), __builtin_bit_cast(f16x2_t, x.xpair[b]), d, false);
+  return d;
+}
+
 // the row waves' work once the weights are issued: the first NP slots are decoded as they
-// land, before the activations are ready (wait_lut / wait_x: the producers' counters; both
-// no-ops when the caller already synchronised), then the dot products, the outlier
-// products and the row totals
-template <int G, int SPR, int RPG, int NP, bool BF, int PRO, typename WL, typename WX>
+// land, before the activations are ready (wait_lut / wait_x(m): the producers' counters,
+// the LUT and activation row m; both no-ops when the caller already synchronised), then
+// the dot products, the outlier products and the row totals.  Several activation rows with
+// every slot decoded up front: the rows are taken one by one as the producers finish them.
+template <int G, int SPR, int RPG, int NP, bool BF, int PRO, int MR, typename WL, typename WX>
 __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& c, uint8_t* smem, int np,
                                             RowRegs<G, SPR, RPG>& r, WL wait_lut, WX wait_x, const bool* late) {
   constexpr int NS = SPR * RPG;
@@ -435,33 +476,99 @@ __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& 
   const uint32_t* xpd = (const uint32_t*)(smem + p.off_xp);
   const float* xsc = (const float*)(smem + p.off_xsc);
   const uint32_t lanebits = (uint32_t)(lane & 31) << 2;  // this lane's LUT copy: conflict-free reads
-  float acc[RPG];
+  float acc[RPG][MR];
 #pragma unroll
-  for (int j = 0; j < RPG; ++j) acc[j] = 0.0f;
+  for (int j = 0; j < RPG; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[j][m] = 0.0f;
+  // several rows: the residual values of the group's rows, loaded here and used at the
+  // end (issued by every lane of the path, from a valid dummy address without a residual)
+  uint16_t rsv[MR > 1 ? RPG : 1][MR];
+  if constexpr (MR > 1) {
+    const bool hr = p.res != nullptr;
+    const void* rb = hr ? p.res : (const void*)p.absmax;
+#pragma unroll
+    for (int j = 0; j < RPG; ++j)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const int row = min(c.grow0 + j, c.Rw - 1);
+        rsv[j][m] = load_at<uint16_t>(rb, hr ? (uint32_t)(((int64_t)m * p.ldr + c.r0 + row) * 2) : 0u);
+      }
+  }
   uint32_t pre[NP > 0 ? NP : 1][16];
   wait_lut();
 #pragma unroll
   for (int s = 0; s < NP; ++s) rows_decode(r.wq[s], lanebits, pre[s]);
-  wait_x();
+  if constexpr (MR > 1 && NP == NS) {
+    const float* scf = (const float*)(smem + p.off_sc);
+    float am[NS];  // the slots' block scales, shared by the rows
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      wait_x(m);
+      if (m == 0) {  // the block scales are staged with row 0
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const int rowc = min(c.grow0 + s / SPR, c.Rw - 1);
+          am[s] = scf[rowc * (c.K >> p.gshift) + (((s % SPR) * G + li) >> (p.gshift - 5))];
+        }
+      }
+#pragma unroll
+      for (int ch = 0; ch < SPR; ++ch) {
+        const XRun xr = rows_xrun<G>(p, c, smem, ch, m);
+#pragma unroll
+        for (int j = 0; j < RPG; ++j) {
+          const int s = j * SPR + ch;
+          acc[j][m] += rows_dot_raw(xr, pre[s < NP ? s : 0]) * (am[s] * xr.xs);
+        }
+      }
+      // row m's products complete before the wait for row m + 1 (none is deferred past it
+      // with its activations held in registers)
+#pragma unroll
+      for (int j = 0; j < RPG; ++j) asm volatile("" : "+v"(acc[j][m]));
+    }
+  } else {
+#pragma unroll
+  for (int m = 0; m < MR; ++m) wait_x(m);
   // chunk-slot major: each run's activations are read once for the group's RPG rows (slot
   // s = j * SPR + ch); every row still sums its chunk-slots in order
 #pragma unroll
   for (int ch = 0; ch < SPR; ++ch) {
-    const XRun xr = rows_xrun<G>(p, c, smem, ch);
+    if constexpr (MR == 1) {
+      const XRun xr = rows_xrun<G>(p, c, smem, ch);
 #pragma unroll
-    for (int j = 0; j < RPG; ++j) {
-      const int s = j * SPR + ch;
-      if (s < NP) {
-        acc[j] += rows_dot(p, c, smem, xr, j, pre[s < NP ? s : 0]);
-      } else {
+      for (int j = 0; j < RPG; ++j) {
+        const int s = j * SPR + ch;
+        if (s < NP) {
+          acc[j][0] += rows_dot(p, c, smem, xr, j, pre[s < NP ? s : 0]);
+        } else {
+          uint32_t dec[16];
+          rows_decode(r.wq[s], lanebits, dec);
+          acc[j][0] += rows_dot(p, c, smem, xr, j, dec);
+        }
+      }
+    } else {  // several activation rows: each slot decoded once, its block scale read once;
+              // each row's activations read just before its product (registers)
+      const float* scf = (const float*)(smem + p.off_sc);
+      const int q = ch * G + li;
+#pragma unroll
+      for (int j = 0; j < RPG; ++j) {
+        const int s = j * SPR + ch;
         uint32_t dec[16];
         rows_decode(r.wq[s], lanebits, dec);
-        acc[j] += rows_dot(p, c, smem, xr, j, dec);
+        const int rowc = min(c.grow0 + j, c.Rw - 1);
+        const float am = scf[rowc * (c.K >> p.gshift) + (q >> (p.gshift - 5))];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const XRun xr = rows_xrun<G>(p, c, smem, ch, m);
+          acc[j][m] += rows_dot_raw(xr, dec) * (am * xr.xs);
+          asm volatile("" : "+v"(acc[j][m]));  // one row's activations in registers at a time
+        }
       }
     }
   }
+  }
   // outliers: entry value x rotated activation, into the row's lanes
-  if (p.csr) {
+  if (MR == 1 && p.csr) {
     const uint16_t* xp16 = (const uint16_t*)xpd;
 #pragma unroll
     for (int j = 0; j < RPG; ++j) {
@@ -469,11 +576,30 @@ __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& 
       int col = r.ocol[j];
       uint32_t ov = r.oval[j];
       asm volatile("" : "+v"(col), "+v"(ov)::"memory");  // consumed here, after the stream
-      if (li < cnt) acc[j] += h2f((uint16_t)ov) * (h2f(xp16[xs_pos(col, p.marlin, Q)]) * xsc[col >> 7]);
+      if (li < cnt) acc[j][0] += h2f((uint16_t)ov) * (h2f(xp16[xs_pos(col, p.marlin, Q)]) * xsc[col >> 7]);
       // entries beyond one per lane (rare): read from the side tensor
       for (int el = G + li; el < cnt; el += G) {
         const int cl = p.ccol[r.e0r[j] + el];
-        acc[j] += h2f(p.cval[r.e0r[j] + el]) * (h2f(xp16[xs_pos(cl, p.marlin, Q)]) * xsc[cl >> 7]);
+        acc[j][0] += h2f(p.cval[r.e0r[j] + el]) * (h2f(xp16[xs_pos(cl, p.marlin, Q)]) * xsc[cl >> 7]);
+      }
+    }
+  } else if (MR > 1 && p.csr) {
+#pragma unroll
+    for (int j = 0; j < RPG; ++j) {
+      const int cnt = r.cntr[j];
+      int col = r.ocol[j];
+      uint32_t ov = r.oval[j];
+      asm volatile("" : "+v"(col), "+v"(ov)::"memory");  // consumed here, after the stream
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const uint16_t* xp16 = (const uint16_t*)((const uint8_t*)xpd + (uint32_t)m * p.xp_row);
+        const float* xs = (const float*)((const uint8_t*)xsc + (uint32_t)m * p.xsc_row);
+        if (li < cnt) acc[j][m] += h2f((uint16_t)ov) * (h2f(xp16[xs_pos(col, p.marlin, Q)]) * xs[col >> 7]);
+        // entries beyond one per lane (rare): read from the side tensor
+        for (int el = G + li; el < cnt; el += G) {
+          const int cl = p.ccol[r.e0r[j] + el];
+          acc[j][m] += h2f(p.cval[r.e0r[j] + el]) * (h2f(xp16[xs_pos(cl, p.marlin, Q)]) * xs[cl >> 7]);
+        }
       }
     }
   }
@@ -490,25 +616,36 @@ __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& 
   const uint16_t* rsl = (const uint16_t*)(smem + p.off_res);
 #pragma unroll
   for (int j = 0; j < RPG; ++j) {
-    const float v = group_sum<G>(acc[j], lane);
-    const int row = c.grow0 + j;
-    if (li == 0 && row < c.Rw) {
-      float y = v * p.out_scale;
-      if constexpr (PRO == kProRms) y *= inv;
-      if (p.bias != nullptr) y += bl[row];
-      if (p.res != nullptr) y = to_f32_16(from_f32_16(y, odt), odt) + to_f32_16(rsl[row], odt);
-      if (late != nullptr && *late) y = __builtin_nanf("");
-      ((uint16_t*)p.out)[c.r0 + row] = from_f32_16(y, odt);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float v = group_sum<G>(acc[j][m], lane);
+      const int row = c.grow0 + j;
+      if (li == 0 && row < c.Rw) {
+        float y = v * p.out_scale;
+        if constexpr (PRO == kProRms) y *= inv;
+        if (p.bias != nullptr) y += bl[row];
+        if (p.res != nullptr)
+          y = to_f32_16(from_f32_16(y, odt), odt) + to_f32_16(MR == 1 ? rsl[row] : rsv[j][m], odt);
+        if (late != nullptr && *late) y = __builtin_nanf("");
+        if constexpr (MR == 1) ((uint16_t*)p.out)[c.r0 + row] = from_f32_16(y, odt);
+        else ((uint16_t*)p.out)[(int64_t)m * p.ldo + c.r0 + row] = from_f32_16(y, odt);
+      }
     }
   }
 }
 
-template <int G, int SPR, int RPG, int XC, bool BF, int PRO, bool SPLIT>
+// MR > 1: MR activation rows (x rows ldx apart, out rows ldo apart), no prologue; the
+// producers rotate the rows one after another (the next row's chunks loading while a row
+// rotates), and the row waves decode each slot once for the MR dot products
+template <int G, int SPR, int RPG, int XC, bool BF, int PRO, bool SPLIT, int MR = 1>
 __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) {
+  static_assert(MR == 1 || PRO == kProNone, "several activation rows: no prologue");
   extern __shared__ __align__(16) uint8_t smem[];
   constexpr int RW = RPG * (64 / G);  // rows per wave
   constexpr int NS = SPR * RPG;
-  constexpr int NP = NS <= 4 ? NS : NS <= 8 ? 2 : 0;  // slots decoded before the activations are ready
+  // slots decoded before the activations are ready (one row: the registers allow it)
+  // (several rows: all of them or none, the rows then taken one by one or together)
+  constexpr int NP = NS <= 4 ? NS : MR > 1 ? 0 : NS <= 8 ? 2 : 0;
   const int tid = threadIdx.x;
   const int W = p.W;  // == blockDim.x / 64; blockDim would pull in the 256-byte implicit-argument block
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -530,7 +667,8 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
   // every argument the issue phase needs, fetched in one round trip before the first load
   asm volatile("" ::"s"(p.x), "s"(p.packed), "s"(p.ldp), "s"(p.absmax), "s"(p.lda), "s"(p.csr), "s"(p.rowptr),
                "s"(p.bias), "s"(p.res), "s"(p.bias_dt), "s"(p.nchunk), "s"(p.cpr), "s"(p.cmagic), "s"(p.wr), "s"(p.W));
-  // [0]: LUT rows built, [1]: producers done
+  // [0]: LUT rows built, [1 + m]: activation row m rotated (the block scales, bias and
+  // residual staged with row 0)
   uint32_t* counter = (uint32_t*)(smem + kRowsCounterOff);
   const int rwave = SPLIT ? wave - np : wave;  // row-wave index
 
@@ -538,11 +676,13 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
     if (wave < np) {
       // ---------------- producer waves ----------------
       if (tid == 0) {
-        counter[0] = 0u;
-        counter[1] = 0u;
+#pragma unroll
+        for (int i = 0; i <= MR; ++i) counter[i] = 0u;
       }
-      ProducerRegs<XC, PRO> pr;
-      rows_producer_loads<XC, PRO>(p, c, wave, np, tid, pr);
+      // several rows: two register sets, the next row's activations loading while a row rotates
+      ProducerRegs<XC, PRO> pr[MR == 1 ? 1 : 2];
+      rows_producer_xloads<XC, PRO>(p, c, p.x, wave, np, pr[0]);
+      rows_producer_sloads<XC, PRO>(p, c, wave, tid, pr[0]);
       // --- start barrier: counters zeroed (this wave waits for its LDS writes); the
       //     activation requests precede the weight runs
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -550,9 +690,15 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
       build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, np, c.lane);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // LDS operations of a wave complete in order
       if (c.lane == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      rows_rotate<XC, BF, PRO>(p, c, smem, wave, np, tid, pr);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (c.lane == 0) __hip_atomic_fetch_add(counter + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        if (m + 1 < MR)
+          rows_producer_xloads<XC, PRO>(p, c, (const uint16_t*)p.x + (int64_t)(m + 1) * p.ldx, wave, np,
+                                        pr[(m + 1) & 1]);
+        rows_rotate<XC, BF, PRO>(p, c, smem, wave, np, tid, pr[m & 1], m);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (c.lane == 0) __hip_atomic_fetch_add(counter + 1 + m, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
       return;
     }
     // ---------------- row waves ----------------
@@ -583,7 +729,8 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
       late = late || it == kRowsSpinLimit;
       asm volatile("" ::: "memory");
     };
-    rows_stream<G, SPR, RPG, NP, BF, PRO>(p, c, smem, np, rr, [&] { wait_for(0); }, [&] { wait_for(1); }, &late);
+    rows_stream<G, SPR, RPG, NP, BF, PRO, MR>(p, c, smem, np, rr, [&] { wait_for(0); }, [&](int m) { wait_for(1 + m); },
+                                              &late);
   } else {
     // every wave loads and produces, then streams its rows
     int sx[RW + 1];
@@ -595,12 +742,24 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
 #pragma unroll
       for (int j = 0; j <= RW; ++j) sx[j] = 0;
     }
-    ProducerRegs<XC, PRO> pr;
-    rows_producer_loads<XC, PRO>(p, c, wave, W, tid, pr);
+    // several rows, one chunk per wave: every row's chunk loaded up front; more chunks: two
+    // register sets, the next row's chunks loading while a row rotates
+    constexpr bool kAll = MR == 1 || XC == 1;
+    ProducerRegs<XC, PRO> pr[kAll ? MR : 2];
+#pragma unroll
+    for (int m = 0; m < (kAll ? MR : 1); ++m)
+      rows_producer_xloads<XC, PRO>(p, c, (const uint16_t*)p.x + (int64_t)m * p.ldx, wave, W, pr[m]);
+    rows_producer_sloads<XC, PRO>(p, c, wave, tid, pr[0]);
     RowRegs<G, SPR, RPG> rr;
     rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
     build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, W, c.lane);
-    rows_rotate<XC, BF, PRO>(p, c, smem, wave, W, tid, pr);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      if (!kAll && m + 1 < MR)
+        rows_producer_xloads<XC, PRO>(p, c, (const uint16_t*)p.x + (int64_t)(m + 1) * p.ldx, wave, W,
+                                      pr[(m + 1) & 1]);
+      rows_rotate<XC, BF, PRO>(p, c, smem, wave, W, tid, pr[kAll ? m : m & 1], m);
+    }
     // --- LUT, activation pairs, scales: this wave's LDS writes complete, then the barrier.
     //     (__syncthreads would also wait for every outstanding global load, the weight
     //     runs included, and so hold the decode back until the whole stream has landed.)
@@ -609,7 +768,7 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
       __builtin_amdgcn_s_waitcnt(0);  // its dummy loads land before it ends
       return;
     }
-    rows_stream<G, SPR, RPG, 0, BF, PRO>(p, c, smem, W, rr, [] {}, [] {}, nullptr);
+    rows_stream<G, SPR, RPG, 0, BF, PRO, MR>(p, c, smem, W, rr, [] {}, [](int) {}, nullptr);
   }
 }
 

@@ -26,5 +26,8 @@ gemv_rows_fn rows_pick_combo(int g, int spr, int rpg, int xc, bool split) {
 
 gemv_rows_fn gemv_rows_pick_plain(int g, int spr, int rpg, int xc, bool split, bool bf);
 gemv_rows_fn gemv_rows_pick_pro(int g, int spr, int rpg, int xc, bool split, int pro);
+// 2 .. 4 activation rows, no prologue (nullptr where the combination is not built for mr rows)
+gemv_rows_fn gemv_rows_pick_multi_f16(int g, int spr, int rpg, int xc, bool split, int mr);
+gemv_rows_fn gemv_rows_pick_multi_bf16(int g, int spr, int rpg, int xc, bool split, int mr);
 
 }  // namespace spectra

@@ -788,15 +788,58 @@ def test_prefill_gemm_against_torch_fp32(hip, m, k, n):
     check_y(y, y_t, torch.bfloat16)
 
 
+@pytest.mark.parametrize("act", ["float16", "bfloat16"])
+@pytest.mark.parametrize("n,k,m,had,marlin,bias", [
+    (3072, 8192, 2, 128, True, False),    # cfg3 down_proj, one row per lane group
+    (3072, 8192, 4, 128, True, True),
+    (8448, 3072, 3, 128, True, False),    # K = 3072 past 32 rows per workgroup (cfg3 gate_up's
+    (8448, 3072, 4, 0, False, True),      # plan): two rows per 32-lane group
+    (4096, 4096, 3, 128, False, True),    # K = 4096
+    (301, 8192, 4, 128, True, False),     # ragged: two rows per workgroup, the last one short
+])
+def test_rows_gemv_several_rows(hip, act, n, k, m, had, marlin, bias):
+    """The row-owning GEMV with 2-4 activation rows (one weight read, each slot decoded once
+    for the rows): bit-identical to one single-row call per row (the same per-row arithmetic)
+    and within the dtype's bar of the oracle's float64 product, x rows ldx apart and output
+    rows ldo apart (both padded)."""
+    case(act=act, n=n, k=k, m=m, had=had, marlin=marlin, bias=bias)
+    q, rng = _format_b(n * 7 + k + m + had, n, k, had, marlin=marlin)
+    rd = act if act == "float16" else "float32"
+    w_eff = O.nf4_dequant(q["packed"], q["absmax"], marlin, rd, q["rowptr"], q["col"], q["val"])
+    x = O.round_to(rand_np(rng, (m, k), 1.0, np.float32), act)
+    b = rand_np(rng, (n,), 0.1) if bias else None
+    y_ref = O.linear_ref(x, act, w_eff, rd, hadamard_block=had, bias=b)
+    ops = K.QWeightOperands(cuda(q["packed"]), cuda(q["absmax"]), None, k, codebook="nf4", group_size=64,
+                            hadamard_block=had, marlin_layout=marlin, bias=cuda(b) if bias else None,
+                            outlier_idx=cuda(q["col"]), outlier_w=cuda(q["val"]), outlier_rowptr=cuda(q["rowptr"]))
+    lib = L.load()
+    dt, code = TDT[act], (L.F16 if act == "float16" else L.BF16)
+    xp = torch.zeros(m, k + 64, dtype=dt, device="cuda")
+    xp[:, :k] = cuda(x, dt)
+    stream = torch.cuda.current_stream().cuda_stream
+    y = torch.full((m, n + 5), float("nan"), dtype=dt, device="cuda")
+    L.check("spectra_w4a16_gemv", lib.spectra_w4a16_gemv(ops.ptr(), xp.data_ptr(), xp.stride(0), m, code,
+                                                          y.data_ptr(), y.stride(0), stream))
+    ys = torch.full((m, n), float("nan"), dtype=dt, device="cuda")
+    for i in range(m):
+        L.check("spectra_w4a16_gemv", lib.spectra_w4a16_gemv(ops.ptr(), xp[i].data_ptr(), xp.stride(0), 1, code,
+                                                              ys[i].data_ptr(), n, stream))
+    torch.cuda.synchronize()
+    assert torch.isnan(y[:, n:]).all(), "a store past the row"
+    assert torch.equal(y[:, :n], ys), "several-row output differs from single-row calls"
+    check_y(y[:, :n], y_ref, dt)
+
+
 @pytest.mark.parametrize("m", [2, 4])
 def test_linear_dispatch_with_and_without_workspace(hip, m):
-    """spectra_w4a16_linear on a wide layer (N=16384, K=3072: the 2-4-row GEMV plan needs more
-    than one workgroup per CU): with the workspace the rows go to the small-batch family,
-    with none (or one too small) they stay on the GEMV; both against the fp32 reference."""
+    """spectra_w4a16_linear on a wide layer the row-owning GEMV does not plan (N=16384,
+    K=5120: K / 1024 odd and not 3; the older multi-row GEMV plan needs more than one
+    workgroup per CU): with the workspace the rows go to the small-batch family, with none
+    (or one too small) they stay on the GEMV; both against the fp32 reference."""
     import ctypes
     from spectra_amd import _lib as L
     case(m=m)
-    n, k = 16384, 3072
+    n, k = 16384, 5120
     g = torch.Generator().manual_seed(m)
     w = (torch.randn(n, k, generator=g) * 0.02).half()
     nnz = int(round(0.005 * n * k))
