@@ -292,7 +292,9 @@ def main():
     ap.add_argument("--profile-gemm-handwritten", action="store_true",
                     help="as --profile-gemm, on the hand-written MFMA GEMM instead of the library path")
     ap.add_argument("--profile-small-batch", action="store_true",
-                    help="only run cfg3's M=16 small-batch calls (down_proj, gate_up) a few times (rocprofv3 runs)")
+                    help="only run cfg3's small-batch calls (down_proj, gate_up) a few times (rocprofv3 runs)")
+    ap.add_argument("--small-batch-m", type=int, default=16, choices=(2, 3, 4, 8, 16),
+                    help="rows per call for --profile-small-batch (2-4: the row-owning GEMV; 8, 16: the MFMA family)")
     ap.add_argument("--decode-e2e", action="store_true",
                     help="only run the cfg5 end-to-end decode (for rocprofv3 runs); prints its JSON fields")
     args = ap.parse_args()
@@ -317,7 +319,7 @@ def main():
         print(json.dumps(profile_gemm(lib, dev, "dispatch" if args.profile_gemm else "handwritten")), flush=True)
         return
     if args.profile_small_batch:
-        print(json.dumps(profile_small_batch(L.load(), dev, args.pool_gb)), flush=True)
+        print(json.dumps(profile_small_batch(L.load(), dev, args.pool_gb, m=args.small_batch_m)), flush=True)
         return
 
     # ---- cfg2 operands
@@ -686,8 +688,9 @@ def profile_gemm(lib, dev, family: str = "dispatch", iters: int = 3) -> dict:
 
 
 def profile_small_batch(lib, dev, pool_gb: float, m: int = 16, reps: int = 3) -> dict:
-    """cfg3 at M=16: down_proj (K=8192, N=3072) and gate_up (K=3072, N=16384) through the
-    module dispatch over a rotated weight pool, each graph replayed ``reps`` times."""
+    """cfg3 at M rows (16 by default): down_proj (K=8192, N=3072) and gate_up (K=3072,
+    N=16384) through the module dispatch over a rotated weight pool, each graph replayed
+    ``reps`` times."""
     out = {}
     for name, nn, kk, seed in (("down", 3072, 8192, 31), ("gate_up", 16384, 3072, 30)):
         q = synth_nf4(nn, kk, seed=seed)
