@@ -883,25 +883,28 @@ def test_determinism_and_graph_replay(hip):
     lin.set_weights(*args, outlier_idx=kw["outlier_idx"], outlier_weight=kw["outlier_w"], marlin_layout=True,
                     outlier_rowptr=kw["outlier_rowptr"])
     x1 = cuda(rand_np(rng, (1, 4096), 1.0))
+    x3 = cuda(rand_np(rng, (3, 4096), 1.0))  # the row-owning GEMV with three activation rows
     x8 = cuda(rand_np(rng, (8, 4096), 1.0))
-    e1, e8 = lin(x1), lin(x8)
-    assert torch.equal(lin(x1), e1) and torch.equal(lin(x8), e8)  # bitwise deterministic
+    e1, e3, e8 = lin(x1), lin(x3), lin(x8)
+    assert torch.equal(lin(x1), e1) and torch.equal(lin(x3), e3) and torch.equal(lin(x8), e8)  # bitwise deterministic
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for _ in range(2):
-            lin(x1), lin(x8)
+            lin(x1), lin(x3), lin(x8)
     torch.cuda.current_stream().wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         g1 = lin(x1)
+        g3 = lin(x3)
         g8 = lin(x8)
     for _ in range(3):
         g1.zero_()
+        g3.zero_()
         g8.zero_()
         graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(g1, e1) and torch.equal(g8, e8)
+        assert torch.equal(g1, e1) and torch.equal(g3, e3) and torch.equal(g8, e8)
         _ = lin(x1)  # eager work between replays
         torch.cuda.synchronize()
 
