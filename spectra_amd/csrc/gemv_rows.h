@@ -185,9 +185,12 @@ __device__ __forceinline__ void rows_producer_loads(const RowsParams& p, const R
 // per 128-block, block scales (fp32), bias, residual, RMSNorm partials
 // (activation row m: its pairs and scales into row m's LDS slots; row 0 also stages the block
 // scales, bias, residual and the RMSNorm partials)
-template <int XC, bool BF, int PRO>
+// RM (several rows, one chunk per wave): chain t is activation row t of chunk pw (its
+// pairs and scales into row t's slots), the chains interleaved as the chunks are
+template <int XC, bool BF, int PRO, bool RM = false>
 __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& c, uint8_t* smem, int pw, int np,
                                              int ptid, const ProducerRegs<XC, PRO>& r, int m = 0) {
+  static_assert(!RM || PRO == kProNone, "rows mode: no prologue");
   uint32_t* xpd = (uint32_t*)(smem + p.off_xp + (uint32_t)m * p.xp_row);  // [pair / 4][run][pair % 4] dwords
   float* xsc = (float*)(smem + p.off_xsc + (uint32_t)m * p.xsc_row);       // one scale per 128-block
   const int lane = c.lane, Q = c.Q;
@@ -338,12 +341,14 @@ __device__ __forceinline__ void rows_rotate(const RowsParams& p, const RowsCtx& 
 
 #pragma unroll
   for (int t = 0; t < XC; ++t) {
-    const int ch = pw + np * t;
+    const int ch = RM ? pw : pw + np * t;
+    uint32_t* xpt = RM ? xpd + t * (p.xp_row >> 2) : xpd;
+    float* xst = RM ? xsc + t * (p.xsc_row >> 2) : xsc;
     if (ch < p.nchunk) {  // wave-uniform
       const int blk = 4 * ch + g;  // global 128-block
 #pragma unroll
-      for (int q = 0; q < 4; ++q) xpd[((jj >> 2) * Q + 4 * blk + q) * 4 + (jj & 3)] = packed[t][q];
-      if (jj == 0) xsc[blk] = bsc[t];
+      for (int q = 0; q < 4; ++q) xpt[((jj >> 2) * Q + 4 * blk + q) * 4 + (jj & 3)] = packed[t][q];
+      if (jj == 0) xst[blk] = bsc[t];
     }
   }
   if (m != 0) return;
@@ -742,8 +747,31 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
 #pragma unroll
       for (int j = 0; j <= RW; ++j) sx[j] = 0;
     }
-    // several rows, one chunk per wave: every row's chunk loaded up front; more chunks: two
-    // register sets, the next row's chunks loading while a row rotates
+    // several rows, one chunk per wave: every row's chunk loaded up front and the rows
+    // rotated as interleaved chains; more chunks: two register sets, the next row's chunks
+    // loading while a row rotates
+    constexpr bool kChains = MR > 1 && XC == 1;
+    if constexpr (kChains) {
+      ProducerRegs<MR, PRO> pm;
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const uint32_t o = (wave < p.nchunk ? (uint32_t)wave * 1024u : 0u) + 64u * (uint32_t)(c.lane & 15) +
+                           16u * (uint32_t)(c.lane >> 4);
+        pm.xr[m] = load_at<uint4>((const uint16_t*)p.x + (int64_t)m * p.ldx, o);
+      }
+      rows_producer_sloads<MR, PRO>(p, c, wave, tid, pm);
+      RowRegs<G, SPR, RPG> rr;
+      rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
+      build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, W, c.lane);
+      rows_rotate<MR, BF, PRO, true>(p, c, smem, wave, W, tid, pm, 0);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if (wave * RW >= c.Rw) {
+        __builtin_amdgcn_s_waitcnt(0);
+        return;
+      }
+      rows_stream<G, SPR, RPG, 0, BF, PRO, MR>(p, c, smem, W, rr, [] {}, [](int) {}, nullptr);
+      return;
+    }
     constexpr bool kAll = MR == 1 || XC == 1;
     ProducerRegs<XC, PRO> pr[kAll ? MR : 2];
 #pragma unroll
