@@ -3,7 +3,7 @@
 //
 // Replaces the reference's single-row Triton GEMV (kernels.py:16-184) for Format B operands
 // at M = 1 with a Hadamard block of 128 (or none), the decode hot path, and its small-batch
-// path (kernels.py:191-389 at M = 2 .. 4, no prologue or residual): each weight slot is
+// path (kernels.py:191-389 at M = 2 .. 4, no prologue): each weight slot is
 // decoded once for the MR rows, and each row's rotated activations get an LDS slot of
 // their own.  A launch is bound
 // by HBM, and what keeps it from the bound is work that cannot overlap the weight stream:
@@ -639,9 +639,11 @@ __device__ __forceinline__ void rows_stream(const RowsParams& p, const RowsCtx& 
   }
 }
 
-// MR > 1: MR activation rows (x rows ldx apart, out rows ldo apart), no prologue; the
-// producers rotate the rows one after another (the next row's chunks loading while a row
-// rotates), and the row waves decode each slot once for the MR dot products
+// MR > 1: MR activation rows (x rows ldx apart, out rows ldo apart), no prologue; the row
+// waves decode each slot once for the MR dot products.  Without producer waves (the form
+// the plan picks) every wave rotates its chunk of all rows as interleaved chains; with
+// them (SPLIT, not instantiated for several rows) the producers rotate the rows one after
+// another, the next row's chunks loading while a row rotates, and count each row
 template <int G, int SPR, int RPG, int XC, bool BF, int PRO, bool SPLIT, int MR = 1>
 __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) {
   static_assert(MR == 1 || PRO == kProNone, "several activation rows: no prologue");
@@ -747,46 +749,26 @@ __global__ void __launch_bounds__(1024, 1) gemv_rows_kernel(const RowsParams p) 
 #pragma unroll
       for (int j = 0; j <= RW; ++j) sx[j] = 0;
     }
-    // several rows, one chunk per wave: every row's chunk loaded up front and the rows
-    // rotated as interleaved chains; more chunks: two register sets, the next row's chunks
-    // loading while a row rotates
-    constexpr bool kChains = MR > 1 && XC == 1;
-    if constexpr (kChains) {
+    RowRegs<G, SPR, RPG> rr;
+    if constexpr (MR > 1) {
+      // several rows (one chunk per wave: the plan gives every wave at most one): each
+      // wave's chunk of every row loaded up front, the rows rotated as interleaved chains
+      static_assert(MR == 1 || XC == 1, "several rows without producer waves: one chunk per wave");
       ProducerRegs<MR, PRO> pm;
+      const uint32_t o = (wave < p.nchunk ? (uint32_t)wave * 1024u : 0u) + 64u * (uint32_t)(c.lane & 15) +
+                         16u * (uint32_t)(c.lane >> 4);
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const uint32_t o = (wave < p.nchunk ? (uint32_t)wave * 1024u : 0u) + 64u * (uint32_t)(c.lane & 15) +
-                           16u * (uint32_t)(c.lane >> 4);
-        pm.xr[m] = load_at<uint4>((const uint16_t*)p.x + (int64_t)m * p.ldx, o);
-      }
+      for (int m = 0; m < MR; ++m) pm.xr[m] = load_at<uint4>((const uint16_t*)p.x + (int64_t)m * p.ldx, o);
       rows_producer_sloads<MR, PRO>(p, c, wave, tid, pm);
-      RowRegs<G, SPR, RPG> rr;
       rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
       build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, W, c.lane);
       rows_rotate<MR, BF, PRO, true>(p, c, smem, wave, W, tid, pm, 0);
-      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if (wave * RW >= c.Rw) {
-        __builtin_amdgcn_s_waitcnt(0);
-        return;
-      }
-      rows_stream<G, SPR, RPG, 0, BF, PRO, MR>(p, c, smem, W, rr, [] {}, [](int) {}, nullptr);
-      return;
-    }
-    constexpr bool kAll = MR == 1 || XC == 1;
-    ProducerRegs<XC, PRO> pr[kAll ? MR : 2];
-#pragma unroll
-    for (int m = 0; m < (kAll ? MR : 1); ++m)
-      rows_producer_xloads<XC, PRO>(p, c, (const uint16_t*)p.x + (int64_t)m * p.ldx, wave, W, pr[m]);
-    rows_producer_sloads<XC, PRO>(p, c, wave, tid, pr[0]);
-    RowRegs<G, SPR, RPG> rr;
-    rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
-    build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, W, c.lane);
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      if (!kAll && m + 1 < MR)
-        rows_producer_xloads<XC, PRO>(p, c, (const uint16_t*)p.x + (int64_t)(m + 1) * p.ldx, wave, W,
-                                      pr[(m + 1) & 1]);
-      rows_rotate<XC, BF, PRO>(p, c, smem, wave, W, tid, pr[kAll ? m : m & 1], m);
+    } else {
+      ProducerRegs<XC, PRO> pr;
+      rows_producer_loads<XC, PRO>(p, c, wave, W, tid, pr);
+      rows_row_loads<G, SPR, RPG>(p, c, sx, rr);
+      build_pair_lut32<SPECTRA_FMT_NF4>(smem, wave, W, c.lane);
+      rows_rotate<XC, BF, PRO>(p, c, smem, wave, W, tid, pr);
     }
     // --- LUT, activation pairs, scales: this wave's LDS writes complete, then the barrier.
     //     (__syncthreads would also wait for every outstanding global load, the weight
