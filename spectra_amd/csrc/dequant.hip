@@ -255,9 +255,12 @@ __global__ void __launch_bounds__(kDqThreads) dequant_rows_kernel(spectra_qweigh
 }
 
 // Embedding gather (engine.py:127-212, SpectraFusedEmbedding.forward): row ids[b] of
-// W_eff, bit-identical to the same row of spectra_w4_dequant.  One workgroup per id: the
-// dense values first, then (after the barrier) the row's outlier columns / CSR entries.
-// Ids outside [0, N) produce a row of zeros.
+// W_eff, bit-identical to the same row of spectra_w4_dequant.  One workgroup per id.  The
+// row's loads are requested before its first store (a wait for a load also waits for every
+// store issued before it, so a load behind a store costs a round trip of its own): the
+// packed bytes (8 per thread), their scales and zero points, the CSR extent and each
+// thread's first CSR entry; then the dense values; then, after the barrier, the outlier
+// columns / CSR entries over them.  Ids outside [0, N) produce a row of zeros.
 __global__ void __launch_bounds__(kDqThreads) embed_kernel(spectra_qweight_t w, const int64_t* __restrict__ ids,
                                                             void* __restrict__ out, int64_t ldo, int out_dt) {
   const int64_t b = blockIdx.x;
@@ -265,29 +268,69 @@ __global__ void __launch_bounds__(kDqThreads) embed_kernel(spectra_qweight_t w, 
   const bool ok = id >= 0 && id < w.n;
   const int64_t row = ok ? id : 0;
   const int64_t kb = w.k / 2;
-  for (int64_t j = threadIdx.x; j < kb; j += blockDim.x) {
-    const uint8_t byte = w.packed[row * w.packed_stride + j];
-    for (int half = 0; half < 2; ++half) {
-      const int q = half ? (byte >> 4) : (byte & 15);
-      const int64_t kk = nibble_k(j, half, w.marlin_layout);
-      float v;
-      if (w.format == SPECTRA_FMT_ASYM_G32) {
-        const int64_t g = kk / 32;
-        v = ((float)q - (float)w.zeros[row * w.zeros_stride + g]) * h2f(w.scales[row * w.scales_stride + g]);
-      } else {
-        v = nf4_code_f32(q) * h2f(w.scales[row * w.scales_stride + kk / w.group_size]);
+  const int tid = threadIdx.x;
+  const bool asym = w.format == SPECTRA_FMT_ASYM_G32;
+  const bool csr = ok && w.outlier_kind == SPECTRA_OUTLIERS_CSR;
+  int eb = 0, ee = 0;
+  if (csr) {
+    eb = w.csr_rowptr[row];
+    ee = w.csr_rowptr[row + 1];
+  }
+  const bool has_e = csr && eb + tid < ee;
+  int ecol = 0;
+  uint16_t eval = 0;
+  if (has_e) {
+    ecol = w.csr_col[eb + tid];
+    eval = w.csr_val[eb + tid];
+  }
+  const uint8_t* prow = w.packed + row * w.packed_stride;
+  const uint16_t* srow = w.scales + row * w.scales_stride;
+  const uint8_t* zrow = asym ? w.zeros + row * w.zeros_stride : nullptr;
+  const int gsh = __builtin_ctz((unsigned)w.group_size);  // the group size is a power of two (validated)
+  const int k32 = (int)w.k;
+  const bool vec = (reinterpret_cast<uintptr_t>(prow) & 7) == 0;
+  for (int64_t j0 = (int64_t)tid * 8; j0 < kb; j0 += (int64_t)blockDim.x * 8) {
+    uint32_t d[2];
+    if (vec && j0 + 8 <= kb) {
+      const uint2 v = *(const uint2*)(prow + j0);
+      d[0] = v.x;
+      d[1] = v.y;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        d[u] = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (j0 + 4 * u + i < kb) d[u] |= (uint32_t)prow[j0 + 4 * u + i] << (8 * i);
       }
-      store_elem(out, b * ldo + kk, out_dt, ok ? v : 0.0f);
+    }
+    float sc[16], zp[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int kk = (int)nibble_k(j0 + (e >> 1), e & 1, w.marlin_layout);
+      const int g = (kk < k32 ? kk : 0) >> gsh;
+      sc[e] = h2f(srow[g]);
+      zp[e] = asym ? (float)zrow[g] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      if (j0 + (e >> 1) < kb) {
+        const int q = (int)((d[e >> 3] >> (4 * (e & 7))) & 15u);  // byte e / 2, nibble e & 1
+        const int64_t kk = nibble_k(j0 + (e >> 1), e & 1, w.marlin_layout);
+        const float v = asym ? ((float)q - zp[e]) * sc[e] : nf4_code_f32(q) * sc[e];
+        store_elem(out, b * ldo + kk, out_dt, ok ? v : 0.0f);
+      }
     }
   }
   __syncthreads();
   if (!ok) return;
   if (w.outlier_kind == SPECTRA_OUTLIERS_COLUMNS) {
-    for (int j = threadIdx.x; j < w.num_outliers; j += blockDim.x)
+    for (int j = tid; j < w.num_outliers; j += blockDim.x)
       store_elem(out, b * ldo + w.outlier_idx[j], out_dt,
                  load_elem(w.outlier_w, row * w.outlier_w_stride + j, w.outlier_w_dtype));
-  } else if (w.outlier_kind == SPECTRA_OUTLIERS_CSR) {
-    for (int e = w.csr_rowptr[row] + threadIdx.x; e < w.csr_rowptr[row + 1]; e += blockDim.x)
+  } else if (csr) {
+    if (has_e) store_elem(out, b * ldo + ecol, out_dt, h2f(eval));
+    for (int e = eb + tid + (int)blockDim.x; e < ee; e += blockDim.x)
       store_elem(out, b * ldo + w.csr_col[e], out_dt, h2f(w.csr_val[e]));
   }
 }
