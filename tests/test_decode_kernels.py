@@ -311,6 +311,27 @@ def test_gemv_residual_without_prologue(hip):
     assert torch.equal(r, res + y)
 
 
+def test_gemv_residual_several_rows_strided(hip):
+    """Four rows on the row-owning kernel (down_proj's shape) with a residual whose rows are
+    N + 40 apart (a padded view): out of place, then in place (out = the residual view, so
+    the output rows are N + 40 apart too); both bit-identical to the separate add of the
+    plain call."""
+    n, k, m = 3072, 8192, 4
+    case(n=n, k=k, had=128, m=m)
+    ops, _ = _nf4_ops(n, k, 128, seed=21)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(m, k, device="cuda", generator=g).half()
+    y = K.w4a16_gemv_fused(ops, x)  # plain
+    wide = (torch.randn(m, n + 40, device="cuda", generator=g) * 4).half()
+    res = wide[:, 8:8 + n]
+    sep = res + y
+    pads = (wide[:, :8].clone(), wide[:, 8 + n:].clone())
+    assert torch.equal(K.w4a16_gemv_fused(ops, x, residual=res), sep)
+    out = K.w4a16_gemv_fused(ops, x, residual=res, out=res)
+    assert out.data_ptr() == res.data_ptr() and torch.equal(res, sep)
+    assert torch.equal(wide[:, :8], pads[0]) and torch.equal(wide[:, 8 + n:], pads[1]), "a store outside the rows"
+
+
 @pytest.mark.parametrize("n,k,had,pro", [(128256, 3072, 0, "rmsnorm"),  # the decoder's lm_head
                                           (1000, 1024, 128, "none"), (257, 2048, 0, "rmsnorm")])
 def test_gemv_fused_greedy_pick(hip, n, k, had, pro):
